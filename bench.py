@@ -1,0 +1,331 @@
+#!/usr/bin/env python3
+"""Benchmark of the gfx950 packed-weight matmul path on one MI355X.
+
+Headline: Q4_K decode GEMV x[1, 4096] . W[14336, 4096]^T (Llama-3-8B FFN up
+projection), weight GB/s over quantized-weight bytes. A step is one call
+of the matmul entry point (int8 activation quantization + GEMV) on inputs
+already resident in HBM; the weight rotates through `--copies` distinct
+device copies (> 256 MB in all) so the MALL cannot serve it. Steps are
+launched from HIP graphs (captured once) so host launch cost does not hide
+the device time.
+
+Also reported: the GEMV kernel alone against the 8 TB/s HBM roofline, the
+M=512 prefill GEMM (x[512, 4096] . W[14336, 4096]^T) in TFLOP/s against the
+2.5 PFLOP/s dense f16 MFMA peak, and the reference's CPU path (the
+oracle's AVX2 restatement) timed on this host's cores.
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "magnetar-provider-cpu_amd"))
+sys.path.insert(0, ROOT)
+
+METRIC = "Q4_K GEMV weight GB/s (% HBM peak) + M=512 GEMM TFLOP/s, 4096x14336"
+HBM_PEAK_GBS = 8000.0
+F16_MFMA_PEAK_TFLOPS = 2500.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+class GraphRunner:
+    """Captures `per_graph` calls of fn(i) into one HIP graph on a private
+    stream, then replays it; falls back to eager launches if capture fails."""
+
+    def __init__(self, torch, fn, per_graph, use_graph=True):
+        self.torch = torch
+        self.fn = fn
+        self.per_graph = per_graph
+        self.stream = torch.cuda.Stream()
+        self.graph = None
+        torch.cuda.synchronize()
+        with torch.cuda.stream(self.stream):
+            for i in range(per_graph):
+                fn(i, self.stream.cuda_stream)
+        self.stream.synchronize()
+        if use_graph:
+            try:
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g, stream=self.stream):
+                    for i in range(per_graph):
+                        fn(i, self.stream.cuda_stream)
+                self.graph = g
+            except Exception as e:  # noqa: BLE001
+                log(f"graph capture failed ({e}); timing eager launches")
+                self.graph = None
+        torch.cuda.synchronize()
+
+    def run(self, calls):
+        """Enqueues `calls` calls (a multiple of per_graph) on the current stream."""
+        torch = self.torch
+        cur = torch.cuda.current_stream()
+        if self.graph is not None:
+            for _ in range(calls // self.per_graph):
+                self.graph.replay()
+        else:
+            for i in range(calls):
+                self.fn(i, cur.cuda_stream)
+
+    def time(self, calls):
+        """Seconds for `calls` calls, HIP events on the launching stream."""
+        torch = self.torch
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record()
+        self.run(calls)
+        end.record()
+        end.synchronize()
+        return start.elapsed_time(end) / 1e3
+
+
+def round_up(v, m):
+    return (v + m - 1) // m * m
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--copies", type=int, default=10, help="distinct weight copies rotated through")
+    ap.add_argument("--per-graph", type=int, default=100, help="calls captured per HIP graph")
+    ap.add_argument("--gemm-steps", type=int, default=50)
+    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=8.0, help="bound on CPU-baseline timing")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this path runs on a single MI355X and takes no "
+              f"multi-GPU figure (asked for --gpus {args.gpus}).", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import magnetar_gpu as mg
+    from magnetar_gpu import workloads
+
+    torch.cuda.set_device(0)
+    ctx = mg.Context(0)
+    per_graph = args.per_graph
+    steps = round_up(max(args.steps, per_graph), per_graph)
+    warmup = round_up(max(args.warmup, per_graph), per_graph)
+
+    # ---- decode GEMV: Q4_K x[1, 4096] . W[14336, 4096]^T -------------------------
+    name = "q4k_14336x4096_s1"
+    fmt, n, k, seed, _ = workloads.WEIGHTS[name]
+    wbytes = workloads.weight_bytes(name)
+    weight_bytes = workloads.weight_bytes_per_call(name)
+    copies = [ctx.upload(fmt, n, k, wbytes) for _ in range(args.copies)]
+    x_host = workloads.activations(seed, 1, k)
+    x = torch.from_numpy(x_host).cuda()
+    y = torch.empty((1, n), dtype=torch.float32, device="cuda")
+    xq = torch.empty(k, dtype=torch.int8, device="cuda")
+    xs = torch.empty(k // 32, dtype=torch.float32, device="cuda")
+    xh = torch.empty(k // 16, dtype=torch.int32, device="cuda")
+    log(f"gemv: {name}, {weight_bytes} weight bytes x {args.copies} copies "
+        f"({args.copies * weight_bytes / 2**20:.0f} MiB rotated)")
+
+    def step(i, stream):
+        ctx.matmul_dev(copies[i % len(copies)], x.data_ptr(), 1, k, y.data_ptr(), int8=True, stream=stream)
+
+    def gemv_only(i, stream):
+        ctx.matmul_prequantized_dev(copies[i % len(copies)], xq.data_ptr(), xs.data_ptr(), xh.data_ptr(), 1, k,
+                                    y.data_ptr(), stream=stream)
+
+    ctx.quantize_activations_dev(x.data_ptr(), 1, k, xq.data_ptr(), xs.data_ptr(), xh.data_ptr(),
+                                 torch.cuda.current_stream().cuda_stream)
+    use_graph = not args.no_graph
+    step_runner = GraphRunner(torch, step, per_graph, use_graph)
+    step_runner.time(warmup)
+    t_step = step_runner.time(steps)
+    ms_per_step = t_step / steps * 1e3
+    value = weight_bytes * steps / t_step / 1e9
+    log(f"gemv step (quantize + GEMV): {ms_per_step * 1e3:.2f} us/step, {value:.1f} GB/s")
+
+    kernel_runner = GraphRunner(torch, gemv_only, per_graph, use_graph)
+    kernel_runner.time(warmup)
+    t_kernel = kernel_runner.time(steps)
+    kernel_us = t_kernel / steps * 1e6
+    achieved = weight_bytes / (kernel_us * 1e-6) / 1e9
+    log(f"gemv kernel alone: {kernel_us:.2f} us, {achieved:.1f} GB/s = {achieved / HBM_PEAK_GBS:.3f} of HBM peak")
+
+    # parity spot check of the timed path against the oracle
+    torch.cuda.synchronize()
+    step(0, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    y_gpu = y.cpu().numpy()
+
+    # ---- other decode shapes (kernel alone) --------------------------------------
+    extra = {}
+    for m in (2, 4, 8):
+        xm = torch.from_numpy(workloads.activations(seed, m, k)).cuda()
+        qv = torch.empty(m * k, dtype=torch.int8, device="cuda")
+        qs = torch.empty(m * k // 32, dtype=torch.float32, device="cuda")
+        qh = torch.empty(m * k // 16, dtype=torch.int32, device="cuda")
+        ym = torch.empty((m, n), dtype=torch.float32, device="cuda")
+        ctx.quantize_activations_dev(xm.data_ptr(), m, k, qv.data_ptr(), qs.data_ptr(), qh.data_ptr(),
+                                     torch.cuda.current_stream().cuda_stream)
+
+        def gm(i, stream, m=m, qv=qv, qs=qs, qh=qh, ym=ym):
+            ctx.matmul_prequantized_dev(copies[i % len(copies)], qv.data_ptr(), qs.data_ptr(), qh.data_ptr(), m,
+                                        k, ym.data_ptr(), stream=stream)
+
+        r = GraphRunner(torch, gm, per_graph, use_graph)
+        r.time(per_graph)
+        t = r.time(5 * per_graph) / (5 * per_graph)
+        extra[f"q4k_gemv_m{m}_kernel_us"] = round(t * 1e6, 3)
+        extra[f"q4k_gemv_m{m}_GBps"] = round(weight_bytes / t / 1e9, 1)
+        log(f"gemv m={m} kernel: {t * 1e6:.2f} us, {weight_bytes / t / 1e9:.1f} GB/s")
+
+    # IQ4_XS GEMV x[1, 14336] . W[4096, 14336]^T
+    iname = "iq4xs_4096x14336_s3"
+    ifmt, inn, ik, iseed, _ = workloads.WEIGHTS[iname]
+    ibytes = workloads.weight_bytes_per_call(iname)
+    iw = workloads.weight_bytes(iname)
+    icopies = [ctx.upload(ifmt, inn, ik, iw) for _ in range(args.copies)]
+    ix = torch.from_numpy(workloads.activations(iseed, 1, ik)).cuda()
+    iq = torch.empty(ik, dtype=torch.int8, device="cuda")
+    isc = torch.empty(ik // 32, dtype=torch.float32, device="cuda")
+    ish = torch.empty(ik // 16, dtype=torch.int32, device="cuda")
+    iy = torch.empty((1, inn), dtype=torch.float32, device="cuda")
+    ctx.quantize_activations_dev(ix.data_ptr(), 1, ik, iq.data_ptr(), isc.data_ptr(), ish.data_ptr(),
+                                 torch.cuda.current_stream().cuda_stream)
+
+    def ig(i, stream):
+        ctx.matmul_prequantized_dev(icopies[i % len(icopies)], iq.data_ptr(), isc.data_ptr(), ish.data_ptr(), 1, ik,
+                                    iy.data_ptr(), stream=stream)
+
+    r = GraphRunner(torch, ig, per_graph, use_graph)
+    r.time(per_graph)
+    t = r.time(5 * per_graph) / (5 * per_graph)
+    extra["iq4xs_gemv_kernel_us"] = round(t * 1e6, 3)
+    extra["iq4xs_gemv_GBps"] = round(ibytes / t / 1e9, 1)
+    extra["iq4xs_gemv_frac_hbm"] = round(ibytes / t / 1e9 / HBM_PEAK_GBS, 4)
+    log(f"iq4xs gemv kernel: {t * 1e6:.2f} us, {ibytes / t / 1e9:.1f} GB/s")
+    for h in icopies:
+        h.release()
+
+    # ---- prefill GEMM: x[512, 4096] . W[14336, 4096]^T ---------------------------
+    gname = "q4k_14336x4096_s2"
+    gfmt, gn, gk, gseed, _ = workloads.WEIGHTS[gname]
+    gm_rows = 512
+    gw = ctx.upload(gfmt, gn, gk, workloads.weight_bytes(gname))
+    gx = torch.from_numpy(workloads.activations(gseed, gm_rows, gk)).cuda()
+    ga = torch.empty(gm_rows * gk, dtype=torch.float16, device="cuda")
+    gy = torch.empty((gm_rows, gn), dtype=torch.float32, device="cuda")
+    flops = 2.0 * gm_rows * gn * gk
+
+    def gstep(i, stream):
+        ctx.matmul_dev(gw, gx.data_ptr(), gm_rows, gk, gy.data_ptr(), int8=True, stream=stream)
+
+    def gkern(i, stream):
+        ctx.matmul_f16_dev(gw, ga.data_ptr(), gm_rows, gk, gy.data_ptr(), stream=stream)
+
+    ctx.prepare_activations_f16_dev(gx.data_ptr(), gm_rows, gk, ga.data_ptr(), int8=True,
+                                    stream=torch.cuda.current_stream().cuda_stream)
+    gper = 10
+    gsteps = round_up(max(args.gemm_steps, gper), gper)
+    r = GraphRunner(torch, gstep, gper, use_graph)
+    r.time(gper)
+    t_gstep = r.time(gsteps) / gsteps
+    r = GraphRunner(torch, gkern, gper, use_graph)
+    r.time(gper)
+    t_gkern = r.time(gsteps) / gsteps
+    gemm = {
+        "workload": "Q4_K prefill GEMM x[512,4096] . W[14336,4096]^T, seed 2",
+        "step_tflops": round(flops / t_gstep / 1e12, 2),
+        "ms_per_step": round(t_gstep * 1e3, 4),
+        "roofline": {"bound": "mfma", "achieved": round(flops / t_gkern / 1e12, 2), "peak": F16_MFMA_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(flops / t_gkern / 1e12 / F16_MFMA_PEAK_TFLOPS, 4),
+                     "traffic": None, "kernel_us": round(t_gkern * 1e6, 2),
+                     "peak_basis": "dense f16 MFMA (f16 activations x f16-dequantized weights, f32 accumulate)"},
+    }
+    log(f"gemm m=512: step {t_gstep * 1e6:.1f} us ({flops / t_gstep / 1e12:.1f} TFLOP/s), "
+        f"kernel {t_gkern * 1e6:.1f} us ({flops / t_gkern / 1e12:.1f} TFLOP/s)")
+    gw.release()
+
+    # ---- CPU baseline: the reference's AVX2 path on this host ------------------------
+    cpu = None
+    if not args.no_cpu:
+        import oracle
+
+        threads = min(16, os.cpu_count() or 1)
+        got = oracle.baseline_packed_matmul(fmt, wbytes, n, k, x_host, threads)  # warm-up
+        err = float(np.max(np.abs(got - y_gpu)))
+        reps = 0
+        t0 = time.perf_counter()
+        while reps < 10 or (time.perf_counter() - t0 < args.cpu_seconds and reps < 1000):
+            oracle.baseline_packed_matmul(fmt, wbytes, n, k, x_host, threads)
+            reps += 1
+        t_cpu = (time.perf_counter() - t0) / reps
+        t1_reps = 0
+        t0 = time.perf_counter()
+        while t1_reps < 3 or (time.perf_counter() - t0 < args.cpu_seconds / 4 and t1_reps < 50):
+            oracle.baseline_packed_matmul(fmt, wbytes, n, k, x_host, 1)
+            t1_reps += 1
+        t_cpu1 = (time.perf_counter() - t0) / t1_reps
+        cpu = {
+            "value": round(weight_bytes / t_cpu / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": (f"Q4_K x[1,4096] . W[14336,4096]^T, int8 activations, AVX2 column kernels + "
+                       f"pool chunking; 1 warm-up + {reps} timed calls ({t_cpu * 1e3:.2f} ms/call)"),
+            "single_thread_GBps": round(weight_bytes / t_cpu1 / 1e9, 2),
+            "cpu_model": cpu_model(),
+            "max_abs_diff_vs_gpu": err,
+        }
+        log(f"cpu baseline ({threads} threads, {cpu_model()}): {t_cpu * 1e3:.2f} ms/call, "
+            f"{cpu['value']} GB/s; 1 thread {cpu['single_thread_GBps']} GB/s; max|gpu-cpu| {err:.2e}")
+
+    for h in copies:
+        h.release()
+    ctx.close()
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(ms_per_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {
+            "workload": "Q4_K decode GEMV x[1,4096] . W[14336,4096]^T (Llama-3-8B FFN up), seed 1",
+            "m": 1, "n": n, "k": k, "weight_bytes": weight_bytes, "weight_copies": args.copies,
+            "launch": "hip_graph" if (use_graph and step_runner.graph is not None) else "eager",
+        },
+        "roofline": {
+            "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel_us": round(kernel_us, 3),
+        },
+        "cpu_baseline": cpu,
+        "gemm": gemm,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

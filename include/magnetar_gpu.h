@@ -1,0 +1,146 @@
+/*
+ * magnetar_gpu: the MI355X (gfx950) packed-weight matmul behind the
+ * Provider's `matmul` Kernel, as a C ABI (libmagnetar_gpu.so).
+ *
+ * Plain pointers and sizes only. Host pointers are borrowed for the call;
+ * device pointers (the *_dev entry points) must be device memory of the
+ * context's GPU, and work is enqueued on the given HIP stream (a
+ * hipStream_t; NULL is HIP's null stream) and is asynchronous. The
+ * host-pointer entry points run on the context's own stream and return
+ * when their results are in host memory. Every entry point returns an
+ * MQ_* status; on failure mq_last_error() holds the reason. Nothing aborts
+ * across the ABI.
+ *
+ * Each declaration names the reference interface it replaces (paths
+ * relative to the reference repository root).
+ */
+#ifndef MAGNETAR_GPU_H
+#define MAGNETAR_GPU_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ggml type ids (public GGUF specification). */
+#define MQ_TYPE_Q4_K 12u
+#define MQ_TYPE_IQ4_XS 23u
+
+/* Status codes. */
+#define MQ_OK 0
+#define MQ_ERR_SHAPE 1     /* KernelError::KernelExecutionFailed (shape) */
+#define MQ_ERR_DTYPE 2     /* KernelError::KernelDTypeUnsupported */
+#define MQ_DECLINED 3      /* PackedWeightWrite::Declined: caller falls back */
+#define MQ_ERR_HIP 4       /* a HIP runtime error */
+#define MQ_ERR_OOM 5       /* device allocation failed */
+#define MQ_ERR_ARGUMENT 6  /* null pointer, unknown handle, bad flag */
+
+/* matmul flags */
+#define MQ_INT8_ACTIVATIONS 1u /* MAGNETAR_CPU_INT8_ACTIVATIONS (default on) */
+
+typedef struct mq_ctx mq_ctx;
+
+/* A context on HIP device `device`, with its own stream and workspace.
+ * Replaces the executor state `NativeState` built by
+ * `NativeCpuExecutor::with_settings` (src/native/mod.rs:525-544). */
+int mq_create(int device, mq_ctx **out);
+
+/* Frees every device buffer of the context (src/native/mod.rs:476-497,
+ * the executor's Drop). */
+void mq_destroy(mq_ctx *ctx);
+
+/* The calling thread's last error on `ctx` (ctx NULL: the thread's last
+ * mq_create error). Valid until that thread's next call on the context.
+ * Mirrors the `reason` text of KernelError (src/native/mod.rs:119-124). */
+const char *mq_last_error(mq_ctx *ctx);
+
+/* Uploads a packed weight: `stored_rows` rows of `stored_cols` values,
+ * `len` = stored_rows * stored_cols / 256 * block_bytes checkpoint bytes.
+ * Returns MQ_DECLINED for a type other than Q4_K / IQ4_XS or for
+ * transposed == 0 (stored rows are the input rows: the axpy layout), so
+ * the caller keeps the f32 path. Replaces
+ * `write_packed_weight_tensor` -> `PackedWeightWrite::{Stored,Declined}`
+ * (src/native/mod.rs:638-653) and `PackedWeight::new` (external,
+ * magnetar-provider-api; used at src/native/tests.rs:66). */
+int mq_weight_upload(mq_ctx *ctx, uint32_t gguf_type, uint64_t stored_rows,
+                     uint64_t stored_cols, int transposed, const uint8_t *bytes,
+                     size_t len, uint64_t *handle);
+
+/* Releases a weight's device memory. Replaces `forget_packed` /
+ * `release_tensor` (src/native/mod.rs:560-562, 655-660). */
+int mq_weight_release(mq_ctx *ctx, uint64_t handle);
+
+/* A weight's format, stored shape and device footprint. The logical shape
+ * is [stored_cols, stored_rows] when transposed (`resident_shape`,
+ * src/native/mod.rs:459-462). */
+int mq_weight_info(mq_ctx *ctx, uint64_t handle, uint32_t *gguf_type,
+                   uint64_t *stored_rows, uint64_t *stored_cols, int *transposed,
+                   uint64_t *device_bytes);
+
+/* y[m][stored_rows] = x[m][k] . W^T, host pointers, synchronous (returns
+ * after y is copied back). k must equal stored_cols (else MQ_ERR_SHAPE).
+ * flags & MQ_INT8_ACTIVATIONS selects int8 activations (the reference
+ * default) else f32 activations. Replaces `NativeState::packed_matmul`
+ * (src/native/mod.rs:110-152) with `quant::matmul_columns`
+ * (src/native/quant.rs:430-446). */
+int mq_matmul(mq_ctx *ctx, uint64_t handle, const float *x, uint64_t m,
+              uint64_t k, uint32_t flags, float *y);
+
+/* mq_matmul on device pointers, enqueued on `stream` (a hipStream_t). */
+int mq_matmul_dev(mq_ctx *ctx, uint64_t handle, const float *x_dev, uint64_t m,
+                  uint64_t k, uint32_t flags, float *y_dev, void *stream);
+
+/* Int8 activation quantization on device: values[m*k], scales[m*k/32],
+ * sums[m*k/32][2] (int32 half sums). Replaces `quant::quantize_rows`
+ * (src/native/quant.rs:350-378). */
+int mq_quantize_activations_dev(mq_ctx *ctx, const float *x_dev, uint64_t m,
+                                uint64_t k, int8_t *values_dev,
+                                float *scales_dev, int32_t *sums_dev,
+                                void *stream);
+
+/* The decode GEMV on already-quantized activations (m <= 8): the column
+ * kernels' int8 path `columns_q4k_avx2` / `columns_iq4xs_avx2`
+ * (src/native/quant.rs:666-744, 1386-1433) without the quantization step,
+ * so one quantized activation can feed several weights. */
+int mq_matmul_prequantized_dev(mq_ctx *ctx, uint64_t handle,
+                               const int8_t *values_dev, const float *scales_dev,
+                               const int32_t *sums_dev, uint64_t m, uint64_t k,
+                               float *y_dev, void *stream);
+
+/* The prefill path's activation operand on device: a16[m*k] f16 holding
+ * f16(int8_rounded(x)) with MQ_INT8_ACTIVATIONS (the values the reference's
+ * int8 activations stand for, `int8_rounded`, src/native/tests.rs:77-89),
+ * else f16(x). */
+int mq_prepare_activations_f16_dev(mq_ctx *ctx, const float *x_dev, uint64_t m,
+                                   uint64_t k, uint32_t flags, uint16_t *a16_dev,
+                                   void *stream);
+
+/* The prefill GEMM on prepared f16 activations (any m): y[m][stored_rows]
+ * = a16 . dequantize(W)^T with f32 accumulation, the MFMA replacement of
+ * the column kernels for many activation rows
+ * (src/native/quant.rs:666-744, 1386-1433 via src/native/mod.rs:110-152). */
+int mq_matmul_f16_dev(mq_ctx *ctx, uint64_t handle, const uint16_t *a16_dev,
+                      uint64_t m, uint64_t k, float *y_dev, void *stream);
+
+/* Bit-exact dequantization into host memory, stored layout
+ * [stored_rows][stored_cols] (logical == 0) or the logical transposed
+ * layout [stored_cols][stored_rows] (logical != 0). Replaces
+ * `PackedWeight::dequantize_stored` / `dequantize` (external) and
+ * `quant::dequantize_row` (src/native/quant.rs:1702-1711), reached through
+ * `read_tensor` -> `materialize` (src/lib.rs:1615-1620,
+ * src/native/mod.rs:196-204). */
+int mq_dequantize(mq_ctx *ctx, uint64_t handle, int logical, float *out);
+
+/* mq_dequantize into device memory, enqueued on `stream`. */
+int mq_dequantize_dev(mq_ctx *ctx, uint64_t handle, int logical, float *out_dev,
+                      void *stream);
+
+/* Library version string. */
+const char *mq_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

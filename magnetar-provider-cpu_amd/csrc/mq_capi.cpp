@@ -1,0 +1,444 @@
+// C ABI of libmagnetar_gpu.so (declared in include/magnetar_gpu.h): device
+// contexts, packed-weight upload into the tiled HBM layout, and the
+// matmul / quantize / dequantize entry points. Shapes, buffer sizes and
+// launch grids are validated here before any kernel runs.
+#include <hip/hip_runtime.h>
+
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <thread>
+#include <unordered_map>
+
+#include "magnetar_gpu.h"
+#include "mq_device.h"
+#include "mq_launch.h"
+
+namespace {
+
+struct Weight {
+  uint32_t type = 0;
+  uint64_t rows = 0, cols = 0, nb = 0, rows_padded = 0;
+  int transposed = 1;
+  uint8_t* dev = nullptr;
+  uint64_t dev_bytes = 0;
+};
+
+thread_local std::string g_create_error;
+
+}  // namespace
+
+struct mq_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::mutex mu;
+  std::unordered_map<uint64_t, Weight> weights;
+  uint64_t next_handle = 1;
+  // Activation workspace: stream-ordered on `ws_stream`; a call on another
+  // stream first waits for the work already queued on it.
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+  hipStream_t ws_stream = nullptr;
+  hipEvent_t ws_event = nullptr;
+  // Host-pointer staging for mq_matmul.
+  void* io = nullptr;
+  size_t io_bytes = 0;
+  int gemv_splits_override = 0;
+  std::mutex err_mu;
+  std::unordered_map<std::thread::id, std::string> errors;
+};
+
+namespace {
+
+int fail(mq_ctx* ctx, int code, const std::string& what) {
+  if (ctx) {
+    std::lock_guard<std::mutex> lock(ctx->err_mu);
+    ctx->errors[std::this_thread::get_id()] = what;
+  } else {
+    g_create_error = what;
+  }
+  return code;
+}
+
+int hip_fail(mq_ctx* ctx, hipError_t e, const char* where) {
+  return fail(ctx, e == hipErrorOutOfMemory ? MQ_ERR_OOM : MQ_ERR_HIP,
+              std::string(where) + ": " + hipGetErrorString(e));
+}
+
+#define MQ_HIP(ctx, call)                                 \
+  do {                                                    \
+    hipError_t e_ = (call);                               \
+    if (e_ != hipSuccess) return hip_fail(ctx, e_, #call); \
+  } while (0)
+
+uint64_t block_bytes(uint32_t type) {
+  return type == MQ_TYPE_Q4_K ? 144 : type == MQ_TYPE_IQ4_XS ? 136 : 0;
+}
+
+class DeviceGuard {
+ public:
+  explicit DeviceGuard(int device) {
+    if (hipGetDevice(&prev_) != hipSuccess) prev_ = -1;
+    if (prev_ != device) (void)hipSetDevice(device);
+    device_ = device;
+  }
+  ~DeviceGuard() {
+    if (prev_ >= 0 && prev_ != device_) (void)hipSetDevice(prev_);
+  }
+
+ private:
+  int prev_ = -1, device_ = 0;
+};
+
+// Makes `stream` the workspace's stream, ordering it after work queued on
+// the previous one, and grows the workspace to `bytes`. Caller holds ctx->mu.
+int acquire_workspace(mq_ctx* ctx, hipStream_t stream, size_t bytes) {
+  if (ctx->ws_stream != stream) {
+    MQ_HIP(ctx, hipEventRecord(ctx->ws_event, ctx->ws_stream));
+    MQ_HIP(ctx, hipStreamWaitEvent(stream, ctx->ws_event, 0));
+    ctx->ws_stream = stream;
+  }
+  if (bytes <= ctx->ws_bytes) return MQ_OK;
+  MQ_HIP(ctx, hipStreamSynchronize(stream));
+  if (ctx->ws) MQ_HIP(ctx, hipFree(ctx->ws));
+  ctx->ws = nullptr;
+  ctx->ws_bytes = 0;
+  size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
+  MQ_HIP(ctx, hipMalloc(&ctx->ws, want));
+  ctx->ws_bytes = want;
+  return MQ_OK;
+}
+
+const Weight* find_weight(mq_ctx* ctx, uint64_t handle) {
+  auto it = ctx->weights.find(handle);
+  return it == ctx->weights.end() ? nullptr : &it->second;
+}
+
+int check_k(mq_ctx* ctx, const Weight& w, uint64_t k) {
+  if (k != w.cols || k % 32 != 0)
+    return fail(ctx, MQ_ERR_SHAPE,
+                "packed matmul: activations have " + std::to_string(k) + " columns, the weight's stored rows " +
+                    std::to_string(w.cols));
+  return MQ_OK;
+}
+
+size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
+
+int gemv_splits(mq_ctx* ctx, const Weight& w) {
+  if (ctx->gemv_splits_override > 0) {
+    int s = ctx->gemv_splits_override;
+    return s > 8 ? 8 : s;
+  }
+  return mq::gemv_default_splits(w.rows, w.nb);
+}
+
+constexpr uint64_t kGemvMaxRows = 8;
+
+// Enqueues y = x . W^T on `stream`. Caller holds ctx->mu.
+int matmul_locked(mq_ctx* ctx, const Weight& w, const float* x, uint64_t m, uint64_t k, uint32_t flags, float* y,
+                  hipStream_t stream) {
+  int rc = check_k(ctx, w, k);
+  if (rc) return rc;
+  if (flags & ~MQ_INT8_ACTIVATIONS) return fail(ctx, MQ_ERR_ARGUMENT, "unknown matmul flag bits");
+  if (m == 0) return MQ_OK;
+  if (!x || !y) return fail(ctx, MQ_ERR_ARGUMENT, "null activation or output pointer");
+  const bool int8 = (flags & MQ_INT8_ACTIVATIONS) != 0;
+  if (m <= kGemvMaxRows) {
+    if (int8) {
+      const size_t vb = align256(m * k), sb = align256(m * k / 32 * 4), hb = align256(m * k / 32 * 8);
+      rc = acquire_workspace(ctx, stream, vb + sb + hb);
+      if (rc) return rc;
+      auto* base = static_cast<uint8_t*>(ctx->ws);
+      auto* values = reinterpret_cast<int8_t*>(base);
+      auto* scales = reinterpret_cast<float*>(base + vb);
+      auto* sums = reinterpret_cast<int32_t*>(base + vb + sb);
+      mq::launch_quantize_activations(x, m, k, values, scales, sums, nullptr, 1, stream);
+      mq::launch_gemv_int8(static_cast<int>(w.type), w.dev, w.rows, w.nb, values, scales, sums, m, y,
+                           gemv_splits(ctx, w), stream);
+    } else {
+      mq::launch_gemv_f32(static_cast<int>(w.type), w.dev, w.rows, w.nb, x, m, y, gemv_splits(ctx, w), stream);
+    }
+  } else {
+    rc = acquire_workspace(ctx, stream, align256(m * k * 2));
+    if (rc) return rc;
+    auto* a16 = static_cast<uint16_t*>(ctx->ws);
+    if (int8)
+      mq::launch_quantize_activations(x, m, k, nullptr, nullptr, nullptr, a16, 1, stream);
+    else
+      mq::launch_activations_f16(x, m, k, a16, stream);
+    mq::launch_gemm(static_cast<int>(w.type), w.dev, w.rows, w.nb, a16, m, y, stream);
+  }
+  MQ_HIP(ctx, hipGetLastError());
+  return MQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* mq_version(void) { return "magnetar_gpu 0.1.0 (gfx950)"; }
+
+int mq_create(int device, mq_ctx** out) {
+  if (!out) return fail(nullptr, MQ_ERR_ARGUMENT, "mq_create: null out pointer");
+  *out = nullptr;
+  int count = 0;
+  hipError_t e = hipGetDeviceCount(&count);
+  if (e != hipSuccess) return hip_fail(nullptr, e, "hipGetDeviceCount");
+  if (device < 0 || device >= count)
+    return fail(nullptr, MQ_ERR_ARGUMENT, "mq_create: no HIP device " + std::to_string(device));
+  DeviceGuard guard(device);
+  auto* ctx = new (std::nothrow) mq_ctx();
+  if (!ctx) return fail(nullptr, MQ_ERR_OOM, "mq_create: out of host memory");
+  ctx->device = device;
+  if ((e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking)) != hipSuccess ||
+      (e = hipEventCreateWithFlags(&ctx->ws_event, hipEventDisableTiming)) != hipSuccess) {
+    if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return hip_fail(nullptr, e, "mq_create");
+  }
+  ctx->ws_stream = ctx->stream;
+  if (const char* s = std::getenv("MQ_GEMV_SPLITS")) ctx->gemv_splits_override = std::atoi(s);
+  *out = ctx;
+  return MQ_OK;
+}
+
+void mq_destroy(mq_ctx* ctx) {
+  if (!ctx) return;
+  DeviceGuard guard(ctx->device);
+  (void)hipDeviceSynchronize();
+  for (auto& kv : ctx->weights) (void)hipFree(kv.second.dev);
+  if (ctx->ws) (void)hipFree(ctx->ws);
+  if (ctx->io) (void)hipFree(ctx->io);
+  (void)hipEventDestroy(ctx->ws_event);
+  (void)hipStreamDestroy(ctx->stream);
+  delete ctx;
+}
+
+const char* mq_last_error(mq_ctx* ctx) {
+  if (!ctx) return g_create_error.c_str();
+  std::lock_guard<std::mutex> lock(ctx->err_mu);
+  return ctx->errors[std::this_thread::get_id()].c_str();
+}
+
+int mq_weight_upload(mq_ctx* ctx, uint32_t gguf_type, uint64_t stored_rows, uint64_t stored_cols, int transposed,
+                     const uint8_t* bytes, size_t len, uint64_t* handle) {
+  if (!ctx || !handle) return fail(ctx, MQ_ERR_ARGUMENT, "mq_weight_upload: null argument");
+  *handle = 0;
+  const uint64_t bb = block_bytes(gguf_type);
+  if (!bb)
+    return fail(ctx, MQ_DECLINED, "packed weight format " + std::to_string(gguf_type) + " has no GPU path");
+  if (!transposed)
+    return fail(ctx, MQ_DECLINED, "packed weight stores input rows (untransposed): no GPU path");
+  if (stored_rows == 0 || stored_cols == 0 || stored_cols % 256 != 0)
+    return fail(ctx, MQ_ERR_SHAPE,
+                "packed weight: stored shape [" + std::to_string(stored_rows) + ", " + std::to_string(stored_cols) +
+                    "] is not whole 256-value blocks");
+  const uint64_t nb = stored_cols / 256;
+  if (stored_rows > (1ull << 32) || nb > (1ull << 24) || len != stored_rows * nb * bb)
+    return fail(ctx, MQ_ERR_SHAPE,
+                "packed weight: " + std::to_string(len) + " bytes for " + std::to_string(stored_rows) + " x " +
+                    std::to_string(stored_cols) + " values");
+  if (!bytes) return fail(ctx, MQ_ERR_ARGUMENT, "mq_weight_upload: null bytes");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  DeviceGuard guard(ctx->device);
+  Weight w;
+  w.type = gguf_type;
+  w.rows = stored_rows;
+  w.cols = stored_cols;
+  w.nb = nb;
+  w.rows_padded = (stored_rows + 7) / 8 * 8;
+  w.transposed = transposed;
+  w.dev_bytes = w.rows_padded / 8 * nb * static_cast<uint64_t>(mq::tile_bytes(static_cast<int>(gguf_type)));
+  uint8_t* raw = nullptr;
+  hipError_t e = hipMalloc(&raw, len);
+  if (e != hipSuccess) return hip_fail(ctx, e, "hipMalloc(staging)");
+  e = hipMalloc(&w.dev, w.dev_bytes);
+  if (e != hipSuccess) {
+    (void)hipFree(raw);
+    return hip_fail(ctx, e, "hipMalloc(weight)");
+  }
+  if ((e = hipMemcpyAsync(raw, bytes, len, hipMemcpyHostToDevice, ctx->stream)) == hipSuccess &&
+      (e = hipMemsetAsync(w.dev, 0, w.dev_bytes, ctx->stream)) == hipSuccess) {
+    mq::launch_repack(static_cast<int>(gguf_type), raw, stored_rows, nb, w.dev, ctx->stream);
+    e = hipGetLastError();
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  }
+  (void)hipFree(raw);
+  if (e != hipSuccess) {
+    (void)hipFree(w.dev);
+    return hip_fail(ctx, e, "mq_weight_upload");
+  }
+  *handle = ctx->next_handle++;
+  ctx->weights.emplace(*handle, w);
+  return MQ_OK;
+}
+
+int mq_weight_release(mq_ctx* ctx, uint64_t handle) {
+  if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_weight_release: null context");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  auto it = ctx->weights.find(handle);
+  if (it == ctx->weights.end()) return fail(ctx, MQ_ERR_ARGUMENT, "unknown weight handle " + std::to_string(handle));
+  DeviceGuard guard(ctx->device);
+  // Work already queued may still read the weight.
+  MQ_HIP(ctx, hipDeviceSynchronize());
+  MQ_HIP(ctx, hipFree(it->second.dev));
+  ctx->weights.erase(it);
+  return MQ_OK;
+}
+
+int mq_weight_info(mq_ctx* ctx, uint64_t handle, uint32_t* gguf_type, uint64_t* stored_rows, uint64_t* stored_cols,
+                   int* transposed, uint64_t* device_bytes) {
+  if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_weight_info: null context");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  const Weight* w = find_weight(ctx, handle);
+  if (!w) return fail(ctx, MQ_ERR_ARGUMENT, "unknown weight handle " + std::to_string(handle));
+  if (gguf_type) *gguf_type = w->type;
+  if (stored_rows) *stored_rows = w->rows;
+  if (stored_cols) *stored_cols = w->cols;
+  if (transposed) *transposed = w->transposed;
+  if (device_bytes) *device_bytes = w->dev_bytes;
+  return MQ_OK;
+}
+
+int mq_matmul_dev(mq_ctx* ctx, uint64_t handle, const float* x_dev, uint64_t m, uint64_t k, uint32_t flags,
+                  float* y_dev, void* stream) {
+  if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_matmul_dev: null context");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  const Weight* w = find_weight(ctx, handle);
+  if (!w) return fail(ctx, MQ_ERR_ARGUMENT, "unknown weight handle " + std::to_string(handle));
+  DeviceGuard guard(ctx->device);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return matmul_locked(ctx, *w, x_dev, m, k, flags, y_dev, s);
+}
+
+int mq_matmul(mq_ctx* ctx, uint64_t handle, const float* x, uint64_t m, uint64_t k, uint32_t flags, float* y) {
+  if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_matmul: null context");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  const Weight* w = find_weight(ctx, handle);
+  if (!w) return fail(ctx, MQ_ERR_ARGUMENT, "unknown weight handle " + std::to_string(handle));
+  int rc = check_k(ctx, *w, k);
+  if (rc) return rc;
+  if (m == 0) return MQ_OK;
+  if (!x || !y) return fail(ctx, MQ_ERR_ARGUMENT, "mq_matmul: null host pointer");
+  DeviceGuard guard(ctx->device);
+  const size_t xb = align256(m * k * sizeof(float)), yb = align256(m * w->rows * sizeof(float));
+  if (xb + yb > ctx->io_bytes) {
+    MQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (ctx->io) MQ_HIP(ctx, hipFree(ctx->io));
+    ctx->io = nullptr;
+    ctx->io_bytes = 0;
+    MQ_HIP(ctx, hipMalloc(&ctx->io, xb + yb));
+    ctx->io_bytes = xb + yb;
+  }
+  auto* xd = static_cast<float*>(ctx->io);
+  auto* yd = reinterpret_cast<float*>(static_cast<uint8_t*>(ctx->io) + xb);
+  MQ_HIP(ctx, hipMemcpyAsync(xd, x, m * k * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
+  rc = matmul_locked(ctx, *w, xd, m, k, flags, yd, ctx->stream);
+  if (rc) return rc;
+  MQ_HIP(ctx, hipMemcpyAsync(y, yd, m * w->rows * sizeof(float), hipMemcpyDeviceToHost, ctx->stream));
+  MQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return MQ_OK;
+}
+
+int mq_quantize_activations_dev(mq_ctx* ctx, const float* x_dev, uint64_t m, uint64_t k, int8_t* values_dev,
+                                float* scales_dev, int32_t* sums_dev, void* stream) {
+  if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_quantize_activations_dev: null context");
+  if (k % 32 != 0) return fail(ctx, MQ_ERR_SHAPE, "activation rows must hold whole 32-value blocks");
+  if (m == 0) return MQ_OK;
+  if (!x_dev || !values_dev || !scales_dev || !sums_dev)
+    return fail(ctx, MQ_ERR_ARGUMENT, "mq_quantize_activations_dev: null pointer");
+  DeviceGuard guard(ctx->device);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  mq::launch_quantize_activations(x_dev, m, k, values_dev, scales_dev, sums_dev, nullptr, 1, s);
+  MQ_HIP(ctx, hipGetLastError());
+  return MQ_OK;
+}
+
+int mq_matmul_prequantized_dev(mq_ctx* ctx, uint64_t handle, const int8_t* values_dev, const float* scales_dev,
+                               const int32_t* sums_dev, uint64_t m, uint64_t k, float* y_dev, void* stream) {
+  if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_matmul_prequantized_dev: null context");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  const Weight* w = find_weight(ctx, handle);
+  if (!w) return fail(ctx, MQ_ERR_ARGUMENT, "unknown weight handle " + std::to_string(handle));
+  int rc = check_k(ctx, *w, k);
+  if (rc) return rc;
+  if (m > kGemvMaxRows) return fail(ctx, MQ_ERR_SHAPE, "prequantized matmul takes at most 8 activation rows");
+  if (m == 0) return MQ_OK;
+  if (!values_dev || !scales_dev || !sums_dev || !y_dev)
+    return fail(ctx, MQ_ERR_ARGUMENT, "mq_matmul_prequantized_dev: null pointer");
+  DeviceGuard guard(ctx->device);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  mq::launch_gemv_int8(static_cast<int>(w->type), w->dev, w->rows, w->nb, values_dev, scales_dev, sums_dev, m, y_dev,
+                       gemv_splits(ctx, *w), s);
+  MQ_HIP(ctx, hipGetLastError());
+  return MQ_OK;
+}
+
+int mq_prepare_activations_f16_dev(mq_ctx* ctx, const float* x_dev, uint64_t m, uint64_t k, uint32_t flags,
+                                   uint16_t* a16_dev, void* stream) {
+  if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_prepare_activations_f16_dev: null context");
+  if (flags & ~MQ_INT8_ACTIVATIONS) return fail(ctx, MQ_ERR_ARGUMENT, "unknown flag bits");
+  if (k % 32 != 0) return fail(ctx, MQ_ERR_SHAPE, "activation rows must hold whole 32-value blocks");
+  if (m == 0) return MQ_OK;
+  if (!x_dev || !a16_dev) return fail(ctx, MQ_ERR_ARGUMENT, "mq_prepare_activations_f16_dev: null pointer");
+  DeviceGuard guard(ctx->device);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (flags & MQ_INT8_ACTIVATIONS)
+    mq::launch_quantize_activations(x_dev, m, k, nullptr, nullptr, nullptr, a16_dev, 1, s);
+  else
+    mq::launch_activations_f16(x_dev, m, k, a16_dev, s);
+  MQ_HIP(ctx, hipGetLastError());
+  return MQ_OK;
+}
+
+int mq_matmul_f16_dev(mq_ctx* ctx, uint64_t handle, const uint16_t* a16_dev, uint64_t m, uint64_t k, float* y_dev,
+                      void* stream) {
+  if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_matmul_f16_dev: null context");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  const Weight* w = find_weight(ctx, handle);
+  if (!w) return fail(ctx, MQ_ERR_ARGUMENT, "unknown weight handle " + std::to_string(handle));
+  int rc = check_k(ctx, *w, k);
+  if (rc) return rc;
+  if (m == 0) return MQ_OK;
+  if (!a16_dev || !y_dev) return fail(ctx, MQ_ERR_ARGUMENT, "mq_matmul_f16_dev: null pointer");
+  DeviceGuard guard(ctx->device);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  mq::launch_gemm(static_cast<int>(w->type), w->dev, w->rows, w->nb, a16_dev, m, y_dev, s);
+  MQ_HIP(ctx, hipGetLastError());
+  return MQ_OK;
+}
+
+int mq_dequantize_dev(mq_ctx* ctx, uint64_t handle, int logical, float* out_dev, void* stream) {
+  if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_dequantize_dev: null context");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  const Weight* w = find_weight(ctx, handle);
+  if (!w) return fail(ctx, MQ_ERR_ARGUMENT, "unknown weight handle " + std::to_string(handle));
+  if (!out_dev) return fail(ctx, MQ_ERR_ARGUMENT, "mq_dequantize_dev: null output");
+  DeviceGuard guard(ctx->device);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  mq::launch_dequantize(static_cast<int>(w->type), w->dev, w->rows, w->nb, logical, out_dev, s);
+  MQ_HIP(ctx, hipGetLastError());
+  return MQ_OK;
+}
+
+int mq_dequantize(mq_ctx* ctx, uint64_t handle, int logical, float* out) {
+  if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_dequantize: null context");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  const Weight* w = find_weight(ctx, handle);
+  if (!w) return fail(ctx, MQ_ERR_ARGUMENT, "unknown weight handle " + std::to_string(handle));
+  if (!out) return fail(ctx, MQ_ERR_ARGUMENT, "mq_dequantize: null output");
+  DeviceGuard guard(ctx->device);
+  const size_t bytes = w->rows * w->cols * sizeof(float);
+  float* dev = nullptr;
+  MQ_HIP(ctx, hipMalloc(&dev, bytes));
+  mq::launch_dequantize(static_cast<int>(w->type), w->dev, w->rows, w->nb, logical, dev, ctx->stream);
+  hipError_t e = hipGetLastError();
+  if (e == hipSuccess) e = hipMemcpyAsync(out, dev, bytes, hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  (void)hipFree(dev);
+  if (e != hipSuccess) return hip_fail(ctx, e, "mq_dequantize");
+  return MQ_OK;
+}
+
+}  // extern "C"

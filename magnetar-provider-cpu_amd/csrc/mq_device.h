@@ -1,0 +1,102 @@
+// Device-side layout and decode helpers shared by the gfx950 kernels.
+//
+// HBM layout of a packed weight (chosen at upload; the bytes are the
+// checkpoint's own, permuted, never re-encoded):
+//
+//   stored rows are grouped by 8 (a "row group", zero-padded to a multiple
+//   of 8 rows); each (row group g, super-block b) is one contiguous tile.
+//
+//   Q4_K tile (1152 B): 9 planes x 8 rows x 16 B. Plane 0 holds each row's
+//     block bytes 0..15 (d, dmin, scales[12]); plane 1+p holds block bytes
+//     16+16p .. 31+16p (the quants).
+//   IQ4_XS tile (1088 B): 8 rows x 8 B of block bytes 0..7 (d, scales_h,
+//     scales_l[4]), then 8 planes x 8 rows x 16 B, plane p holding block
+//     bytes 8+16p .. 23+16p (run p's 32 indices).
+//
+//   tile(g, b) starts at (g * nb + b) * tile_bytes, nb = K / 256.
+//
+// So a 64-lane load of one plane by 8 rows x 8 blocks touches eight whole
+// 128-byte lines, and a GEMM K-step reads whole lines per 8 rows.
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mq {
+
+constexpr int kTypeQ4K = 12;
+constexpr int kTypeIq4Xs = 23;
+constexpr int kGroupRows = 8;
+constexpr int kQ4kBlockBytes = 144;
+constexpr int kIq4xsBlockBytes = 136;
+constexpr int kQ4kTileBytes = 1152;
+constexpr int kIq4xsTileBytes = 1088;
+
+__host__ __device__ inline int tile_bytes(int type) {
+  return type == kTypeQ4K ? kQ4kTileBytes : kIq4xsTileBytes;
+}
+
+// The GGUF kvalues_iq4nl codebook packed 4 bytes per word (little end
+// first): words 0..3 hold entries 0..3, 4..7, 8..11, 12..15.
+constexpr uint32_t kIq4Word0 = 0xBFAD9881u;  // -127 -104 -83 -65
+constexpr uint32_t kIq4Word1 = 0xF6EADDCFu;  //  -49  -35 -22 -10
+constexpr uint32_t kIq4Word2 = 0x26190D01u;  //    1   13  25  38
+constexpr uint32_t kIq4Word3 = 0x71594535u;  //   53   69  89 113
+
+__device__ inline float half_bits(uint32_t bits16) {
+  return __half2float(__ushort_as_half(static_cast<unsigned short>(bits16 & 0xFFFFu)));
+}
+
+// Q4_K super-block scales: run j's 6-bit scale and min (ggml
+// get_scale_min_k4) from the 12 scale bytes in header words y, z, w.
+// Bytes 0..3 of the result hold runs 0..3 (lo) or 4..7 (hi).
+struct Q4kSixBit {
+  uint32_t sc_lo, sc_hi, m_lo, m_hi;
+};
+
+__device__ inline Q4kSixBit q4k_six_bit(uint4 hdr) {
+  Q4kSixBit r;
+  r.sc_lo = hdr.y & 0x3F3F3F3Fu;
+  r.m_lo = hdr.z & 0x3F3F3F3Fu;
+  r.sc_hi = (hdr.w & 0x0F0F0F0Fu) | ((hdr.y >> 2) & 0x30303030u);
+  r.m_hi = ((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u);
+  return r;
+}
+
+__device__ inline uint32_t byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xFFu; }
+
+// Run j's 6-bit scale and min as integers, j in 0..7.
+__device__ inline void q4k_sc_m(const Q4kSixBit& s, int j, uint32_t& sc, uint32_t& m) {
+  if (j < 4) {
+    sc = byte_of(s.sc_lo, j);
+    m = byte_of(s.m_lo, j);
+  } else {
+    sc = byte_of(s.sc_hi, j - 4);
+    m = byte_of(s.m_hi, j - 4);
+  }
+}
+
+// IQ4_XS run j's signed scale (ls - 32) from header words x (d | scales_h)
+// and y (scales_l[4]).
+__device__ inline int iq4xs_ls(uint2 hdr, int j) {
+  uint32_t low = (hdr.y >> (4 * j)) & 0xFu;
+  uint32_t high = (hdr.x >> (16 + 2 * j)) & 3u;
+  return static_cast<int>(low | (high << 4)) - 32;
+}
+
+// Four codebook lookups: bytes of `nib` are indices 0..15, result bytes are
+// the signed codebook values.
+__device__ inline uint32_t iq4_lookup4(uint32_t nib) {
+  uint32_t i7 = nib & 0x07070707u;
+  uint32_t lo = __builtin_amdgcn_perm(kIq4Word1, kIq4Word0, i7);
+  uint32_t hi = __builtin_amdgcn_perm(kIq4Word3, kIq4Word2, i7);
+  uint32_t mask = ((nib >> 3) & 0x01010101u) * 0xFFu;
+  return (hi & mask) | (lo & ~mask);
+}
+
+__device__ inline int sdot4(uint32_t a, uint32_t b, int c) {
+  return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), c, false);
+}
+
+}  // namespace mq

@@ -1,0 +1,46 @@
+// Host launchers for the gfx950 kernels (defined in the .hip files).
+// Every launcher checks nothing: the C-ABI layer validates shapes, buffer
+// sizes and grids before calling, and reports errors to the caller.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mq {
+
+// Raw checkpoint bytes (rows x nb blocks, row-major) -> tiled layout.
+void launch_repack(int type, const uint8_t* raw, uint64_t rows, uint64_t nb,
+                   uint8_t* tiled, hipStream_t stream);
+
+// Bit-exact dequantization; logical != 0 writes out[k * rows + n] (the
+// transposed, logical [K, N] view), else out[n * K + k] (stored view).
+void launch_dequantize(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb,
+                       int logical, float* out, hipStream_t stream);
+
+// Int8 activation quantization of x[m][k] per 32-value block; a16 (may be
+// null) receives f16(q * d) when int8 != 0, else f16(x).
+void launch_quantize_activations(const float* x, uint64_t m, uint64_t k, int8_t* values,
+                                 float* scales, int32_t* sums, uint16_t* a16, int int8,
+                                 hipStream_t stream);
+
+// f16 copy of x (f32 activations for the MFMA path), no int8 outputs.
+void launch_activations_f16(const float* x, uint64_t m, uint64_t k, uint16_t* a16,
+                            hipStream_t stream);
+
+// Decode GEMV, m in 1..8, int8 activations.
+void launch_gemv_int8(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb,
+                      const int8_t* values, const float* scales, const int32_t* sums,
+                      uint64_t m, float* y, int splits, hipStream_t stream);
+
+// Decode GEMV, m in 1..8, f32 activations.
+void launch_gemv_f32(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb,
+                     const float* x, uint64_t m, float* y, int splits, hipStream_t stream);
+
+// Prefill GEMM on MFMA: y[m][rows] = a16[m][K] . dequant(W)^T, f32 out.
+void launch_gemm(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb,
+                 const uint16_t* a16, uint64_t m, float* y, hipStream_t stream);
+
+// Grid-shape helper for the GEMV (waves per work-group).
+int gemv_default_splits(uint64_t rows, uint64_t nb);
+
+}  // namespace mq

@@ -1,0 +1,240 @@
+"""ctypes binding of the gfx950 packed-weight matmul library.
+
+``libmagnetar_gpu.so`` (C ABI in ``include/magnetar_gpu.h``) is the product:
+packed-weight upload, the int8-activation decode GEMV, the MFMA prefill
+GEMM and the bit-exact dequantizer. ``libmagnetar_gguf.so``
+(``include/magnetar_gguf.h``) holds host-side GGUF encoders and the seeded
+Gaussian generator. Loading fails loudly when a library is missing: there
+is no CPU fallback anywhere in this package.
+"""
+
+import ctypes
+import os
+
+import numpy as np
+
+PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+GPU_LIB = os.path.join(PKG_DIR, "libmagnetar_gpu.so")
+GGUF_LIB = os.path.join(PKG_DIR, "libmagnetar_gguf.so")
+EXECUTOR_LIB = os.path.join(PKG_DIR, "libmagnetar_executor.so")
+
+Q4_K = 12
+IQ4_XS = 23
+BLOCK_BYTES = {Q4_K: 144, IQ4_XS: 136}
+
+OK = 0
+ERR_SHAPE = 1
+ERR_DTYPE = 2
+DECLINED = 3
+ERR_HIP = 4
+ERR_OOM = 5
+ERR_ARGUMENT = 6
+INT8_ACTIVATIONS = 1
+
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+_f32p = ctypes.POINTER(ctypes.c_float)
+_i8p = ctypes.POINTER(ctypes.c_int8)
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_u64 = ctypes.c_uint64
+_vp = ctypes.c_void_p
+
+_gpu = None
+_gguf = None
+
+
+class GpuError(RuntimeError):
+    def __init__(self, code, reason):
+        super().__init__(f"[{code}] {reason}")
+        self.code = code
+        self.reason = reason
+
+
+class Declined(GpuError):
+    """PackedWeightWrite::Declined: the caller keeps the f32 path."""
+
+
+def _load(path):
+    if not os.path.exists(path):
+        raise ImportError(f"{path} is not built: run `make -C {PKG_DIR}` (or __graft_entry__.build())")
+    return ctypes.CDLL(path)
+
+
+def gpu_lib():
+    global _gpu
+    if _gpu is None:
+        L = _load(GPU_LIB)
+        L.mq_create.argtypes = [ctypes.c_int, ctypes.POINTER(_vp)]
+        L.mq_destroy.argtypes = [_vp]
+        L.mq_destroy.restype = None
+        L.mq_last_error.argtypes = [_vp]
+        L.mq_last_error.restype = ctypes.c_char_p
+        L.mq_version.restype = ctypes.c_char_p
+        L.mq_weight_upload.argtypes = [_vp, ctypes.c_uint32, _u64, _u64, ctypes.c_int, _u8p,
+                                       ctypes.c_size_t, ctypes.POINTER(_u64)]
+        L.mq_weight_release.argtypes = [_vp, _u64]
+        L.mq_weight_info.argtypes = [_vp, _u64, ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(_u64),
+                                     ctypes.POINTER(_u64), ctypes.POINTER(ctypes.c_int), ctypes.POINTER(_u64)]
+        L.mq_matmul.argtypes = [_vp, _u64, _f32p, _u64, _u64, ctypes.c_uint32, _f32p]
+        L.mq_matmul_dev.argtypes = [_vp, _u64, _vp, _u64, _u64, ctypes.c_uint32, _vp, _vp]
+        L.mq_quantize_activations_dev.argtypes = [_vp, _vp, _u64, _u64, _vp, _vp, _vp, _vp]
+        L.mq_matmul_prequantized_dev.argtypes = [_vp, _u64, _vp, _vp, _vp, _u64, _u64, _vp, _vp]
+        L.mq_prepare_activations_f16_dev.argtypes = [_vp, _vp, _u64, _u64, ctypes.c_uint32, _vp, _vp]
+        L.mq_matmul_f16_dev.argtypes = [_vp, _u64, _vp, _u64, _u64, _vp, _vp]
+        L.mq_dequantize.argtypes = [_vp, _u64, ctypes.c_int, _f32p]
+        L.mq_dequantize_dev.argtypes = [_vp, _u64, ctypes.c_int, _vp, _vp]
+        _gpu = L
+    return _gpu
+
+
+def gguf_lib():
+    global _gguf
+    if _gguf is None:
+        L = _load(GGUF_LIB)
+        L.gg_f32_to_f16.argtypes = [ctypes.c_float]
+        L.gg_f32_to_f16.restype = ctypes.c_uint16
+        L.gg_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.gg_f16_to_f32.restype = ctypes.c_float
+        L.gg_gaussian_f32.argtypes = [_u64, ctypes.c_float, _f32p, _u64]
+        L.gg_gaussian_f32.restype = None
+        L.gg_row_bytes.argtypes = [ctypes.c_uint32, _u64]
+        L.gg_row_bytes.restype = _u64
+        L.gg_quantize.argtypes = [ctypes.c_uint32, _f32p, _u64, _u64, _u8p]
+        _gguf = L
+    return _gguf
+
+
+def _p(a, ctype):
+    return a.ctypes.data_as(ctypes.POINTER(ctype))
+
+
+# ---- host GGUF helpers -----------------------------------------------------
+
+def gaussian(seed, sigma, n):
+    out = np.empty(n, np.float32)
+    gguf_lib().gg_gaussian_f32(seed, sigma, _p(out, ctypes.c_float), n)
+    return out
+
+
+def row_bytes(gguf_type, cols):
+    return int(gguf_lib().gg_row_bytes(gguf_type, cols))
+
+
+def quantize(gguf_type, w):
+    """Encodes f32 weights [rows, cols] into GGUF blocks (uint8 [rows, row_bytes])."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    rows, cols = w.shape
+    rb = row_bytes(gguf_type, cols)
+    if rb == 0:
+        raise ValueError(f"type {gguf_type} cannot encode {cols} columns")
+    out = np.empty((rows, rb), np.uint8)
+    if gguf_lib().gg_quantize(gguf_type, _p(w, ctypes.c_float), rows, cols, _p(out, ctypes.c_uint8)):
+        raise ValueError("gg_quantize failed")
+    return out
+
+
+# ---- device context --------------------------------------------------------
+
+class Weight:
+    def __init__(self, ctx, handle, gguf_type, rows, cols, transposed):
+        self.ctx = ctx
+        self.handle = handle
+        self.gguf_type = gguf_type
+        self.stored_rows = rows
+        self.stored_cols = cols
+        self.transposed = transposed
+
+    @property
+    def logical_shape(self):
+        return (self.stored_cols, self.stored_rows) if self.transposed else (self.stored_rows, self.stored_cols)
+
+    def release(self):
+        if self.handle:
+            self.ctx._check(gpu_lib().mq_weight_release(self.ctx.ptr, self.handle))
+            self.handle = 0
+
+
+class Context:
+    """One device context (mq_ctx): a stream, a workspace, uploaded weights."""
+
+    def __init__(self, device=0):
+        L = gpu_lib()
+        ptr = _vp()
+        rc = L.mq_create(device, ctypes.byref(ptr))
+        if rc:
+            raise GpuError(rc, L.mq_last_error(None).decode())
+        self.ptr = ptr
+
+    def close(self):
+        if self.ptr:
+            gpu_lib().mq_destroy(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def last_error(self):
+        return gpu_lib().mq_last_error(self.ptr).decode()
+
+    def _check(self, rc):
+        if rc == DECLINED:
+            raise Declined(rc, self.last_error())
+        if rc:
+            raise GpuError(rc, self.last_error())
+
+    def upload(self, gguf_type, rows, cols, data, transposed=True):
+        b = np.ascontiguousarray(data, dtype=np.uint8).reshape(-1)
+        h = _u64()
+        self._check(gpu_lib().mq_weight_upload(self.ptr, gguf_type, rows, cols, int(transposed),
+                                               _p(b, ctypes.c_uint8), b.size, ctypes.byref(h)))
+        return Weight(self, h.value, gguf_type, rows, cols, transposed)
+
+    def info(self, weight):
+        t = ctypes.c_uint32()
+        r, c, nbytes = _u64(), _u64(), _u64()
+        tr = ctypes.c_int()
+        self._check(gpu_lib().mq_weight_info(self.ptr, weight.handle, ctypes.byref(t), ctypes.byref(r),
+                                             ctypes.byref(c), ctypes.byref(tr), ctypes.byref(nbytes)))
+        return {"type": t.value, "stored_rows": r.value, "stored_cols": c.value,
+                "transposed": tr.value, "device_bytes": nbytes.value}
+
+    def matmul(self, weight, x, int8=True):
+        """y = x . W^T on host arrays (synchronous)."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        if x.ndim != 2:
+            raise ValueError("x must be [m, k]")
+        m, k = x.shape
+        y = np.empty((m, weight.stored_rows), np.float32)
+        self._check(gpu_lib().mq_matmul(self.ptr, weight.handle, _p(x, ctypes.c_float), m, k,
+                                        INT8_ACTIVATIONS if int8 else 0, _p(y, ctypes.c_float)))
+        return y
+
+    def matmul_dev(self, weight, x_ptr, m, k, y_ptr, int8=True, stream=None):
+        self._check(gpu_lib().mq_matmul_dev(self.ptr, weight.handle, x_ptr, m, k,
+                                            INT8_ACTIVATIONS if int8 else 0, y_ptr, stream))
+
+    def quantize_activations_dev(self, x_ptr, m, k, values_ptr, scales_ptr, sums_ptr, stream=None):
+        self._check(gpu_lib().mq_quantize_activations_dev(self.ptr, x_ptr, m, k, values_ptr, scales_ptr,
+                                                          sums_ptr, stream))
+
+    def matmul_prequantized_dev(self, weight, values_ptr, scales_ptr, sums_ptr, m, k, y_ptr, stream=None):
+        self._check(gpu_lib().mq_matmul_prequantized_dev(self.ptr, weight.handle, values_ptr, scales_ptr,
+                                                         sums_ptr, m, k, y_ptr, stream))
+
+    def prepare_activations_f16_dev(self, x_ptr, m, k, a16_ptr, int8=True, stream=None):
+        self._check(gpu_lib().mq_prepare_activations_f16_dev(self.ptr, x_ptr, m, k,
+                                                             INT8_ACTIVATIONS if int8 else 0, a16_ptr, stream))
+
+    def matmul_f16_dev(self, weight, a16_ptr, m, k, y_ptr, stream=None):
+        self._check(gpu_lib().mq_matmul_f16_dev(self.ptr, weight.handle, a16_ptr, m, k, y_ptr, stream))
+
+    def dequantize(self, weight, logical=False):
+        shape = weight.logical_shape if logical else (weight.stored_rows, weight.stored_cols)
+        out = np.empty(shape, np.float32)
+        self._check(gpu_lib().mq_dequantize(self.ptr, weight.handle, int(logical), _p(out, ctypes.c_float)))
+        return out
+
+    def dequantize_dev(self, weight, out_ptr, logical=False, stream=None):
+        self._check(gpu_lib().mq_dequantize_dev(self.ptr, weight.handle, int(logical), out_ptr, stream))

@@ -1,0 +1,182 @@
+"""CPU oracle for the GGUF block-quantized matmul path.
+
+TEST INFRASTRUCTURE ONLY. This package is the checker: ``tests/``,
+``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline leg use it. The
+product library (``magnetar-provider-cpu_amd``) never imports it.
+
+``liboracle.so`` (built from ``oracle.c`` and ``cpu_baseline.c`` by the
+Makefile here) restates, in C, the reference's
+ - packed decode (src/native/quant.rs:46-57, 96-121, 196-206, 284-338),
+ - dequantization (quant.rs:1702-1711),
+ - int8 activation quantizer and scalar dot (quant.rs:340-388),
+ - scalar int8 / f32 column kernel (quant.rs:559-597),
+ - dense f32 matmul (src/lib.rs:262-318),
+ - and, as the timed CPU baseline, the AVX2 Q4_K / IQ4_XS column kernels
+   with the column chunking and worker pool (quant.rs:666-744, 956-984,
+   1364-1433; src/native/mod.rs:110-152; src/native/pool.rs:58-155).
+"""
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+Q4_K = 12
+IQ4_XS = 23
+BLOCK_BYTES = {Q4_K: 144, IQ4_XS: 136}
+
+_lib = None
+
+
+def build():
+    """Compiles liboracle.so with the Makefile beside this file."""
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        u8p = ctypes.POINTER(ctypes.c_uint8)
+        f32p = ctypes.POINTER(ctypes.c_float)
+        i8p = ctypes.POINTER(ctypes.c_int8)
+        i32p = ctypes.POINTER(ctypes.c_int32)
+        u64 = ctypes.c_uint64
+        L.or_f16_to_f32.restype = ctypes.c_float
+        L.or_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.or_scale_min_k4.argtypes = [ctypes.c_int, u8p, u8p, u8p]
+        L.or_iq4_xs_scales.argtypes = [u8p, i8p]
+        L.or_decode_run.argtypes = [ctypes.c_int, u8p, ctypes.c_int, i8p, f32p, f32p]
+        L.or_dequantize_rows.argtypes = [ctypes.c_int, u8p, u64, u64, f32p]
+        L.or_quantize_rows.argtypes = [f32p, u64, i8p, f32p, i32p]
+        L.or_int8_rounded.argtypes = [f32p, u64, f32p]
+        L.or_dot_halves.argtypes = [i8p, i8p, i32p]
+        L.or_columns_scalar.argtypes = [ctypes.c_int, u8p, u64, u64, f32p, u64,
+                                        ctypes.c_int, u64, u64, f32p]
+        L.or_matmul_dense.argtypes = [f32p, u64, u64, f32p, u64, u64,
+                                      ctypes.c_int, ctypes.c_int, f32p]
+        L.bl_half_f16c.restype = ctypes.c_float
+        L.bl_half_f16c.argtypes = [ctypes.c_uint16]
+        L.bl_packed_matmul.argtypes = [ctypes.c_int, u8p, u64, u64, f32p, u64,
+                                       ctypes.c_int, f32p]
+        _lib = L
+    return _lib
+
+
+def _p(a, ctype):
+    return a.ctypes.data_as(ctypes.POINTER(ctype))
+
+
+def f16_to_f32(bits):
+    return lib().or_f16_to_f32(int(bits))
+
+
+def half_f16c(bits):
+    return lib().bl_half_f16c(int(bits))
+
+
+def scale_min_k4(j, twelve):
+    q = np.ascontiguousarray(twelve, dtype=np.uint8)
+    sc = np.zeros(1, np.uint8)
+    m = np.zeros(1, np.uint8)
+    lib().or_scale_min_k4(j, _p(q, ctypes.c_uint8), _p(sc, ctypes.c_uint8), _p(m, ctypes.c_uint8))
+    return int(sc[0]), int(m[0])
+
+
+def iq4_xs_scales(six):
+    b = np.ascontiguousarray(six, dtype=np.uint8)
+    out = np.zeros(8, np.int8)
+    lib().or_iq4_xs_scales(_p(b, ctypes.c_uint8), _p(out, ctypes.c_int8))
+    return out
+
+
+def decode_run(fmt, block, run):
+    b = np.ascontiguousarray(block, dtype=np.uint8)
+    q = np.zeros(32, np.int8)
+    scale = np.zeros(2, np.float32)
+    mn = np.zeros(2, np.float32)
+    lib().or_decode_run(fmt, _p(b, ctypes.c_uint8), run, _p(q, ctypes.c_int8),
+                        _p(scale, ctypes.c_float), _p(mn, ctypes.c_float))
+    return q, scale, mn
+
+
+def dequantize(fmt, data, rows, cols):
+    """Stored rows x cols f32 (the stored layout, `dequantize_stored`)."""
+    b = np.ascontiguousarray(data, dtype=np.uint8)
+    out = np.empty((rows, cols), np.float32)
+    rc = lib().or_dequantize_rows(fmt, _p(b, ctypes.c_uint8), rows, cols, _p(out, ctypes.c_float))
+    if rc:
+        raise ValueError("oracle dequantize: unsupported format or shape")
+    return out
+
+
+def quantize_rows(x):
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    n = x.size
+    values = np.empty(n, np.int8)
+    scales = np.empty(n // 32, np.float32)
+    sums = np.empty((n // 32, 2), np.int32)
+    lib().or_quantize_rows(_p(x, ctypes.c_float), n, _p(values, ctypes.c_int8),
+                           _p(scales, ctypes.c_float), _p(sums, ctypes.c_int32))
+    return values, scales, sums
+
+
+def int8_rounded(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    lib().or_int8_rounded(_p(x, ctypes.c_float), x.size, _p(out, ctypes.c_float))
+    return out
+
+
+def dot_halves(q, a):
+    q = np.ascontiguousarray(q, dtype=np.int8)
+    a = np.ascontiguousarray(a, dtype=np.int8)
+    out = np.zeros(2, np.int32)
+    lib().or_dot_halves(_p(q, ctypes.c_int8), _p(a, ctypes.c_int8), _p(out, ctypes.c_int32))
+    return out
+
+
+def columns_scalar(fmt, data, n, k, x, int8, first=0, count=None):
+    """The scalar column kernel over columns first..first+count: [m, count]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    m = x.shape[0]
+    count = n - first if count is None else count
+    b = np.ascontiguousarray(data, dtype=np.uint8)
+    out = np.empty((m, count), np.float32)
+    rc = lib().or_columns_scalar(fmt, _p(b, ctypes.c_uint8), n, k, _p(x, ctypes.c_float), m,
+                                 1 if int8 else 0, first, count, _p(out, ctypes.c_float))
+    if rc:
+        raise ValueError("oracle columns: bad arguments")
+    return out
+
+
+def matmul_dense(a, b, transpose_a=False, transpose_b=False):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    m = a.shape[1] if transpose_a else a.shape[0]
+    n = b.shape[0] if transpose_b else b.shape[1]
+    out = np.empty((m, n), np.float32)
+    rc = lib().or_matmul_dense(_p(a, ctypes.c_float), a.shape[0], a.shape[1],
+                               _p(b, ctypes.c_float), b.shape[0], b.shape[1],
+                               int(transpose_a), int(transpose_b), _p(out, ctypes.c_float))
+    if rc:
+        raise ValueError("matmul inner dimension mismatch")
+    return out
+
+
+def baseline_packed_matmul(fmt, data, n, k, x, threads):
+    """The AVX2 CPU path with `threads` pool threads: [m, n]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    b = np.ascontiguousarray(data, dtype=np.uint8)
+    out = np.empty((x.shape[0], n), np.float32)
+    rc = lib().bl_packed_matmul(fmt, _p(b, ctypes.c_uint8), n, k, _p(x, ctypes.c_float),
+                                x.shape[0], threads, _p(out, ctypes.c_float))
+    if rc:
+        raise RuntimeError(f"baseline packed matmul failed ({rc})")
+    return out

@@ -1,0 +1,280 @@
+/*
+ * CPU oracle: a plain-C restatement of the reference's packed-weight
+ * decode, int8 activation quantizer, scalar column kernel and dense f32
+ * matmul. TEST INFRASTRUCTURE ONLY (see oracle.h).
+ *
+ * Build with -O2 -ffp-contract=off and without -ffast-math: every
+ * product and sum below is one IEEE f32 operation, in the reference's
+ * order.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* The external `f16_to_f32` (magnetar-provider-api 1.0.0, not vendored;
+ * used at src/native/quant.rs:34 and through F16C at quant.rs:1494-1502):
+ * IEEE binary16 -> binary32, exact for every pattern. */
+float or_f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h >> 15) << 31;
+    uint32_t exp = (h >> 10) & 0x1F;
+    uint32_t mant = h & 0x3FF;
+    uint32_t bits;
+    if (exp == 0) {
+        if (mant == 0) {
+            bits = sign;
+        } else {
+            /* subnormal: mant * 2^-24, renormalised */
+            int e = -1;
+            do {
+                mant <<= 1;
+                e++;
+            } while ((mant & 0x400) == 0);
+            mant &= 0x3FF;
+            bits = sign | ((uint32_t)(127 - 15 - e) << 23) | (mant << 13);
+        }
+    } else if (exp == 31) {
+        /* inf, or NaN with its payload kept and the quiet bit set as F16C does */
+        bits = sign | 0x7F800000u | (mant << 13) | (mant ? 0x00400000u : 0);
+    } else {
+        bits = sign | ((exp - 15 + 127) << 23) | (mant << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+/* Block geometry (PackedWeightFormat::{block_bytes, block_elements},
+ * external; values fixed by the GGUF layouts decoded at quant.rs:110-121
+ * and 196-206). */
+int or_block_bytes(int fmt) {
+    return fmt == OR_Q4_K ? 144 : fmt == OR_IQ4_XS ? 136 : 0;
+}
+
+int or_block_elements(int fmt) {
+    return (fmt == OR_Q4_K || fmt == OR_IQ4_XS) ? 256 : 0;
+}
+
+/* src/native/quant.rs:46-57 (`scale_min_k4`). */
+void or_scale_min_k4(int j, const uint8_t *q, uint8_t *sc, uint8_t *m) {
+    if (j < 4) {
+        *sc = q[j] & 63;
+        *m = q[j + 4] & 63;
+    } else {
+        *sc = (uint8_t)((q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4));
+        *m = (uint8_t)((q[j + 4] >> 4) | ((q[j] >> 6) << 4));
+    }
+}
+
+/* The external `iq4_xs_scales` (called at quant.rs:198, 1411): the GGUF
+ * IQ4_XS layout, scales_h (u16 LE) then scales_l[4]; run j's 6-bit
+ * scale is low nibble j of scales_l plus bits 2j..2j+1 of scales_h, less
+ * 32. Parity unpinned by the reference tree (the crate is not vendored). */
+void or_iq4_xs_scales(const uint8_t *six, int8_t out[8]) {
+    uint32_t h = (uint32_t)six[0] | ((uint32_t)six[1] << 8);
+    for (int j = 0; j < 8; j++) {
+        int low = (six[2 + j / 2] >> (4 * (j % 2))) & 0xF;
+        int high = (h >> (2 * j)) & 3;
+        out[j] = (int8_t)((low | (high << 4)) - 32);
+    }
+}
+
+/* The external `IQ4_NL_VALUES` (quant.rs:185, 201-202): the GGUF
+ * kvalues_iq4nl codebook. Parity unpinned by the reference tree. */
+static const int8_t IQ4NL[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
+                                 1,    13,   25,  38,  53,  69,  89,  113};
+
+const int8_t *or_iq4nl_values(void) { return IQ4NL; }
+
+/* src/native/quant.rs:96-121 (Q4K arm) and 196-206 (Iq4Xs arm). */
+void or_decode_run(int fmt, const uint8_t *block, int run, int8_t q[OR_RUN],
+                   float scale[2], float min[2]) {
+    if (fmt == OR_Q4_K) {
+        float d = or_f16_to_f32((uint16_t)(block[0] | (block[1] << 8)));
+        float dmin = or_f16_to_f32((uint16_t)(block[2] | (block[3] << 8)));
+        uint8_t sc, m;
+        or_scale_min_k4(run, block + 4, &sc, &m);
+        int chunk = run / 2;
+        int shift = 4 * (run % 2);
+        const uint8_t *qs = block + 16 + 32 * chunk;
+        for (int i = 0; i < OR_RUN; i++) q[i] = (int8_t)((qs[i] >> shift) & 0xF);
+        float s = d * (float)sc;
+        float mn = dmin * (float)m;
+        scale[0] = scale[1] = s;
+        min[0] = min[1] = mn;
+    } else {
+        float d = or_f16_to_f32((uint16_t)(block[0] | (block[1] << 8)));
+        int8_t ls[8];
+        or_iq4_xs_scales(block + 2, ls);
+        float s = d * (float)ls[run];
+        for (int l = 0; l < 16; l++) {
+            uint8_t byte = block[8 + 16 * run + l];
+            q[l] = IQ4NL[byte & 0xF];
+            q[l + 16] = IQ4NL[byte >> 4];
+        }
+        scale[0] = scale[1] = s;
+        min[0] = min[1] = 0.0f;
+    }
+}
+
+/* RunReader addressing (quant.rs:284-338) and `dequantize_row`
+ * (quant.rs:1702-1711): value = scale[p] * q - min[p], p = i / 16. */
+int or_dequantize_rows(int fmt, const uint8_t *bytes, uint64_t rows,
+                       uint64_t cols, float *out) {
+    int bb = or_block_bytes(fmt);
+    if (!bb || cols % 256) return -1;
+    uint64_t row_bytes = cols / 256 * (uint64_t)bb;
+    int8_t q[OR_RUN];
+    float scale[2], min[2];
+    for (uint64_t r = 0; r < rows; r++) {
+        for (uint64_t u = 0; u < cols / OR_RUN; u++) {
+            const uint8_t *block = bytes + r * row_bytes + (u / 8) * bb;
+            or_decode_run(fmt, block, (int)(u % 8), q, scale, min);
+            float *o = out + r * cols + u * OR_RUN;
+            for (int i = 0; i < OR_RUN; i++) {
+                int p = i / 16;
+                float v = scale[p] * (float)q[i];
+                o[i] = v - min[p];
+            }
+        }
+    }
+    return 0;
+}
+
+/* Rust `f32 as i8`: saturating, NaN -> 0. */
+static int8_t sat_i8(float v) {
+    if (isnan(v)) return 0;
+    if (v >= 127.0f) return 127;
+    if (v <= -128.0f) return -128;
+    return (int8_t)v;
+}
+
+/* `quantize_rows` (quant.rs:350-378): per 32-value block,
+ * amax = fold(0, f32::max(|x|)) (f32::max ignores NaN, as fmaxf does),
+ * d = amax / 127 (true division), q = round_ties_even(x / d) as i8
+ * (0 when amax == 0), sums of each 16-value half. */
+void or_quantize_rows(const float *x, uint64_t n, int8_t *values,
+                      float *scales, int32_t *sums) {
+    for (uint64_t b = 0; b < n / OR_RUN; b++) {
+        const float *blk = x + b * OR_RUN;
+        float amax = 0.0f;
+        for (int i = 0; i < OR_RUN; i++) amax = fmaxf(amax, fabsf(blk[i]));
+        float d = amax / 127.0f;
+        int32_t s[2] = {0, 0};
+        for (int i = 0; i < OR_RUN; i++) {
+            int8_t q = 0;
+            if (amax != 0.0f) q = sat_i8(nearbyintf(blk[i] / d));
+            values[b * OR_RUN + i] = q;
+            s[i / 16] += q;
+        }
+        scales[b] = d;
+        sums[2 * b] = s[0];
+        sums[2 * b + 1] = s[1];
+    }
+}
+
+/* `int8_rounded` (src/native/tests.rs:77-89): the activations as int8
+ * activations see them, f32::from(q) * d. */
+void or_int8_rounded(const float *x, uint64_t n, float *out) {
+    for (uint64_t b = 0; b < n / OR_RUN; b++) {
+        int8_t v[OR_RUN];
+        float d;
+        int32_t s[2];
+        or_quantize_rows(x + b * OR_RUN, OR_RUN, v, &d, s);
+        for (int i = 0; i < OR_RUN; i++) out[b * OR_RUN + i] = (float)v[i] * d;
+    }
+}
+
+/* `dot_halves_scalar` (quant.rs:380-388). */
+void or_dot_halves(const int8_t *q, const int8_t *a, int32_t out[2]) {
+    out[0] = out[1] = 0;
+    for (int i = 0; i < OR_RUN; i++) out[i / 16] += (int32_t)q[i] * (int32_t)a[i];
+}
+
+/* The scalar int8 / f32 column loop of `columns::<F>`
+ * (quant.rs:559-597). */
+int or_columns_scalar(int fmt, const uint8_t *bytes, uint64_t n, uint64_t k,
+                      const float *x, uint64_t m, int int8,
+                      uint64_t first, uint64_t count, float *out) {
+    int bb = or_block_bytes(fmt);
+    if (!bb || k % 256 || first + count > n) return -1;
+    uint64_t runs = k / OR_RUN;
+    uint64_t row_bytes = k / 256 * (uint64_t)bb;
+    int8_t *qv = 0;
+    float *qs = 0;
+    int32_t *qsum = 0;
+    if (int8) {
+        qv = (int8_t *)malloc(m * k);
+        qs = (float *)malloc(m * runs * sizeof(float));
+        qsum = (int32_t *)malloc(m * runs * 2 * sizeof(int32_t));
+        if (!qv || !qs || !qsum) {
+            free(qv); free(qs); free(qsum);
+            return -2;
+        }
+        or_quantize_rows(x, m * k, qv, qs, qsum);
+    }
+    float *acc = (float *)calloc(m ? m : 1, sizeof(float));
+    int8_t q[OR_RUN];
+    float scale[2], min[2];
+    for (uint64_t c = 0; c < count; c++) {
+        for (uint64_t r = 0; r < m; r++) acc[r] = 0.0f;
+        for (uint64_t u = 0; u < runs; u++) {
+            const uint8_t *block = bytes + (first + c) * row_bytes + (u / 8) * bb;
+            or_decode_run(fmt, block, (int)(u % 8), q, scale, min);
+            for (uint64_t r = 0; r < m; r++) {
+                uint64_t blk = r * runs + u;
+                if (int8) {
+                    int32_t dots[2];
+                    or_dot_halves(q, qv + blk * OR_RUN, dots);
+                    float d = qs[blk];
+                    float t = scale[0] * (float)dots[0];
+                    t = t + scale[1] * (float)dots[1];
+                    t = t - min[0] * (float)qsum[2 * blk];
+                    t = t - min[1] * (float)qsum[2 * blk + 1];
+                    acc[r] += d * t;
+                } else {
+                    const float *xa = x + blk * OR_RUN;
+                    for (int i = 0; i < OR_RUN; i++) {
+                        int p = i / 16;
+                        float w = scale[p] * (float)q[i];
+                        w = w - min[p];
+                        acc[r] += w * xa[i];
+                    }
+                }
+            }
+        }
+        for (uint64_t r = 0; r < m; r++) out[r * count + c] = acc[r];
+    }
+    free(acc);
+    free(qv);
+    free(qs);
+    free(qsum);
+    return 0;
+}
+
+/* Dense `matmul` (src/lib.rs:262-318): row -> inner -> col, f32, no
+ * zero-skip, transposes by stride swap. */
+int or_matmul_dense(const float *a, uint64_t a_rows, uint64_t a_cols,
+                    const float *b, uint64_t b_rows, uint64_t b_cols,
+                    int transpose_a, int transpose_b, float *out) {
+    uint64_t m = transpose_a ? a_cols : a_rows;
+    uint64_t k = transpose_a ? a_rows : a_cols;
+    uint64_t k2 = transpose_b ? b_cols : b_rows;
+    uint64_t n = transpose_b ? b_rows : b_cols;
+    if (k != k2) return -1;
+    uint64_t a_row_stride = transpose_a ? 1 : a_cols;
+    uint64_t a_inner_stride = transpose_a ? a_cols : 1;
+    uint64_t b_inner_stride = transpose_b ? 1 : b_cols;
+    uint64_t b_col_stride = transpose_b ? b_cols : 1;
+    memset(out, 0, m * n * sizeof(float));
+    for (uint64_t row = 0; row < m; row++) {
+        float *o = out + row * n;
+        for (uint64_t inner = 0; inner < k; inner++) {
+            float av = a[row * a_row_stride + inner * a_inner_stride];
+            uint64_t base = inner * b_inner_stride;
+            for (uint64_t col = 0; col < n; col++) o[col] += av * b[base + col * b_col_stride];
+        }
+    }
+    return 0;
+}

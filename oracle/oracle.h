@@ -1,0 +1,73 @@
+/*
+ * CPU oracle for the GGUF block-quantized matmul path (Q4_K, IQ4_XS).
+ *
+ * TEST INFRASTRUCTURE ONLY. This library is the checker: tests, the
+ * smoke check and bench.py's CPU-baseline leg load it; the product
+ * library never links or calls it.
+ *
+ * Every function restates the reference's Rust algorithm in plain C and
+ * cites the file:line it follows (paths relative to the reference repo
+ * root). Compiled with -ffp-contract=off: the reference never contracts a
+ * multiply and an add into an FMA unless it calls an explicit fmadd.
+ */
+#ifndef MAGNETAR_ORACLE_H
+#define MAGNETAR_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ggml type ids (public GGUF spec) */
+#define OR_Q4_K 12
+#define OR_IQ4_XS 23
+
+/* Values per run (src/native/quant.rs:18-19). */
+#define OR_RUN 32
+
+float or_f16_to_f32(uint16_t bits);
+int or_block_bytes(int fmt);
+int or_block_elements(int fmt);
+void or_scale_min_k4(int j, const uint8_t *q, uint8_t *sc, uint8_t *m);
+void or_iq4_xs_scales(const uint8_t *six, int8_t out[8]);
+const int8_t *or_iq4nl_values(void);
+
+/* Run `run` of one block: 32 signed values, per-half scale and min. */
+void or_decode_run(int fmt, const uint8_t *block, int run, int8_t q[OR_RUN],
+                   float scale[2], float min[2]);
+
+/* Stored rows of a packed weight dequantized to f32, stored layout. */
+int or_dequantize_rows(int fmt, const uint8_t *bytes, uint64_t rows,
+                       uint64_t cols, float *out);
+
+/* Activation int8 quantization per 32-value block. */
+void or_quantize_rows(const float *x, uint64_t n, int8_t *values,
+                      float *scales, int32_t *sums);
+void or_int8_rounded(const float *x, uint64_t n, float *out);
+void or_dot_halves(const int8_t *q, const int8_t *a, int32_t out[2]);
+
+/* The scalar column kernel: out[r*count + c] for columns first..first+count
+ * of a x W (W stored output-major: n stored rows of k). */
+int or_columns_scalar(int fmt, const uint8_t *bytes, uint64_t n, uint64_t k,
+                      const float *x, uint64_t m, int int8,
+                      uint64_t first, uint64_t count, float *out);
+
+/* The dense f32 matmul oracle; returns 0 or -1 on an inner-size mismatch. */
+int or_matmul_dense(const float *a, uint64_t a_rows, uint64_t a_cols,
+                    const float *b, uint64_t b_rows, uint64_t b_cols,
+                    int transpose_a, int transpose_b, float *out);
+
+/* CPU baseline: the reference's default AVX2 path (int8 activations,
+ * Q4_K / IQ4_XS specialised column kernels) across a persistent pool of
+ * `threads` threads, caller participating. out is m x n. */
+int bl_packed_matmul(int fmt, const uint8_t *bytes, uint64_t n, uint64_t k,
+                     const float *x, uint64_t m, int threads, float *out);
+int bl_has_avx2(void);
+float bl_half_f16c(uint16_t bits);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,78 @@
+"""Test data generators restating the reference's own test helpers
+(src/native/tests.rs:24-103) plus tolerance checks."""
+
+import numpy as np
+
+Q4_K = 12
+IQ4_XS = 23
+BLOCK_BYTES = {Q4_K: 144, IQ4_XS: 136}
+
+
+class Rng:
+    """xorshift32 (src/native/tests.rs:34-43)."""
+
+    def __init__(self, state):
+        self.state = state & 0xFFFFFFFF
+
+    def next(self):
+        x = self.state
+        x ^= (x << 13) & 0xFFFFFFFF
+        x ^= x >> 17
+        x ^= (x << 5) & 0xFFFFFFFF
+        self.state = x
+        return x
+
+
+def half_offsets(fmt):
+    """Byte offsets of each block's f16 scale fields (src/native/tests.rs:24-32)."""
+    return [0, 2] if fmt == Q4_K else [0]
+
+
+def packed(fmt, rows, cols, seed):
+    """A random packed matrix: random bytes, small positive f16 scales with
+    exponent 3..7 (src/native/tests.rs:45-67). uint8 [rows, row_bytes]."""
+    rng = Rng((seed * 2654435761 + 1) & 0xFFFFFFFF)
+    bb = BLOCK_BYTES[fmt]
+    blocks = rows * cols // 256
+    out = np.empty(blocks * bb, np.uint8)
+    for i in range(blocks):
+        blk = [rng.next() % 256 for _ in range(bb)]
+        for at in half_offsets(fmt):
+            exponent = 3 + rng.next() % 5
+            bits = (exponent << 10) | (rng.next() % 1024)
+            blk[at] = bits & 0xFF
+            blk[at + 1] = bits >> 8
+        out[i * bb:(i + 1) * bb] = blk
+    return out.reshape(rows, cols // 256 * bb)
+
+
+def activations(rows, cols, seed):
+    """Uniform in [-1, 1] in 0.001 steps (src/native/tests.rs:69-75)."""
+    rng = Rng(seed + 7)
+    v = np.array([rng.next() % 2001 for _ in range(rows * cols)], dtype=np.float32)
+    return (v / np.float32(1000.0) - np.float32(1.0)).astype(np.float32).reshape(rows, cols)
+
+
+def assert_close_reference(actual, expected, what=""):
+    """`assert_close` (src/native/tests.rs:91-103): |a - e| <= 2e-5 max(1, max|e|)."""
+    scale = max(1.0, float(np.max(np.abs(expected)))) if expected.size else 1.0
+    err = np.abs(actual.astype(np.float64) - expected.astype(np.float64))
+    assert err.max(initial=0.0) <= 2e-5 * scale, f"{what}: max err {err.max()} vs {2e-5 * scale}"
+
+
+def row_tolerance_violation(actual, expected):
+    """Largest max|d| / (1e-3 ||row||_inf) over rows: <= 1 passes the
+    stated output tolerance (max |d| <= 1e-3 ||row||_inf, f32 accumulate)."""
+    a = actual.astype(np.float64)
+    e = expected.astype(np.float64)
+    norm = np.max(np.abs(e), axis=1)
+    err = np.max(np.abs(a - e), axis=1)
+    ratio = err / np.maximum(1e-3 * norm, 1e-30)
+    return float(ratio.max(initial=0.0))
+
+
+def assert_row_tolerance(actual, expected, what=""):
+    assert actual.shape == expected.shape, f"{what}: shape {actual.shape} vs {expected.shape}"
+    assert np.isfinite(actual).all() == np.isfinite(expected).all(), f"{what}: non-finite mismatch"
+    r = row_tolerance_violation(actual, expected)
+    assert r <= 1.0, f"{what}: max|d| is {r:.3f} x the 1e-3 ||row||_inf tolerance"

@@ -1,0 +1,338 @@
+"""GPU parity: the gfx950 path through the C ABI against the oracle.
+
+Bars: dequantization and int8 activation quantization bit-exact; matmul
+outputs within max|d| <= 1e-3 ||row||_inf of the mode-matched dense
+oracle (int8 mode: matmul(int8_rounded(x), dequantize(W)); f32 mode:
+matmul(x, dequantize(W))), f32 accumulate. The decode GEMV (m <= 8) also
+meets the reference's own 2e-5 max(1, max|e|) tolerance."""
+
+import numpy as np
+import pytest
+
+import magnetar_gpu as mg
+import oracle
+from helpers import (IQ4_XS, Q4_K, activations, assert_close_reference, assert_row_tolerance, packed,
+                     row_tolerance_violation)
+from magnetar_gpu import workloads
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda")
+
+
+def expected(fmt, w, n, k, x, int8, rows=None):
+    """Dense oracle on the (optionally row-sampled) activations."""
+    dense_t = oracle.dequantize(fmt, w, n, k)
+    xs = x if rows is None else x[rows]
+    a = oracle.int8_rounded(xs) if int8 else xs
+    return oracle.matmul_dense(a, dense_t, False, True)
+
+
+# ---- dequantization ------------------------------------------------------------
+
+@pytest.mark.parametrize("fmt", [Q4_K, IQ4_XS])
+@pytest.mark.parametrize("rows,cols,gen", [(3, 512, "packed"), (37, 512, "packed"), (8, 4096, "gauss"),
+                                           (1, 256, "packed"), (65, 1024, "gauss")])
+def test_dequantize_bit_exact(ctx, fmt, rows, cols, gen):
+    if gen == "packed":
+        w = packed(fmt, rows, cols, 11 + rows)
+    else:
+        w = mg.quantize(fmt, mg.gaussian(rows, 0.02, rows * cols).reshape(rows, cols))
+    exp = oracle.dequantize(fmt, w, rows, cols)
+    h = ctx.upload(fmt, rows, cols, w)
+    try:
+        got = ctx.dequantize(h)
+        np.testing.assert_array_equal(got.view(np.uint32), exp.view(np.uint32))
+        got_l = ctx.dequantize(h, logical=True)
+        assert got_l.shape == (cols, rows)
+        np.testing.assert_array_equal(got_l.view(np.uint32), np.ascontiguousarray(exp.T).view(np.uint32))
+    finally:
+        h.release()
+
+
+def test_dequantize_full_size_bit_exact(ctx):
+    name = "q4k_14336x4096_s1"
+    fmt, n, k, _, _ = workloads.WEIGHTS[name]
+    w = workloads.weight_bytes(name)
+    h = ctx.upload(fmt, n, k, w)
+    try:
+        got = ctx.dequantize(h)
+        exp = oracle.dequantize(fmt, w, n, k)
+        np.testing.assert_array_equal(got.view(np.uint32), exp.view(np.uint32))
+    finally:
+        h.release()
+
+
+# ---- activation quantization -----------------------------------------------------
+
+def _special_blocks():
+    b = []
+    b.append(np.zeros(32, np.float32))
+    t = np.zeros(32, np.float32); t[0] = 127; t[1] = 2.5; t[2] = 3.5; t[3] = -2.5; t[4] = 0.5; t[5] = -0.5
+    b.append(t)
+    t = np.ones(32, np.float32); t[5] = np.nan; b.append(t)
+    t = np.ones(32, np.float32); t[7] = np.inf; t[8] = -np.inf; b.append(t)
+    b.append(np.full(32, np.nan, np.float32))
+    b.append(np.full(32, -0.0, np.float32))
+    b.append(np.full(32, 1e-42, np.float32))
+    t = np.linspace(-3e38, 3e38, 32).astype(np.float32); b.append(t)
+    return np.concatenate(b)
+
+
+@pytest.mark.parametrize("m,k", [(1, 256), (3, 512), (9, 4096), (1, 14336), (512, 4096)])
+def test_quantize_activations_bit_exact(ctx, m, k):
+    rng = np.random.default_rng(m * 7 + k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    if m * k >= 256:
+        s = _special_blocks()
+        x.reshape(-1)[:s.size] = s
+    ev, es, eh = oracle.quantize_rows(x)
+    xd = dev(x)
+    v = torch.empty(m * k, dtype=torch.int8, device="cuda")
+    sc = torch.empty(m * k // 32, dtype=torch.float32, device="cuda")
+    sm = torch.empty(m * k // 32 * 2, dtype=torch.int32, device="cuda")
+    ctx.quantize_activations_dev(xd.data_ptr(), m, k, v.data_ptr(), sc.data_ptr(), sm.data_ptr(),
+                                 torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(v.cpu().numpy(), ev)
+    np.testing.assert_array_equal(sc.cpu().numpy().view(np.uint32), es.view(np.uint32))
+    np.testing.assert_array_equal(sm.cpu().numpy().reshape(-1, 2), eh)
+
+
+# ---- matmul at the reference's own test shapes --------------------------------
+
+@pytest.mark.parametrize("fmt", [Q4_K, IQ4_XS])
+@pytest.mark.parametrize("int8", [True, False])
+@pytest.mark.parametrize("m", [1, 3, 9])
+def test_packed_matmul_matches_reference_cpu(ctx, fmt, int8, m):
+    """`packed_matmuls_match_the_reference_cpu` (src/native/tests.rs:134-154):
+    K = 512, N = 37 (not a multiple of the 8-row group), M in {1, 3, 9}."""
+    k, n = 512, 37
+    w = packed(fmt, n, k, 21)
+    a = activations(m, k, m)
+    h = ctx.upload(fmt, n, k, w)
+    try:
+        got = ctx.matmul(h, a, int8=int8)
+    finally:
+        h.release()
+    exp = expected(fmt, w, n, k, a, int8)
+    assert_row_tolerance(got, exp, f"fmt {fmt} int8 {int8} m {m}")
+    if m <= 8:
+        assert_close_reference(got, exp, f"fmt {fmt} int8 {int8} m {m}")
+
+
+@pytest.mark.parametrize("fmt", [Q4_K, IQ4_XS])
+@pytest.mark.parametrize("int8", [True, False])
+def test_gemv_every_row_count(ctx, fmt, int8):
+    n, k = 1000, 2048
+    w = mg.quantize(fmt, mg.gaussian(77, 0.02, n * k).reshape(n, k))
+    h = ctx.upload(fmt, n, k, w)
+    try:
+        for m in range(1, 9):
+            a = mg.gaussian(100 + m, 1.0, m * k).reshape(m, k)
+            got = ctx.matmul(h, a, int8=int8)
+            exp = expected(fmt, w, n, k, a, int8)
+            assert_row_tolerance(got, exp, f"m {m}")
+            assert_close_reference(got, exp, f"m {m}")
+    finally:
+        h.release()
+
+
+# ---- the benchmark workloads -----------------------------------------------------
+
+@pytest.mark.parametrize("int8", [True, False])
+def test_decode_gemv_q4k_llama_ffn_up(ctx, int8):
+    """Q4_K decode GEMV, x [M, 4096], W [14336, 4096], M in {1, 2, 4, 8}, seed 1."""
+    name = "q4k_14336x4096_s1"
+    fmt, n, k, seed, _ = workloads.WEIGHTS[name]
+    w = workloads.weight_bytes(name)
+    h = ctx.upload(fmt, n, k, w)
+    try:
+        for m in (1, 2, 4, 8):
+            a = workloads.activations(seed, m, k)
+            got = ctx.matmul(h, a, int8=int8)
+            exp = expected(fmt, w, n, k, a, int8)
+            assert_row_tolerance(got, exp, f"m {m}")
+    finally:
+        h.release()
+
+
+def test_q4k_matvec_cpu_config(ctx):
+    """Q4_K matvec x [1, 4096] . W [4096, 4096]^T, seed 0."""
+    name = "q4k_4096x4096_s0"
+    fmt, n, k, seed, _ = workloads.WEIGHTS[name]
+    w = workloads.weight_bytes(name)
+    a = workloads.activations(seed, 1, k)
+    h = ctx.upload(fmt, n, k, w)
+    try:
+        got = ctx.matmul(h, a)
+    finally:
+        h.release()
+    exp = expected(fmt, w, n, k, a, True)
+    assert_row_tolerance(got, exp)
+    assert_close_reference(got, exp)
+
+
+@pytest.mark.parametrize("int8", [True, False])
+def test_iq4xs_gemv_llama_ffn_down(ctx, int8):
+    """IQ4_XS GEMV x [1, 14336] . W [4096, 14336]^T, seed 3."""
+    name = "iq4xs_4096x14336_s3"
+    fmt, n, k, seed, _ = workloads.WEIGHTS[name]
+    w = workloads.weight_bytes(name)
+    a = workloads.activations(seed, 1, k)
+    h = ctx.upload(fmt, n, k, w)
+    try:
+        got = ctx.matmul(h, a, int8=int8)
+    finally:
+        h.release()
+    exp = expected(fmt, w, n, k, a, int8)
+    assert_row_tolerance(got, exp)
+    assert_close_reference(got, exp)
+
+
+@pytest.mark.parametrize("name", ["q4k_4096x4096_s2", "q4k_14336x4096_s2"])
+@pytest.mark.parametrize("m", [128, 512, 2048])
+@pytest.mark.parametrize("int8", [True, False])
+def test_prefill_gemm(ctx, name, m, int8):
+    """Q4_K prefill GEMM x [M, 4096], M in {128, 512, 2048}, seed 2; the dense
+    oracle runs on 24 sampled rows (it is row-independent, so each sampled
+    row is exactly the full product's row)."""
+    fmt, n, k, seed, _ = workloads.WEIGHTS[name]
+    w = workloads.weight_bytes(name)
+    a = workloads.activations(seed, m, k)
+    h = ctx.upload(fmt, n, k, w)
+    try:
+        got = ctx.matmul(h, a, int8=int8)
+    finally:
+        h.release()
+    rows = np.unique(np.concatenate([[0, m - 1], np.random.default_rng(m).integers(0, m, 22)]))
+    exp = expected(fmt, w, n, k, a, int8, rows)
+    assert_row_tolerance(got[rows], exp, f"{name} m {m}")
+    assert np.isfinite(got).all()
+
+
+# ---- properties at full size -------------------------------------------------------
+
+@pytest.mark.parametrize("m", [1, 8, 512])
+def test_int8_power_of_two_scaling_is_exact(ctx, m):
+    """y(2^e x) = 2^e y(x) bit for bit in int8 mode: the activation scales
+    change by 2^e, the quantized values do not."""
+    name = "q4k_14336x4096_s1"
+    fmt, n, k, seed, _ = workloads.WEIGHTS[name]
+    h = ctx.upload(fmt, n, k, workloads.weight_bytes(name))
+    try:
+        a = workloads.activations(seed, m, k)
+        y = ctx.matmul(h, a)
+        for e in (-2, 3):
+            y2 = ctx.matmul(h, a * np.float32(2.0 ** e))
+            np.testing.assert_array_equal(y2, (y * np.float32(2.0 ** e)).astype(np.float32))
+    finally:
+        h.release()
+
+
+def test_matmul_is_deterministic_and_linear_in_weights_rows(ctx):
+    """Repeated calls are bit-identical; each output column depends on its
+    stored row only (a permutation of stored rows permutes the outputs)."""
+    n, k = 512, 4096
+    w = mg.quantize(Q4_K, mg.gaussian(9, 0.02, n * k).reshape(n, k))
+    perm = np.random.default_rng(1).permutation(n)
+    a = mg.gaussian(10, 1.0, 4 * k).reshape(4, k)
+    h = ctx.upload(Q4_K, n, k, w)
+    hp = ctx.upload(Q4_K, n, k, w[perm])
+    try:
+        for m in (1, 4):
+            y1 = ctx.matmul(h, a[:m])
+            np.testing.assert_array_equal(y1, ctx.matmul(h, a[:m]))
+            np.testing.assert_array_equal(ctx.matmul(hp, a[:m]), y1[:, perm])
+    finally:
+        h.release()
+        hp.release()
+
+
+# ---- device-pointer entry points ------------------------------------------------------
+
+def test_device_entry_points_agree_with_host_entry_point(ctx):
+    name = "q4k_14336x4096_s1"
+    fmt, n, k, seed, _ = workloads.WEIGHTS[name]
+    h = ctx.upload(fmt, n, k, workloads.weight_bytes(name))
+    try:
+        stream = torch.cuda.current_stream().cuda_stream
+        for m in (1, 4, 200):
+            a = workloads.activations(seed, m, k)
+            host = ctx.matmul(h, a)
+            xd = dev(a)
+            yd = torch.empty((m, n), dtype=torch.float32, device="cuda")
+            ctx.matmul_dev(h, xd.data_ptr(), m, k, yd.data_ptr(), stream=stream)
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(yd.cpu().numpy(), host)
+            if m <= 8:
+                v = torch.empty(m * k, dtype=torch.int8, device="cuda")
+                sc = torch.empty(m * k // 32, dtype=torch.float32, device="cuda")
+                sm = torch.empty(m * k // 16, dtype=torch.int32, device="cuda")
+                ctx.quantize_activations_dev(xd.data_ptr(), m, k, v.data_ptr(), sc.data_ptr(), sm.data_ptr(),
+                                             stream)
+                y2 = torch.empty((m, n), dtype=torch.float32, device="cuda")
+                ctx.matmul_prequantized_dev(h, v.data_ptr(), sc.data_ptr(), sm.data_ptr(), m, k,
+                                            y2.data_ptr(), stream)
+                torch.cuda.synchronize()
+                np.testing.assert_array_equal(y2.cpu().numpy(), host)
+        out = torch.empty((n, k), dtype=torch.float32, device="cuda")
+        ctx.dequantize_dev(h, out.data_ptr(), stream=stream)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(out.cpu().numpy(), ctx.dequantize(h))
+    finally:
+        h.release()
+
+
+# ---- boundary behaviour ---------------------------------------------------------------
+
+def test_boundary_errors_and_declines(ctx):
+    w = packed(Q4_K, 4, 256, 41)
+    with pytest.raises(mg.Declined):
+        ctx.upload(8, 4, 256, np.zeros(4 * 34, np.uint8))  # Q8_0 has no GPU path
+    with pytest.raises(mg.Declined):
+        ctx.upload(Q4_K, 4, 256, w, transposed=False)
+    with pytest.raises(mg.GpuError) as e:
+        ctx.upload(Q4_K, 4, 256, w[:, :100])
+    assert e.value.code == mg.ERR_SHAPE
+    with pytest.raises(mg.GpuError) as e:
+        ctx.upload(Q4_K, 4, 200, np.zeros(4 * 144, np.uint8))
+    assert e.value.code == mg.ERR_SHAPE
+    h = ctx.upload(Q4_K, 4, 256, w)
+    try:
+        info = ctx.info(h)
+        assert (info["stored_rows"], info["stored_cols"], info["type"]) == (4, 256, Q4_K)
+        assert h.logical_shape == (256, 4)
+        with pytest.raises(mg.GpuError) as e:
+            ctx.matmul(h, np.zeros((1, 512), np.float32))
+        assert e.value.code == mg.ERR_SHAPE and "512 columns" in e.value.reason
+        assert ctx.matmul(h, np.zeros((0, 256), np.float32)).shape == (0, 4)
+    finally:
+        h.release()
+    with pytest.raises(mg.GpuError) as e:
+        ctx.matmul(h, np.zeros((1, 256), np.float32))
+    assert e.value.code == mg.ERR_ARGUMENT
+
+
+def test_non_finite_activations(ctx):
+    """f32 mode: a NaN activation makes its output row NaN (no zero-skip);
+    int8 mode: NaN quantizes to 0, as the reference's `as i8` does."""
+    n, k = 64, 512
+    w = packed(Q4_K, n, k, 3)
+    h = ctx.upload(Q4_K, n, k, w)
+    try:
+        for m in (1, 12):
+            a = activations(m, k, 5)
+            a[0, 17] = np.nan
+            y32 = ctx.matmul(h, a, int8=False)
+            assert np.isnan(y32[0]).all() and np.isfinite(y32[1:]).all()
+            y8 = ctx.matmul(h, a, int8=True)
+            exp = expected(Q4_K, w, n, k, a, True)
+            assert np.isfinite(y8).all()
+            assert row_tolerance_violation(y8, exp) <= 1.0
+    finally:
+        h.release()
