@@ -1,0 +1,123 @@
+/*
+ * magnetar_executor: the Provider-side contract of the GPU packed-weight
+ * matmul Kernel (libmagnetar_executor.so), a C surface over the C++
+ * GpuExecutor, which itself calls only libmagnetar_gpu (magnetar_gpu.h).
+ *
+ * Resource ids are NUL-terminated strings (TensorResourceId). Tensors are
+ * row-major f32 with an explicit shape (HostTensor). Every call returns
+ * an MG_* status; mg_executor_last_error() holds the reason text.
+ */
+#ifndef MAGNETAR_EXECUTOR_H
+#define MAGNETAR_EXECUTOR_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes; MG_KERNEL_* carry the KernelError variant of a completed
+ * invocation (external magnetar-kernel type). */
+#define MG_OK 0
+#define MG_KERNEL_EXECUTION_FAILED 1
+#define MG_KERNEL_DTYPE_UNSUPPORTED 2
+#define MG_KERNEL_ATTRIBUTE_UNSUPPORTED 3
+#define MG_KERNEL_NOT_FOUND 4
+#define MG_KERNEL_TIMEOUT 5
+#define MG_MEMORY_DENIED 6  /* MemoryError: admission denied */
+#define MG_UNKNOWN 7        /* unknown resource id or execution handle */
+#define MG_ERR_ARGUMENT 8
+#define MG_ERR_DEVICE 9     /* the GPU context could not be created */
+
+typedef struct mg_executor mg_executor;
+
+/* An executor on HIP device `device` (`NativeCpuExecutor::with_settings`,
+ * src/native/mod.rs:525-544): packed_weights = 0 declines every packed
+ * weight (MAGNETAR_CPU_PACKED_WEIGHTS=0), int8_activations selects the
+ * reference's default int8 activations (MAGNETAR_CPU_INT8_ACTIVATIONS),
+ * memory_capacity bounds admitted tensor bytes (the MemoryManager ledger).
+ * Records ProviderRegistered and DeviceDetected observations
+ * (`Provider::initialize`, src/native/mod.rs:928-938). */
+int mg_executor_create(int device, int packed_weights, int int8_activations,
+                       uint64_t memory_capacity, mg_executor **out);
+void mg_executor_destroy(mg_executor *ex);
+const char *mg_executor_last_error(mg_executor *ex);
+
+/* `write_packed_weight_tensor` (src/native/mod.rs:638-653): *stored = 1
+ * (PackedWeightWrite::Stored) or 0 (Declined: unsupported format,
+ * untransposed weight, or packed weights disabled). */
+int mg_write_packed_weight_tensor(mg_executor *ex, const char *id, uint32_t gguf_type,
+                                  uint64_t stored_rows, uint64_t stored_cols,
+                                  int transposed, const uint8_t *bytes, size_t len,
+                                  int *stored);
+
+/* `write_tensor` (src/native/mod.rs:629-636): f32 storage; forgets a packed
+ * weight of the same id. */
+int mg_write_tensor(mg_executor *ex, const char *id, const uint64_t *shape,
+                    uint32_t rank, const float *data);
+
+/* `write_tensor_admitted` (src/native/mod.rs:664-681): MG_MEMORY_DENIED
+ * leaves storage and any packed weight unchanged. */
+int mg_write_tensor_admitted(mg_executor *ex, const char *id, const uint64_t *shape,
+                             uint32_t rank, const float *data);
+
+/* `resident_shape` (src/native/mod.rs:704-706): *rank in = capacity of
+ * `shape`, out = the rank. A packed weight reports its logical shape. */
+int mg_resident_shape(mg_executor *ex, const char *id, uint64_t *shape, uint32_t *rank);
+
+/* `read_tensor` (src/lib.rs:1615-1620): f32 values; a packed weight is
+ * materialized (dequantized, logical layout). `count` = capacity of out. */
+int mg_read_tensor(mg_executor *ex, const char *id, float *out, uint64_t count);
+
+/* `is_packed` (src/native/mod.rs:554-557); `read_tensor_value` answers
+ * Opaque for every resident id (src/native/mod.rs:695-702). */
+int mg_is_packed(mg_executor *ex, const char *id);
+int mg_read_tensor_value_is_opaque(mg_executor *ex, const char *id);
+
+/* `release_tensor` (src/native/mod.rs:655-660): *released = 1 if the id
+ * held a tensor or a packed weight. */
+int mg_release_tensor(mg_executor *ex, const char *id, int *released);
+
+/* One invocation attribute: "transpose_a"/"transpose_b" = "true"/"false",
+ * "accumulation_dtype" = a dtype name ("f32", "f16", ...). */
+typedef struct {
+  const char *name;
+  const char *value;
+} mg_attribute;
+
+/* `submit_kernel` (src/native/mod.rs:598-620, src/lib.rs:2301-2330): runs
+ * the invocation synchronously and stores its KernelResult under the
+ * returned handle text ("<provider>:<invocation>:<n>"). deadline_millis < 0:
+ * none; 0 fails with KernelTimeout before dispatch. */
+int mg_submit_kernel(mg_executor *ex, const char *kernel, const char *invocation_id,
+                     const char *const *inputs, uint32_t n_inputs, const char *output,
+                     const mg_attribute *attributes, uint32_t n_attributes,
+                     int64_t deadline_millis, char *handle, size_t handle_capacity);
+
+/* `complete_kernel` (src/lib.rs:2337-2356): consumes the stored result once;
+ * MG_UNKNOWN for a handle never submitted or already completed. On success
+ * *kernel_error is MG_OK or the KernelError variant, with its reason. */
+int mg_complete_kernel(mg_executor *ex, const char *handle, int *kernel_error,
+                       char *reason, size_t reason_capacity);
+
+/* Observation log (`observations`, src/lib.rs:1848-1868), kind text such as
+ * "KernelDispatchStarted", "KernelDispatchCompleted", "KernelDispatchFailed",
+ * "KernelTimeout", "KernelMemoryFeasibilityFailed". */
+uint64_t mg_observation_count(mg_executor *ex);
+int mg_observation(mg_executor *ex, uint64_t index, char *kind, size_t kind_capacity,
+                   char *kernel, size_t kernel_capacity);
+
+/* Kernel advertisements (`native_cpu_kernel_advertisements`,
+ * src/native/mod.rs:847-864) as JSON text, one per index. */
+uint32_t mg_kernel_advertisement_count(void);
+const char *mg_kernel_advertisement_json(uint32_t index);
+
+/* Packed weights materialized to f32 so far (the profile counter,
+ * src/native/mod.rs:79-81). */
+uint64_t mg_materialization_count(mg_executor *ex);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

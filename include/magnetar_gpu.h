@@ -92,6 +92,22 @@ int mq_matmul(mq_ctx *ctx, uint64_t handle, const float *x, uint64_t m,
 int mq_matmul_dev(mq_ctx *ctx, uint64_t handle, const float *x_dev, uint64_t m,
                   uint64_t k, uint32_t flags, float *y_dev, void *stream);
 
+/* y = x . W^T + addend, the addition fused into the kernel's output write
+ * (the product rounded first, then the addend added): addend_rows = 1
+ * broadcasts one [stored_rows] row (a bias), addend_rows = m adds an
+ * [m][stored_rows] tensor (a residual). Replaces the `matmul-bias` /
+ * `matmul-residual` epilogue `add` / `residual_add` after `packed_matmul`
+ * (src/native/mod.rs:228-235; src/lib.rs:1028-1073, 1128-1133).
+ * Host pointers, synchronous. */
+int mq_matmul_add(mq_ctx *ctx, uint64_t handle, const float *x, uint64_t m,
+                  uint64_t k, uint32_t flags, const float *addend,
+                  uint64_t addend_rows, float *y);
+
+/* mq_matmul_add on device pointers, enqueued on `stream`. */
+int mq_matmul_add_dev(mq_ctx *ctx, uint64_t handle, const float *x_dev, uint64_t m,
+                      uint64_t k, uint32_t flags, const float *addend_dev,
+                      uint64_t addend_rows, float *y_dev, void *stream);
+
 /* Int8 activation quantization on device: values[m*k], scales[m*k/32],
  * sums[m*k/32][2] (int32 half sums). Replaces `quant::quantize_rows`
  * (src/native/quant.rs:350-378). */

@@ -135,14 +135,20 @@ int gemv_splits(mq_ctx* ctx, const Weight& w) {
 
 constexpr uint64_t kGemvMaxRows = 8;
 
-// Enqueues y = x . W^T on `stream`. Caller holds ctx->mu.
+// Enqueues y = x . W^T [+ addend] on `stream`. Caller holds ctx->mu.
+// addend_rows: 0 (no addend), 1 (one row broadcast) or m.
 int matmul_locked(mq_ctx* ctx, const Weight& w, const float* x, uint64_t m, uint64_t k, uint32_t flags, float* y,
-                  hipStream_t stream) {
+                  hipStream_t stream, const float* addend = nullptr, uint64_t addend_rows = 0) {
   int rc = check_k(ctx, w, k);
   if (rc) return rc;
   if (flags & ~MQ_INT8_ACTIVATIONS) return fail(ctx, MQ_ERR_ARGUMENT, "unknown matmul flag bits");
   if (m == 0) return MQ_OK;
   if (!x || !y) return fail(ctx, MQ_ERR_ARGUMENT, "null activation or output pointer");
+  if (addend && addend_rows != 1 && addend_rows != m)
+    return fail(ctx, MQ_ERR_SHAPE, "addend must hold 1 or " + std::to_string(m) + " rows, not " +
+                                       std::to_string(addend_rows));
+  const uint64_t addend_stride = addend && addend_rows == m && m > 1 ? w.rows : 0;
+  if (!addend) addend_rows = 0;
   const bool int8 = (flags & MQ_INT8_ACTIVATIONS) != 0;
   if (m <= kGemvMaxRows) {
     if (int8) {
@@ -154,10 +160,11 @@ int matmul_locked(mq_ctx* ctx, const Weight& w, const float* x, uint64_t m, uint
       auto* scales = reinterpret_cast<float*>(base + vb);
       auto* sums = reinterpret_cast<int32_t*>(base + vb + sb);
       mq::launch_quantize_activations(x, m, k, values, scales, sums, nullptr, 1, stream);
-      mq::launch_gemv_int8(static_cast<int>(w.type), w.dev, w.rows, w.nb, values, scales, sums, m, y,
-                           gemv_splits(ctx, w), stream);
+      mq::launch_gemv_int8(static_cast<int>(w.type), w.dev, w.rows, w.nb, values, scales, sums, m, y, addend,
+                           addend_stride, gemv_splits(ctx, w), stream);
     } else {
-      mq::launch_gemv_f32(static_cast<int>(w.type), w.dev, w.rows, w.nb, x, m, y, gemv_splits(ctx, w), stream);
+      mq::launch_gemv_f32(static_cast<int>(w.type), w.dev, w.rows, w.nb, x, m, y, addend, addend_stride,
+                          gemv_splits(ctx, w), stream);
     }
   } else {
     rc = acquire_workspace(ctx, stream, align256(m * k * 2));
@@ -167,7 +174,7 @@ int matmul_locked(mq_ctx* ctx, const Weight& w, const float* x, uint64_t m, uint
       mq::launch_quantize_activations(x, m, k, nullptr, nullptr, nullptr, a16, 1, stream);
     else
       mq::launch_activations_f16(x, m, k, a16, stream);
-    mq::launch_gemm(static_cast<int>(w.type), w.dev, w.rows, w.nb, a16, m, y, stream);
+    mq::launch_gemm(static_cast<int>(w.type), w.dev, w.rows, w.nb, a16, m, y, addend, addend_stride, stream);
   }
   MQ_HIP(ctx, hipGetLastError());
   return MQ_OK;
@@ -312,33 +319,74 @@ int mq_matmul_dev(mq_ctx* ctx, uint64_t handle, const float* x_dev, uint64_t m, 
   return matmul_locked(ctx, *w, x_dev, m, k, flags, y_dev, s);
 }
 
+namespace {
+
+// Host-pointer matmul: stage x (and the addend) in device memory, run on the
+// context's stream, copy y back. Caller holds ctx->mu.
+int matmul_host_locked(mq_ctx* ctx, const Weight& w, const float* x, uint64_t m, uint64_t k, uint32_t flags,
+                       const float* addend, uint64_t addend_rows, float* y) {
+  int rc = check_k(ctx, w, k);
+  if (rc) return rc;
+  if (m == 0) return MQ_OK;
+  if (!x || !y) return fail(ctx, MQ_ERR_ARGUMENT, "mq_matmul: null host pointer");
+  if (addend && addend_rows != 1 && addend_rows != m)
+    return fail(ctx, MQ_ERR_SHAPE, "addend must hold 1 or " + std::to_string(m) + " rows, not " +
+                                       std::to_string(addend_rows));
+  const uint64_t add_count = addend ? addend_rows * w.rows : 0;
+  const size_t xb = align256(m * k * sizeof(float)), yb = align256(m * w.rows * sizeof(float));
+  const size_t ab = align256(add_count * sizeof(float));
+  if (xb + yb + ab > ctx->io_bytes) {
+    MQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (ctx->io) MQ_HIP(ctx, hipFree(ctx->io));
+    ctx->io = nullptr;
+    ctx->io_bytes = 0;
+    MQ_HIP(ctx, hipMalloc(&ctx->io, xb + yb + ab));
+    ctx->io_bytes = xb + yb + ab;
+  }
+  auto* base = static_cast<uint8_t*>(ctx->io);
+  auto* xd = reinterpret_cast<float*>(base);
+  auto* yd = reinterpret_cast<float*>(base + xb);
+  auto* ad = addend ? reinterpret_cast<float*>(base + xb + yb) : nullptr;
+  MQ_HIP(ctx, hipMemcpyAsync(xd, x, m * k * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
+  if (ad) MQ_HIP(ctx, hipMemcpyAsync(ad, addend, add_count * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
+  rc = matmul_locked(ctx, w, xd, m, k, flags, yd, ctx->stream, ad, addend_rows);
+  if (rc) return rc;
+  MQ_HIP(ctx, hipMemcpyAsync(y, yd, m * w.rows * sizeof(float), hipMemcpyDeviceToHost, ctx->stream));
+  MQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return MQ_OK;
+}
+
+}  // namespace
+
 int mq_matmul(mq_ctx* ctx, uint64_t handle, const float* x, uint64_t m, uint64_t k, uint32_t flags, float* y) {
   if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_matmul: null context");
   std::lock_guard<std::mutex> lock(ctx->mu);
   const Weight* w = find_weight(ctx, handle);
   if (!w) return fail(ctx, MQ_ERR_ARGUMENT, "unknown weight handle " + std::to_string(handle));
-  int rc = check_k(ctx, *w, k);
-  if (rc) return rc;
-  if (m == 0) return MQ_OK;
-  if (!x || !y) return fail(ctx, MQ_ERR_ARGUMENT, "mq_matmul: null host pointer");
   DeviceGuard guard(ctx->device);
-  const size_t xb = align256(m * k * sizeof(float)), yb = align256(m * w->rows * sizeof(float));
-  if (xb + yb > ctx->io_bytes) {
-    MQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
-    if (ctx->io) MQ_HIP(ctx, hipFree(ctx->io));
-    ctx->io = nullptr;
-    ctx->io_bytes = 0;
-    MQ_HIP(ctx, hipMalloc(&ctx->io, xb + yb));
-    ctx->io_bytes = xb + yb;
-  }
-  auto* xd = static_cast<float*>(ctx->io);
-  auto* yd = reinterpret_cast<float*>(static_cast<uint8_t*>(ctx->io) + xb);
-  MQ_HIP(ctx, hipMemcpyAsync(xd, x, m * k * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
-  rc = matmul_locked(ctx, *w, xd, m, k, flags, yd, ctx->stream);
-  if (rc) return rc;
-  MQ_HIP(ctx, hipMemcpyAsync(y, yd, m * w->rows * sizeof(float), hipMemcpyDeviceToHost, ctx->stream));
-  MQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
-  return MQ_OK;
+  return matmul_host_locked(ctx, *w, x, m, k, flags, nullptr, 0, y);
+}
+
+int mq_matmul_add(mq_ctx* ctx, uint64_t handle, const float* x, uint64_t m, uint64_t k, uint32_t flags,
+                  const float* addend, uint64_t addend_rows, float* y) {
+  if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_matmul_add: null context");
+  if (!addend) return fail(ctx, MQ_ERR_ARGUMENT, "mq_matmul_add: null addend");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  const Weight* w = find_weight(ctx, handle);
+  if (!w) return fail(ctx, MQ_ERR_ARGUMENT, "unknown weight handle " + std::to_string(handle));
+  DeviceGuard guard(ctx->device);
+  return matmul_host_locked(ctx, *w, x, m, k, flags, addend, addend_rows, y);
+}
+
+int mq_matmul_add_dev(mq_ctx* ctx, uint64_t handle, const float* x_dev, uint64_t m, uint64_t k, uint32_t flags,
+                      const float* addend_dev, uint64_t addend_rows, float* y_dev, void* stream) {
+  if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_matmul_add_dev: null context");
+  if (!addend_dev) return fail(ctx, MQ_ERR_ARGUMENT, "mq_matmul_add_dev: null addend");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  const Weight* w = find_weight(ctx, handle);
+  if (!w) return fail(ctx, MQ_ERR_ARGUMENT, "unknown weight handle " + std::to_string(handle));
+  DeviceGuard guard(ctx->device);
+  return matmul_locked(ctx, *w, x_dev, m, k, flags, y_dev, static_cast<hipStream_t>(stream), addend_dev, addend_rows);
 }
 
 int mq_quantize_activations_dev(mq_ctx* ctx, const float* x_dev, uint64_t m, uint64_t k, int8_t* values_dev,
@@ -370,7 +418,7 @@ int mq_matmul_prequantized_dev(mq_ctx* ctx, uint64_t handle, const int8_t* value
   DeviceGuard guard(ctx->device);
   hipStream_t s = static_cast<hipStream_t>(stream);
   mq::launch_gemv_int8(static_cast<int>(w->type), w->dev, w->rows, w->nb, values_dev, scales_dev, sums_dev, m, y_dev,
-                       gemv_splits(ctx, *w), s);
+                       nullptr, 0, gemv_splits(ctx, *w), s);
   MQ_HIP(ctx, hipGetLastError());
   return MQ_OK;
 }
@@ -404,7 +452,7 @@ int mq_matmul_f16_dev(mq_ctx* ctx, uint64_t handle, const uint16_t* a16_dev, uin
   if (!a16_dev || !y_dev) return fail(ctx, MQ_ERR_ARGUMENT, "mq_matmul_f16_dev: null pointer");
   DeviceGuard guard(ctx->device);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  mq::launch_gemm(static_cast<int>(w->type), w->dev, w->rows, w->nb, a16_dev, m, y_dev, s);
+  mq::launch_gemm(static_cast<int>(w->type), w->dev, w->rows, w->nb, a16_dev, m, y_dev, nullptr, 0, s);
   MQ_HIP(ctx, hipGetLastError());
   return MQ_OK;
 }

@@ -202,8 +202,12 @@ __global__ void activations_f16_kernel(const float* __restrict__ x, uint64_t tot
 // a row reduced by shuffles, waves of a group through LDS in fixed order.
 // ---------------------------------------------------------------------------
 
+// y[m][row] = (acc - mins) [+ addend[m * addend_stride + row]]: the
+// product rounded first, then the bias / residual added, as the reference's
+// separate `add` does.
 template <int M>
-__device__ inline void reduce_and_store(float (&acc)[M], float (&mins)[M], uint64_t rows, float* y) {
+__device__ inline void reduce_and_store(float (&acc)[M], float (&mins)[M], uint64_t rows, float* y,
+                                        const float* addend, uint64_t addend_stride) {
   __shared__ float red[8][M][8][2];
   const int lane = threadIdx.x & 63, s = threadIdx.x >> 6, S = blockDim.x >> 6;
   const int r = lane & 7, lam = lane >> 3;
@@ -219,7 +223,11 @@ __device__ inline void reduce_and_store(float (&acc)[M], float (&mins)[M], uint6
   if (S == 1) {
     if (lam == 0 && row < rows) {
 #pragma unroll
-      for (int m = 0; m < M; ++m) y[m * rows + row] = acc[m] - mins[m];
+      for (int m = 0; m < M; ++m) {
+        float v = acc[m] - mins[m];
+        if (addend) v = v + addend[m * addend_stride + row];
+        y[m * rows + row] = v;
+      }
     }
     return;
   }
@@ -239,7 +247,9 @@ __device__ inline void reduce_and_store(float (&acc)[M], float (&mins)[M], uint6
         a += red[i][m][threadIdx.x][0];
         mn += red[i][m][threadIdx.x][1];
       }
-      y[m * rows + row] = a - mn;
+      float v = a - mn;
+      if (addend) v = v + addend[m * addend_stride + row];
+      y[m * rows + row] = v;
     }
   }
 }
@@ -247,7 +257,8 @@ __device__ inline void reduce_and_store(float (&acc)[M], float (&mins)[M], uint6
 template <int M>
 __global__ __launch_bounds__(512) void gemv_q4k_int8_kernel(
     const uint8_t* __restrict__ w, int nb, uint64_t rows, const int8_t* __restrict__ xv,
-    const float* __restrict__ xs, const int32_t* __restrict__ xsum, float* __restrict__ y) {
+    const float* __restrict__ xs, const int32_t* __restrict__ xsum, float* __restrict__ y,
+    const float* __restrict__ addend, uint64_t addend_stride) {
   const int lane = threadIdx.x & 63, s = threadIdx.x >> 6, S = blockDim.x >> 6;
   const int r = lane & 7, lam = lane >> 3;
   const uint64_t g = blockIdx.x;
@@ -307,13 +318,14 @@ __global__ __launch_bounds__(512) void gemv_q4k_int8_kernel(
       }
     }
   }
-  reduce_and_store<M>(acc, mins, rows, y);
+  reduce_and_store<M>(acc, mins, rows, y, addend, addend_stride);
 }
 
 template <int M>
 __global__ __launch_bounds__(512) void gemv_iq4xs_int8_kernel(
     const uint8_t* __restrict__ w, int nb, uint64_t rows, const int8_t* __restrict__ xv,
-    const float* __restrict__ xs, float* __restrict__ y) {
+    const float* __restrict__ xs, float* __restrict__ y, const float* __restrict__ addend,
+    uint64_t addend_stride) {
   const int lane = threadIdx.x & 63, s = threadIdx.x >> 6, S = blockDim.x >> 6;
   const int r = lane & 7, lam = lane >> 3;
   const uint64_t g = blockIdx.x;
@@ -354,7 +366,7 @@ __global__ __launch_bounds__(512) void gemv_iq4xs_int8_kernel(
       }
     }
   }
-  reduce_and_store<M>(acc, mins, rows, y);
+  reduce_and_store<M>(acc, mins, rows, y, addend, addend_stride);
 }
 
 // f32 activations: per run half, sum(q * x) and sum(x) in f32, then
@@ -379,7 +391,8 @@ __device__ inline void dot_signed_f32(uint32_t bytes4, float4 x, float& dq) {
 template <int M>
 __global__ __launch_bounds__(512) void gemv_q4k_f32_kernel(const uint8_t* __restrict__ w, int nb,
                                                            uint64_t rows, const float* __restrict__ x,
-                                                           float* __restrict__ y) {
+                                                           float* __restrict__ y, const float* __restrict__ addend,
+                                                           uint64_t addend_stride) {
   const int lane = threadIdx.x & 63, s = threadIdx.x >> 6, S = blockDim.x >> 6;
   const int r = lane & 7, lam = lane >> 3;
   const uint64_t g = blockIdx.x;
@@ -420,13 +433,14 @@ __global__ __launch_bounds__(512) void gemv_q4k_f32_kernel(const uint8_t* __rest
       }
     }
   }
-  reduce_and_store<M>(acc, mins, rows, y);
+  reduce_and_store<M>(acc, mins, rows, y, addend, addend_stride);
 }
 
 template <int M>
 __global__ __launch_bounds__(512) void gemv_iq4xs_f32_kernel(const uint8_t* __restrict__ w, int nb,
                                                              uint64_t rows, const float* __restrict__ x,
-                                                             float* __restrict__ y) {
+                                                             float* __restrict__ y, const float* __restrict__ addend,
+                                                             uint64_t addend_stride) {
   const int lane = threadIdx.x & 63, s = threadIdx.x >> 6, S = blockDim.x >> 6;
   const int r = lane & 7, lam = lane >> 3;
   const uint64_t g = blockIdx.x;
@@ -456,7 +470,7 @@ __global__ __launch_bounds__(512) void gemv_iq4xs_f32_kernel(const uint8_t* __re
       }
     }
   }
-  reduce_and_store<M>(acc, mins, rows, y);
+  reduce_and_store<M>(acc, mins, rows, y, addend, addend_stride);
 }
 
 // ---------------------------------------------------------------------------
@@ -480,7 +494,8 @@ __device__ inline uint32_t pack_f16x2(float a, float b) {
 template <int TYPE>
 __global__ __launch_bounds__(256) void gemm_kernel(const uint8_t* __restrict__ w, int nb, uint64_t rows,
                                                    uint64_t rows_padded, const uint16_t* __restrict__ a16,
-                                                   uint64_t m_rows, float* __restrict__ y) {
+                                                   uint64_t m_rows, float* __restrict__ y,
+                                                   const float* __restrict__ addend, uint64_t addend_stride) {
   __shared__ __attribute__((aligned(16))) uint16_t As[kBM][kLdsK];
   __shared__ __attribute__((aligned(16))) uint16_t Bs[kBN][kLdsK];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -599,7 +614,11 @@ __global__ __launch_bounds__(256) void gemm_kernel(const uint8_t* __restrict__ w
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const uint64_t row = m0 + wm + 16 * i + 4 * (lane >> 4) + e;
-        if (row < m_rows && col < rows) y[row * rows + col] = acc[i][j][e];
+        if (row < m_rows && col < rows) {
+          float v = acc[i][j][e];
+          if (addend) v = v + addend[row * addend_stride + col];
+          y[row * rows + col] = v;
+        }
       }
     }
   }
@@ -658,8 +677,8 @@ int gemv_default_splits(uint64_t rows, uint64_t nb) {
 #define MQ_GEMV_CASES(X) X(1) X(2) X(3) X(4) X(5) X(6) X(7) X(8)
 
 void launch_gemv_int8(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, const int8_t* values,
-                      const float* scales, const int32_t* sums, uint64_t m, float* y, int splits,
-                      hipStream_t stream) {
+                      const float* scales, const int32_t* sums, uint64_t m, float* y, const float* addend,
+                      uint64_t addend_stride, int splits, hipStream_t stream) {
   dim3 grid(static_cast<unsigned>((rows + 7) / 8)), block(64 * splits);
   const int inb = static_cast<int>(nb);
   if (type == kTypeQ4K) {
@@ -667,7 +686,7 @@ void launch_gemv_int8(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb
 #define X(MM)                                                                                           \
   case MM:                                                                                              \
     hipLaunchKernelGGL(gemv_q4k_int8_kernel<MM>, grid, block, 0, stream, tiled, inb, rows, values, scales, \
-                       sums, y);                                                                        \
+                       sums, y, addend, addend_stride);                                                                        \
     break;
       MQ_GEMV_CASES(X)
 #undef X
@@ -679,7 +698,7 @@ void launch_gemv_int8(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb
 #define X(MM)                                                                                             \
   case MM:                                                                                                \
     hipLaunchKernelGGL(gemv_iq4xs_int8_kernel<MM>, grid, block, 0, stream, tiled, inb, rows, values, scales, \
-                       y);                                                                                \
+                       y, addend, addend_stride);                                                                                \
     break;
       MQ_GEMV_CASES(X)
 #undef X
@@ -690,14 +709,15 @@ void launch_gemv_int8(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb
 }
 
 void launch_gemv_f32(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, const float* x, uint64_t m,
-                     float* y, int splits, hipStream_t stream) {
+                     float* y, const float* addend, uint64_t addend_stride, int splits, hipStream_t stream) {
   dim3 grid(static_cast<unsigned>((rows + 7) / 8)), block(64 * splits);
   const int inb = static_cast<int>(nb);
   if (type == kTypeQ4K) {
     switch (m) {
 #define X(MM)                                                                                       \
   case MM:                                                                                          \
-    hipLaunchKernelGGL(gemv_q4k_f32_kernel<MM>, grid, block, 0, stream, tiled, inb, rows, x, y); \
+    hipLaunchKernelGGL(gemv_q4k_f32_kernel<MM>, grid, block, 0, stream, tiled, inb, rows, x, y, addend, \
+                       addend_stride);                                                            \
     break;
       MQ_GEMV_CASES(X)
 #undef X
@@ -708,7 +728,8 @@ void launch_gemv_f32(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb,
     switch (m) {
 #define X(MM)                                                                                         \
   case MM:                                                                                            \
-    hipLaunchKernelGGL(gemv_iq4xs_f32_kernel<MM>, grid, block, 0, stream, tiled, inb, rows, x, y); \
+    hipLaunchKernelGGL(gemv_iq4xs_f32_kernel<MM>, grid, block, 0, stream, tiled, inb, rows, x, y, addend, \
+                       addend_stride);                                                              \
     break;
       MQ_GEMV_CASES(X)
 #undef X
@@ -719,15 +740,15 @@ void launch_gemv_f32(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb,
 }
 
 void launch_gemm(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, const uint16_t* a16, uint64_t m,
-                 float* y, hipStream_t stream) {
+                 float* y, const float* addend, uint64_t addend_stride, hipStream_t stream) {
   const uint64_t rows_padded = (rows + 7) / 8 * 8;
   dim3 grid(static_cast<unsigned>((rows + kBN - 1) / kBN), static_cast<unsigned>((m + kBM - 1) / kBM));
   if (type == kTypeQ4K)
     hipLaunchKernelGGL(gemm_kernel<kTypeQ4K>, grid, dim3(256), 0, stream, tiled, static_cast<int>(nb), rows,
-                       rows_padded, a16, m, y);
+                       rows_padded, a16, m, y, addend, addend_stride);
   else
     hipLaunchKernelGGL(gemm_kernel<kTypeIq4Xs>, grid, dim3(256), 0, stream, tiled, static_cast<int>(nb), rows,
-                       rows_padded, a16, m, y);
+                       rows_padded, a16, m, y, addend, addend_stride);
 }
 
 }  // namespace mq

@@ -27,18 +27,24 @@ void launch_quantize_activations(const float* x, uint64_t m, uint64_t k, int8_t*
 void launch_activations_f16(const float* x, uint64_t m, uint64_t k, uint16_t* a16,
                             hipStream_t stream);
 
+// The matmul kernels write y[i][n] = product [+ addend[i * addend_stride + n]]
+// (addend may be null; stride 0 broadcasts one row, as a bias).
+
 // Decode GEMV, m in 1..8, int8 activations.
 void launch_gemv_int8(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb,
                       const int8_t* values, const float* scales, const int32_t* sums,
-                      uint64_t m, float* y, int splits, hipStream_t stream);
+                      uint64_t m, float* y, const float* addend, uint64_t addend_stride, int splits,
+                      hipStream_t stream);
 
 // Decode GEMV, m in 1..8, f32 activations.
 void launch_gemv_f32(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb,
-                     const float* x, uint64_t m, float* y, int splits, hipStream_t stream);
+                     const float* x, uint64_t m, float* y, const float* addend, uint64_t addend_stride,
+                     int splits, hipStream_t stream);
 
 // Prefill GEMM on MFMA: y[m][rows] = a16[m][K] . dequant(W)^T, f32 out.
 void launch_gemm(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb,
-                 const uint16_t* a16, uint64_t m, float* y, hipStream_t stream);
+                 const uint16_t* a16, uint64_t m, float* y, const float* addend, uint64_t addend_stride,
+                 hipStream_t stream);
 
 // Grid-shape helper for the GEMV (waves per work-group).
 int gemv_default_splits(uint64_t rows, uint64_t nb);

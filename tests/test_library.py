@@ -26,6 +26,7 @@ def _declared(header):
 @pytest.mark.parametrize("header,lib", [
     ("magnetar_gpu.h", mg.GPU_LIB),
     ("magnetar_gguf.h", mg.GGUF_LIB),
+    ("magnetar_executor.h", mg.EXECUTOR_LIB),
 ])
 def test_library_exports_every_declared_symbol(header, lib):
     names = _declared(header)
