@@ -110,7 +110,14 @@ def main():
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=8.0, help="bound on CPU-baseline timing")
+    ap.add_argument("--parts", default="gemv,shapes,iq4xs,gemm,cpu",
+                    help="comma list of parts to run (the headline line needs gemv)")
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="also run a plain device copy of this size (counter calibration under rocprofv3)")
     args = ap.parse_args()
+    parts = set(args.parts.split(","))
+    if args.no_cpu:
+        parts.discard("cpu")
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this path runs on a single MI355X and takes no "
@@ -174,9 +181,18 @@ def main():
     torch.cuda.synchronize()
     y_gpu = y.cpu().numpy()
 
+    if args.copy_calibration_mib:
+        nbytes = args.copy_calibration_mib << 20
+        src = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy calibration: 5 plain copies of {nbytes} bytes (read {nbytes}, write {nbytes} per copy)")
+
     # ---- other decode shapes (kernel alone) --------------------------------------
     extra = {}
-    for m in (2, 4, 8):
+    for m in ((2, 4, 8) if "shapes" in parts else ()):
         xm = torch.from_numpy(workloads.activations(seed, m, k)).cuda()
         qv = torch.empty(m * k, dtype=torch.int8, device="cuda")
         qs = torch.empty(m * k // 32, dtype=torch.float32, device="cuda")
@@ -196,6 +212,19 @@ def main():
         extra[f"q4k_gemv_m{m}_GBps"] = round(weight_bytes / t / 1e9, 1)
         log(f"gemv m={m} kernel: {t * 1e6:.2f} us, {weight_bytes / t / 1e9:.1f} GB/s")
 
+    if "iq4xs" in parts:
+        iq4xs_part(ctx, torch, workloads, args, per_graph, use_graph, extra)
+    gemm = gemm_part(ctx, torch, workloads, use_graph, args) if "gemm" in parts else None
+    cpu = cpu_part(fmt, wbytes, n, k, x_host, y_gpu, weight_bytes, args) if "cpu" in parts else None
+
+    for h in copies:
+        h.release()
+    ctx.close()
+    emit(args, value, steps, warmup, ms_per_step, n, k, weight_bytes, use_graph, step_runner, achieved, kernel_us,
+         cpu, gemm, extra)
+
+
+def iq4xs_part(ctx, torch, workloads, args, per_graph, use_graph, extra):
     # IQ4_XS GEMV x[1, 14336] . W[4096, 14336]^T
     iname = "iq4xs_4096x14336_s3"
     ifmt, inn, ik, iseed, _ = workloads.WEIGHTS[iname]
@@ -224,6 +253,8 @@ def main():
     for h in icopies:
         h.release()
 
+
+def gemm_part(ctx, torch, workloads, use_graph, args):
     # ---- prefill GEMM: x[512, 4096] . W[14336, 4096]^T ---------------------------
     gname = "q4k_14336x4096_s2"
     gfmt, gn, gk, gseed, _ = workloads.WEIGHTS[gname]
@@ -262,42 +293,45 @@ def main():
     log(f"gemm m=512: step {t_gstep * 1e6:.1f} us ({flops / t_gstep / 1e12:.1f} TFLOP/s), "
         f"kernel {t_gkern * 1e6:.1f} us ({flops / t_gkern / 1e12:.1f} TFLOP/s)")
     gw.release()
+    return gemm
 
+
+def cpu_part(fmt, wbytes, n, k, x_host, y_gpu, weight_bytes, args):
     # ---- CPU baseline: the reference's AVX2 path on this host ------------------------
-    cpu = None
-    if not args.no_cpu:
-        import oracle
+    import numpy as np
 
-        threads = min(16, os.cpu_count() or 1)
-        got = oracle.baseline_packed_matmul(fmt, wbytes, n, k, x_host, threads)  # warm-up
-        err = float(np.max(np.abs(got - y_gpu)))
-        reps = 0
-        t0 = time.perf_counter()
-        while reps < 10 or (time.perf_counter() - t0 < args.cpu_seconds and reps < 1000):
-            oracle.baseline_packed_matmul(fmt, wbytes, n, k, x_host, threads)
-            reps += 1
-        t_cpu = (time.perf_counter() - t0) / reps
-        t1_reps = 0
-        t0 = time.perf_counter()
-        while t1_reps < 3 or (time.perf_counter() - t0 < args.cpu_seconds / 4 and t1_reps < 50):
-            oracle.baseline_packed_matmul(fmt, wbytes, n, k, x_host, 1)
-            t1_reps += 1
-        t_cpu1 = (time.perf_counter() - t0) / t1_reps
-        cpu = {
-            "value": round(weight_bytes / t_cpu / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": (f"Q4_K x[1,4096] . W[14336,4096]^T, int8 activations, AVX2 column kernels + "
-                       f"pool chunking; 1 warm-up + {reps} timed calls ({t_cpu * 1e3:.2f} ms/call)"),
-            "single_thread_GBps": round(weight_bytes / t_cpu1 / 1e9, 2),
-            "cpu_model": cpu_model(),
-            "max_abs_diff_vs_gpu": err,
-        }
-        log(f"cpu baseline ({threads} threads, {cpu_model()}): {t_cpu * 1e3:.2f} ms/call, "
-            f"{cpu['value']} GB/s; 1 thread {cpu['single_thread_GBps']} GB/s; max|gpu-cpu| {err:.2e}")
+    import oracle
 
-    for h in copies:
-        h.release()
-    ctx.close()
+    threads = min(16, os.cpu_count() or 1)
+    got = oracle.baseline_packed_matmul(fmt, wbytes, n, k, x_host, threads)  # warm-up
+    err = float(np.max(np.abs(got - y_gpu)))
+    reps = 0
+    t0 = time.perf_counter()
+    while reps < 10 or (time.perf_counter() - t0 < args.cpu_seconds and reps < 1000):
+        oracle.baseline_packed_matmul(fmt, wbytes, n, k, x_host, threads)
+        reps += 1
+    t_cpu = (time.perf_counter() - t0) / reps
+    t1_reps = 0
+    t0 = time.perf_counter()
+    while t1_reps < 3 or (time.perf_counter() - t0 < args.cpu_seconds / 4 and t1_reps < 50):
+        oracle.baseline_packed_matmul(fmt, wbytes, n, k, x_host, 1)
+        t1_reps += 1
+    t_cpu1 = (time.perf_counter() - t0) / t1_reps
+    cpu = {
+        "value": round(weight_bytes / t_cpu / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+        "sample": (f"Q4_K x[1,4096] . W[14336,4096]^T, int8 activations, AVX2 column kernels + "
+                   f"pool chunking; 1 warm-up + {reps} timed calls ({t_cpu * 1e3:.2f} ms/call)"),
+        "single_thread_GBps": round(weight_bytes / t_cpu1 / 1e9, 2),
+        "cpu_model": cpu_model(),
+        "max_abs_diff_vs_gpu": err,
+    }
+    log(f"cpu baseline ({threads} threads, {cpu_model()}): {t_cpu * 1e3:.2f} ms/call, "
+        f"{cpu['value']} GB/s; 1 thread {cpu['single_thread_GBps']} GB/s; max|gpu-cpu| {err:.2e}")
+    return cpu
 
+
+def emit(args, value, steps, warmup, ms_per_step, n, k, weight_bytes, use_graph, step_runner, achieved, kernel_us,
+         cpu, gemm, extra):
     line = {
         "metric": METRIC,
         "value": round(value, 2),

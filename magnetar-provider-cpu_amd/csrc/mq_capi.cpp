@@ -45,6 +45,8 @@ struct mq_ctx {
   void* io = nullptr;
   size_t io_bytes = 0;
   int gemv_splits_override = 0;
+  int gemv_variant = 0;
+  int gemm_variant = 0;
   std::mutex err_mu;
   std::unordered_map<std::thread::id, std::string> errors;
 };
@@ -125,12 +127,12 @@ int check_k(mq_ctx* ctx, const Weight& w, uint64_t k) {
 
 size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 
-int gemv_splits(mq_ctx* ctx, const Weight& w) {
+int gemv_splits(mq_ctx* ctx, const Weight& w, uint64_t m, bool int8) {
   if (ctx->gemv_splits_override > 0) {
     int s = ctx->gemv_splits_override;
-    return s > 8 ? 8 : s;
+    return s > 16 ? 16 : s;
   }
-  return mq::gemv_default_splits(w.rows, w.nb);
+  return mq::gemv_default_splits(w.rows, w.nb, m, int8 ? ctx->gemv_variant : 1);
 }
 
 constexpr uint64_t kGemvMaxRows = 8;
@@ -161,10 +163,10 @@ int matmul_locked(mq_ctx* ctx, const Weight& w, const float* x, uint64_t m, uint
       auto* sums = reinterpret_cast<int32_t*>(base + vb + sb);
       mq::launch_quantize_activations(x, m, k, values, scales, sums, nullptr, 1, stream);
       mq::launch_gemv_int8(static_cast<int>(w.type), w.dev, w.rows, w.nb, values, scales, sums, m, y, addend,
-                           addend_stride, gemv_splits(ctx, w), stream);
+                           addend_stride, gemv_splits(ctx, w, m, true), ctx->gemv_variant, stream);
     } else {
       mq::launch_gemv_f32(static_cast<int>(w.type), w.dev, w.rows, w.nb, x, m, y, addend, addend_stride,
-                          gemv_splits(ctx, w), stream);
+                          gemv_splits(ctx, w, m, false), stream);
     }
   } else {
     rc = acquire_workspace(ctx, stream, align256(m * k * 2));
@@ -174,7 +176,8 @@ int matmul_locked(mq_ctx* ctx, const Weight& w, const float* x, uint64_t m, uint
       mq::launch_quantize_activations(x, m, k, nullptr, nullptr, nullptr, a16, 1, stream);
     else
       mq::launch_activations_f16(x, m, k, a16, stream);
-    mq::launch_gemm(static_cast<int>(w.type), w.dev, w.rows, w.nb, a16, m, y, addend, addend_stride, stream);
+    mq::launch_gemm(static_cast<int>(w.type), w.dev, w.rows, w.nb, a16, m, y, addend, addend_stride,
+                    ctx->gemm_variant, stream);
   }
   MQ_HIP(ctx, hipGetLastError());
   return MQ_OK;
@@ -206,6 +209,8 @@ int mq_create(int device, mq_ctx** out) {
   }
   ctx->ws_stream = ctx->stream;
   if (const char* s = std::getenv("MQ_GEMV_SPLITS")) ctx->gemv_splits_override = std::atoi(s);
+  if (const char* s = std::getenv("MQ_GEMV_VARIANT")) ctx->gemv_variant = std::atoi(s);
+  if (const char* s = std::getenv("MQ_GEMM_VARIANT")) ctx->gemm_variant = std::atoi(s);
   *out = ctx;
   return MQ_OK;
 }
@@ -418,7 +423,7 @@ int mq_matmul_prequantized_dev(mq_ctx* ctx, uint64_t handle, const int8_t* value
   DeviceGuard guard(ctx->device);
   hipStream_t s = static_cast<hipStream_t>(stream);
   mq::launch_gemv_int8(static_cast<int>(w->type), w->dev, w->rows, w->nb, values_dev, scales_dev, sums_dev, m, y_dev,
-                       nullptr, 0, gemv_splits(ctx, *w), s);
+                       nullptr, 0, gemv_splits(ctx, *w, m, true), ctx->gemv_variant, s);
   MQ_HIP(ctx, hipGetLastError());
   return MQ_OK;
 }
@@ -452,7 +457,8 @@ int mq_matmul_f16_dev(mq_ctx* ctx, uint64_t handle, const uint16_t* a16_dev, uin
   if (!a16_dev || !y_dev) return fail(ctx, MQ_ERR_ARGUMENT, "mq_matmul_f16_dev: null pointer");
   DeviceGuard guard(ctx->device);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  mq::launch_gemm(static_cast<int>(w->type), w->dev, w->rows, w->nb, a16_dev, m, y_dev, nullptr, 0, s);
+  mq::launch_gemm(static_cast<int>(w->type), w->dev, w->rows, w->nb, a16_dev, m, y_dev, nullptr, 0,
+                  ctx->gemm_variant, s);
   MQ_HIP(ctx, hipGetLastError());
   return MQ_OK;
 }

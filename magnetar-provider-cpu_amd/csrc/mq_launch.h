@@ -30,11 +30,13 @@ void launch_activations_f16(const float* x, uint64_t m, uint64_t k, uint16_t* a1
 // The matmul kernels write y[i][n] = product [+ addend[i * addend_stride + n]]
 // (addend may be null; stride 0 broadcasts one row, as a bias).
 
-// Decode GEMV, m in 1..8, int8 activations.
+// Decode GEMV, m in 1..8, int8 activations. variant 1: 8 lanes per row
+// (any m); variant 2: one row per lane, activations through scalar loads
+// (m <= 4); 0: choose. `splits` = waves per work-group.
 void launch_gemv_int8(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb,
                       const int8_t* values, const float* scales, const int32_t* sums,
                       uint64_t m, float* y, const float* addend, uint64_t addend_stride, int splits,
-                      hipStream_t stream);
+                      int variant, hipStream_t stream);
 
 // Decode GEMV, m in 1..8, f32 activations.
 void launch_gemv_f32(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb,
@@ -42,11 +44,14 @@ void launch_gemv_f32(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb,
                      int splits, hipStream_t stream);
 
 // Prefill GEMM on MFMA: y[m][rows] = a16[m][K] . dequant(W)^T, f32 out.
+// variant 1: B dequantized through LDS (128 x 128 tiles); 2, 3, 4: B in
+// registers with 128 x 256, 128 x 128 and 64 x 256 tiles; 0: choose.
 void launch_gemm(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb,
                  const uint16_t* a16, uint64_t m, float* y, const float* addend, uint64_t addend_stride,
-                 hipStream_t stream);
+                 int variant, hipStream_t stream);
+int gemm_default_variant(uint64_t rows, uint64_t m);
 
 // Grid-shape helper for the GEMV (waves per work-group).
-int gemv_default_splits(uint64_t rows, uint64_t nb);
+int gemv_default_splits(uint64_t rows, uint64_t nb, uint64_t m, int variant);
 
 }  // namespace mq

@@ -1,0 +1,204 @@
+"""The Provider-side contract of the GPU packed-weight matmul Kernel, ported
+from the reference's own executor tests (src/native/tests.rs:251-331) and
+the fused-epilogue tests (src/tests.rs:740-888)."""
+
+import numpy as np
+import pytest
+
+import magnetar_gpu as mg
+import oracle
+from helpers import IQ4_XS, Q4_K, activations, assert_close_reference, assert_row_tolerance, packed
+from magnetar_gpu import executor as ex
+
+
+# ---- CPU-side -----------------------------------------------------------------
+
+def test_kernel_advertisements_under_the_gpu_identity():
+    """`provider_identity_is_distinct` (src/native/tests.rs:315-331): matmul is
+    advertised, every advertisement under this Provider's identity, with the
+    reference's f32 / contiguous / Host / TimeoutOnly shape."""
+    ads = ex.kernel_advertisements()
+    names = {a["name"] for a in ads}
+    assert {"matmul", "matmul-bias", "matmul-residual"} <= names
+    for a in ads:
+        assert a["provider"] == "magnetar-provider-gpu-mi355x"
+        assert a["provider"] != "magnetar-provider-cpu-reference"
+        assert a["input_dtypes"] == ["f32"] and a["output_dtypes"] == ["f32"]
+        assert a["layouts"] == ["Contiguous"] and a["memory_classes"] == ["Host"]
+        assert a["cancellation"] == "TimeoutOnly"
+        assert a["conformance_profile"] == "reference-cpu-conformance-v1"
+    assert [a["rank"] for a in ads if a["name"] == "matmul"] == [2]
+
+
+def test_executor_without_a_device_reports_an_error():
+    """No GPU: creation fails with a structured error, nothing aborts."""
+    torch = pytest.importorskip("torch")
+    if torch.cuda.device_count() > 0:
+        pytest.skip("a GPU is present")
+    with pytest.raises(ex.ExecutorError) as e:
+        ex.GpuExecutor(0)
+    assert e.value.code == ex.ERR_DEVICE
+
+
+# ---- GPU ------------------------------------------------------------------------
+
+gpu = pytest.mark.gpu
+
+
+@pytest.fixture
+def executor():
+    e = ex.GpuExecutor(0, packed_weights=True, int8_activations=True)
+    yield e
+    e.close()
+
+
+@gpu
+def test_executor_stores_packed_weights(executor):
+    """`executor_stores_packed_weights` (src/native/tests.rs:251-274)."""
+    w = packed(Q4_K, 4, 256, 41)
+    assert executor.write_packed_weight_tensor("w", Q4_K, 4, 256, w)
+    assert executor.is_packed("w")
+    got = executor.read_tensor("w")
+    exp = oracle.dequantize(Q4_K, w, 4, 256).T
+    np.testing.assert_array_equal(got.view(np.uint32), np.ascontiguousarray(exp).view(np.uint32))
+    assert executor.resident_shape("w") == [256, 4]
+    assert executor.materializations() == 1
+    assert executor.release_tensor("w")
+    assert not executor.is_packed("w")
+    declining = ex.GpuExecutor(0, packed_weights=False)
+    try:
+        assert not declining.write_packed_weight_tensor("w", Q4_K, 4, 256, w)
+    finally:
+        declining.close()
+    # formats without a GPU path and input-major weights are declined too
+    assert not executor.write_packed_weight_tensor("q8", 8, 2, 32, np.zeros(2 * 34, np.uint8))
+    assert not executor.write_packed_weight_tensor("t", Q4_K, 4, 256, w, transposed=False)
+
+
+@gpu
+def test_packed_weights_yield_to_f32_writes_and_admission(executor):
+    """`packed_weights_survive_opaque_writes_and_yield_to_copies`
+    (src/native/tests.rs:276-313) for the writes this executor takes: an f32
+    write replaces the packed weight; a denied admission leaves it resident."""
+    w = packed(Q4_K, 2, 256, 43)
+    assert executor.write_packed_weight_tensor("w", Q4_K, 2, 256, w)
+    assert executor.read_tensor_value_is_opaque("w")
+    replacement = np.full((256, 2), 0.5, np.float32)
+    executor.write_tensor_admitted("w", replacement)
+    assert not executor.is_packed("w")
+    np.testing.assert_array_equal(executor.read_tensor("w"), replacement)
+    small = ex.GpuExecutor(0, memory_capacity=1024)
+    try:
+        assert small.write_packed_weight_tensor("w", Q4_K, 2, 256, w)
+        with pytest.raises(ex.ExecutorError) as e:
+            small.write_tensor_admitted("w", replacement)
+        assert e.value.code == ex.MEMORY_DENIED
+        assert small.is_packed("w")
+    finally:
+        small.close()
+
+
+@gpu
+@pytest.mark.parametrize("fmt", [Q4_K, IQ4_XS])
+@pytest.mark.parametrize("int8", [True, False])
+def test_submitted_matmul_matches_reference_cpu(fmt, int8):
+    """A `matmul` Kernel invocation through submit/complete, reading a packed
+    weight: mode-matched against the dense oracle (src/native/tests.rs:134-154)."""
+    e = ex.GpuExecutor(0, int8_activations=int8)
+    try:
+        k, n = 512, 37
+        w = packed(fmt, n, k, 21)
+        assert e.write_packed_weight_tensor("w", fmt, n, k, w)
+        dense_t = oracle.dequantize(fmt, w, n, k)
+        for m in (1, 3, 9):
+            a = activations(m, k, m)
+            e.write_tensor("a", a)
+            h = e.submit_kernel("matmul", f"inv{m}", ["a", "w"], "y")
+            r = e.complete_kernel(h)
+            assert r.succeeded, r.reason
+            got = e.read_tensor("y")
+            exp = oracle.matmul_dense(oracle.int8_rounded(a) if int8 else a, dense_t, False, True)
+            assert_row_tolerance(got, exp, f"m {m}")
+            if m <= 8:
+                assert_close_reference(got, exp, f"m {m}")
+    finally:
+        e.close()
+
+
+@gpu
+def test_fused_epilogues_equal_their_unfused_pairs(executor):
+    """`matmul-bias` / `matmul-residual` bit-identical to matmul then add
+    (src/tests.rs:740-888): the product is rounded before the addition."""
+    k, n = 512, 64
+    w = mg.quantize(Q4_K, mg.gaussian(3, 0.02, n * k).reshape(n, k))
+    executor.write_packed_weight_tensor("w", Q4_K, n, k, w)
+    for m in (1, 4, 12):
+        a = mg.gaussian(10 + m, 1.0, m * k).reshape(m, k)
+        executor.write_tensor("a", a)
+        executor.complete_kernel(executor.submit_kernel("matmul", "p", ["a", "w"], "y"))
+        y = executor.read_tensor("y")
+        bias = mg.gaussian(20 + m, 1.0, n)
+        residual = mg.gaussian(30 + m, 1.0, m * n).reshape(m, n)
+        for kernel, extra, shape in (("matmul-bias", bias, (n,)), ("matmul-bias", bias.reshape(1, n), (1, n)),
+                                     ("matmul-residual", residual, (m, n))):
+            executor.write_tensor("x2", extra.reshape(shape))
+            r = executor.complete_kernel(executor.submit_kernel(kernel, "f", ["a", "w", "x2"], "z"))
+            assert r.succeeded, r.reason
+            exp = (y + extra.reshape(1, n) if extra.size == n else residual + y).astype(np.float32)
+            np.testing.assert_array_equal(executor.read_tensor("z"), exp)
+
+
+@gpu
+def test_transpose_a_takes_the_f32_path(executor):
+    """`transpose_a` expands to the dense f32 matmul in the reference
+    (src/native/mod.rs:221-222): f32 activations, read transposed."""
+    k, n, m = 256, 16, 3
+    w = packed(Q4_K, n, k, 8)
+    executor.write_packed_weight_tensor("w", Q4_K, n, k, w)
+    a_t = activations(k, m, 2)  # stored [k, m]
+    executor.write_tensor("a", a_t)
+    r = executor.complete_kernel(executor.submit_kernel("matmul", "t", ["a", "w"], "y", {"transpose_a": "true"}))
+    assert r.succeeded, r.reason
+    exp = oracle.matmul_dense(a_t, oracle.dequantize(Q4_K, w, n, k), True, True)
+    assert_close_reference(executor.read_tensor("y"), exp)
+
+
+@gpu
+def test_kernel_errors_and_single_completion(executor):
+    """Deadline 0 -> KernelTimeout before dispatch; f16 accumulation rejected
+    (src/lib.rs:2445-2456); unknown Kernel; a second completion of one handle
+    is rejected (src/lib.rs:2337-2356); a column mismatch carries the
+    reference's reason text."""
+    w = packed(Q4_K, 8, 256, 1)
+    executor.write_packed_weight_tensor("w", Q4_K, 8, 256, w)
+    executor.write_tensor("a", activations(1, 256, 1))
+    h = executor.submit_kernel("matmul", "d0", ["a", "w"], "y", deadline_millis=0)
+    assert executor.complete_kernel(h).error == ex.KERNEL_TIMEOUT
+    with pytest.raises(ex.ExecutorError) as e:
+        executor.complete_kernel(h)
+    assert e.value.code == ex.UNKNOWN
+    h = executor.submit_kernel("matmul", "f16", ["a", "w"], "y", {"accumulation_dtype": "f16"})
+    assert executor.complete_kernel(h).error == ex.KERNEL_DTYPE_UNSUPPORTED
+    h = executor.submit_kernel("softmax", "s", ["a"], "y")
+    assert executor.complete_kernel(h).error == ex.KERNEL_NOT_FOUND
+    executor.write_tensor("b", activations(1, 512, 1))
+    r = executor.complete_kernel(executor.submit_kernel("matmul", "k", ["b", "w"], "y"))
+    assert r.error == ex.KERNEL_EXECUTION_FAILED and "512 columns" in r.reason
+    kinds = [k for k, _ in executor.observations()]
+    assert kinds[:2] == ["ProviderRegistered", "DeviceDetected"]
+    assert "KernelTimeout" in kinds and "KernelDispatchFailed" in kinds
+
+
+@gpu
+def test_output_admission_denial_does_not_store(executor):
+    small = ex.GpuExecutor(0, memory_capacity=16)
+    try:
+        w = packed(Q4_K, 8, 256, 1)
+        small.write_packed_weight_tensor("w", Q4_K, 8, 256, w)
+        small.write_tensor("a", activations(1, 256, 1))
+        r = small.complete_kernel(small.submit_kernel("matmul", "big", ["a", "w"], "y"))
+        assert r.error == ex.KERNEL_EXECUTION_FAILED and "admission denied" in r.reason
+        assert small.read_tensor("y") is None
+        assert ("KernelMemoryFeasibilityFailed", "matmul") in small.observations()
+    finally:
+        small.close()
