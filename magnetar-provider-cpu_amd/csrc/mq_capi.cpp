@@ -44,6 +44,13 @@ struct mq_ctx {
   // Host-pointer staging for mq_matmul.
   void* io = nullptr;
   size_t io_bytes = 0;
+  // Split-K arrival counters and partials of the decode GEMV: `sk_counters`
+  // u32 counters at the front (zeroed at allocation; every launch leaves
+  // them zero), partials after them.
+  void* sk = nullptr;
+  size_t sk_bytes = 0;
+  uint64_t sk_counters = 0;
+  int gemv_ksplit_override = 0;
   int gemv_splits_override = 0;
   int gemv_variant = 0;
   int gemm_variant = 0;
@@ -95,12 +102,18 @@ class DeviceGuard {
 
 // Makes `stream` the workspace's stream, ordering it after work queued on
 // the previous one, and grows the workspace to `bytes`. Caller holds ctx->mu.
-int acquire_workspace(mq_ctx* ctx, hipStream_t stream, size_t bytes) {
+int order_stream(mq_ctx* ctx, hipStream_t stream) {
   if (ctx->ws_stream != stream) {
     MQ_HIP(ctx, hipEventRecord(ctx->ws_event, ctx->ws_stream));
     MQ_HIP(ctx, hipStreamWaitEvent(stream, ctx->ws_event, 0));
     ctx->ws_stream = stream;
   }
+  return MQ_OK;
+}
+
+int acquire_workspace(mq_ctx* ctx, hipStream_t stream, size_t bytes) {
+  int rc = order_stream(ctx, stream);
+  if (rc) return rc;
   if (bytes <= ctx->ws_bytes) return MQ_OK;
   MQ_HIP(ctx, hipStreamSynchronize(stream));
   if (ctx->ws) MQ_HIP(ctx, hipFree(ctx->ws));
@@ -109,6 +122,40 @@ int acquire_workspace(mq_ctx* ctx, hipStream_t stream, size_t bytes) {
   size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
   MQ_HIP(ctx, hipMalloc(&ctx->ws, want));
   ctx->ws_bytes = want;
+  return MQ_OK;
+}
+
+// The GEMV's split-K buffers for `w` and m rows (ks == 1: none). Caller
+// holds ctx->mu and has ordered `stream` (order_stream).
+int acquire_splitk(mq_ctx* ctx, hipStream_t stream, const Weight& w, uint64_t m, mq::GemvSplitK& sk) {
+  sk = mq::GemvSplitK{};
+  sk.ks = ctx->gemv_ksplit_override > 0 ? ctx->gemv_ksplit_override : mq::gemv_default_ksplit(w.rows, w.nb);
+  if (sk.ks > 16) sk.ks = 16;
+  if (static_cast<uint64_t>(sk.ks) > w.nb) sk.ks = static_cast<int>(w.nb);
+  if (sk.ks <= 1) {
+    sk.ks = 1;
+    return MQ_OK;
+  }
+  const uint64_t blocks = (w.rows + 63) / 64;
+  const size_t partials = static_cast<size_t>(sk.ks) * m * 2 * blocks * 64 * sizeof(float);
+  if (blocks > ctx->sk_counters || ctx->sk_counters * sizeof(uint32_t) + partials > ctx->sk_bytes) {
+    // grow: the counter region keeps a fixed capacity between growths, so a
+    // smaller weight's partials never land on another weight's counters
+    MQ_HIP(ctx, hipStreamSynchronize(stream));
+    if (ctx->sk) MQ_HIP(ctx, hipFree(ctx->sk));
+    ctx->sk = nullptr;
+    ctx->sk_bytes = 0;
+    ctx->sk_counters = 0;
+    const uint64_t cap = (blocks + 1023) / 1024 * 1024;
+    const size_t want = cap * sizeof(uint32_t) + 16ull * 8 * 2 * cap * 64 * sizeof(float);
+    MQ_HIP(ctx, hipMalloc(&ctx->sk, want));
+    MQ_HIP(ctx, hipMemset(ctx->sk, 0, want));
+    MQ_HIP(ctx, hipDeviceSynchronize());  // zeroed before any stream's kernel reads it
+    ctx->sk_bytes = want;
+    ctx->sk_counters = cap;
+  }
+  sk.counters = static_cast<uint32_t*>(ctx->sk);
+  sk.partials = reinterpret_cast<float*>(static_cast<uint8_t*>(ctx->sk) + ctx->sk_counters * sizeof(uint32_t));
   return MQ_OK;
 }
 
@@ -153,7 +200,18 @@ int matmul_locked(mq_ctx* ctx, const Weight& w, const float* x, uint64_t m, uint
   if (!addend) addend_rows = 0;
   const bool int8 = (flags & MQ_INT8_ACTIVATIONS) != 0;
   if (m <= kGemvMaxRows) {
+    mq::GemvSplitK sk;
     if (int8) {
+      rc = order_stream(ctx, stream);
+      if (!rc) rc = acquire_splitk(ctx, stream, w, m, sk);
+      if (rc) return rc;
+    }
+    const bool fused = int8 && ctx->gemv_variant == 0 &&
+                       mq::launch_gemv_fused(static_cast<int>(w.type), w.dev, w.rows, w.nb, x, m, y, addend,
+                                             addend_stride, ctx->gemv_splits_override, sk, stream);
+    if (fused) {
+      // one launch: quantized into LDS and multiplied
+    } else if (int8) {
       const size_t vb = align256(m * k), sb = align256(m * k / 32 * 4), hb = align256(m * k / 32 * 8);
       rc = acquire_workspace(ctx, stream, vb + sb + hb);
       if (rc) return rc;
@@ -163,7 +221,7 @@ int matmul_locked(mq_ctx* ctx, const Weight& w, const float* x, uint64_t m, uint
       auto* sums = reinterpret_cast<int32_t*>(base + vb + sb);
       mq::launch_quantize_activations(x, m, k, values, scales, sums, nullptr, 1, stream);
       mq::launch_gemv_int8(static_cast<int>(w.type), w.dev, w.rows, w.nb, values, scales, sums, m, y, addend,
-                           addend_stride, gemv_splits(ctx, w, m, true), ctx->gemv_variant, stream);
+                           addend_stride, ctx->gemv_splits_override, ctx->gemv_variant, sk, stream);
     } else {
       mq::launch_gemv_f32(static_cast<int>(w.type), w.dev, w.rows, w.nb, x, m, y, addend, addend_stride,
                           gemv_splits(ctx, w, m, false), stream);
@@ -209,6 +267,7 @@ int mq_create(int device, mq_ctx** out) {
   }
   ctx->ws_stream = ctx->stream;
   if (const char* s = std::getenv("MQ_GEMV_SPLITS")) ctx->gemv_splits_override = std::atoi(s);
+  if (const char* s = std::getenv("MQ_GEMV_KSPLIT")) ctx->gemv_ksplit_override = std::atoi(s);
   if (const char* s = std::getenv("MQ_GEMV_VARIANT")) ctx->gemv_variant = std::atoi(s);
   if (const char* s = std::getenv("MQ_GEMM_VARIANT")) ctx->gemm_variant = std::atoi(s);
   *out = ctx;
@@ -222,6 +281,7 @@ void mq_destroy(mq_ctx* ctx) {
   for (auto& kv : ctx->weights) (void)hipFree(kv.second.dev);
   if (ctx->ws) (void)hipFree(ctx->ws);
   if (ctx->io) (void)hipFree(ctx->io);
+  if (ctx->sk) (void)hipFree(ctx->sk);
   (void)hipEventDestroy(ctx->ws_event);
   (void)hipStreamDestroy(ctx->stream);
   delete ctx;
@@ -422,8 +482,12 @@ int mq_matmul_prequantized_dev(mq_ctx* ctx, uint64_t handle, const int8_t* value
     return fail(ctx, MQ_ERR_ARGUMENT, "mq_matmul_prequantized_dev: null pointer");
   DeviceGuard guard(ctx->device);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  mq::GemvSplitK sk;
+  rc = order_stream(ctx, s);
+  if (!rc) rc = acquire_splitk(ctx, s, *w, m, sk);
+  if (rc) return rc;
   mq::launch_gemv_int8(static_cast<int>(w->type), w->dev, w->rows, w->nb, values_dev, scales_dev, sums_dev, m, y_dev,
-                       nullptr, 0, gemv_splits(ctx, *w, m, true), ctx->gemv_variant, s);
+                       nullptr, 0, ctx->gemv_splits_override, ctx->gemv_variant, sk, s);
   MQ_HIP(ctx, hipGetLastError());
   return MQ_OK;
 }

@@ -131,43 +131,61 @@ __device__ inline int sat_i8(float v) {
   return static_cast<int>(v);
 }
 
+// Four values of one 32-value block; the block's 8 lanes are consecutive
+// and all execute this together (the shuffles stay inside the 8).
+struct Quant4 {
+  int q0, q1, q2, q3;
+  float d;
+  int half_sum;  // sum of q over this lane's 16-value half
+  int run_sum;   // sum of q over the 32 values
+};
+
+__device__ inline Quant4 quantize4(float4 v) {
+  Quant4 r;
+  float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+  for (int o = 1; o < 8; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 8));
+  amax = fmaxf(0.0f, amax);
+  r.d = amax / 127.0f;
+  r.q0 = r.q1 = r.q2 = r.q3 = 0;
+  if (amax != 0.0f) {
+    r.q0 = sat_i8(rintf(v.x / r.d));
+    r.q1 = sat_i8(rintf(v.y / r.d));
+    r.q2 = sat_i8(rintf(v.z / r.d));
+    r.q3 = sat_i8(rintf(v.w / r.d));
+  }
+  int hs = r.q0 + r.q1 + r.q2 + r.q3;
+  hs += __shfl_xor(hs, 1, 8);
+  hs += __shfl_xor(hs, 2, 8);
+  r.half_sum = hs;
+  r.run_sum = hs + __shfl_xor(hs, 4, 8);
+  return r;
+}
+
+__device__ inline uint32_t pack_q4(const Quant4& q) {
+  return (static_cast<uint32_t>(q.q0) & 0xFFu) | ((static_cast<uint32_t>(q.q1) & 0xFFu) << 8) |
+         ((static_cast<uint32_t>(q.q2) & 0xFFu) << 16) | (static_cast<uint32_t>(q.q3) << 24);
+}
+
 __global__ void quantize_act_kernel(const float* __restrict__ x, uint64_t total,
                                     int8_t* __restrict__ values, float* __restrict__ scales,
                                     int32_t* __restrict__ sums, uint16_t* __restrict__ a16, int int8) {
   uint64_t t = blockIdx.x * static_cast<uint64_t>(blockDim.x) + threadIdx.x;
   bool active = t < total / 4;
   float4 v = active ? reinterpret_cast<const float4*>(x)[t] : make_float4(0.f, 0.f, 0.f, 0.f);
-  float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-  for (int o = 1; o < 8; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 8));
-  amax = fmaxf(0.0f, amax);
-  float d = amax / 127.0f;
-  int q0 = 0, q1 = 0, q2 = 0, q3 = 0;
-  if (amax != 0.0f) {
-    q0 = sat_i8(rintf(v.x / d));
-    q1 = sat_i8(rintf(v.y / d));
-    q2 = sat_i8(rintf(v.z / d));
-    q3 = sat_i8(rintf(v.w / d));
-  }
-  int hs = q0 + q1 + q2 + q3;
-  hs += __shfl_xor(hs, 1, 8);
-  hs += __shfl_xor(hs, 2, 8);
+  const Quant4 q = quantize4(v);
   if (!active) return;
-  if (values) {
-    uint32_t packed = (static_cast<uint32_t>(q0) & 0xFFu) | ((static_cast<uint32_t>(q1) & 0xFFu) << 8) |
-                      ((static_cast<uint32_t>(q2) & 0xFFu) << 16) | (static_cast<uint32_t>(q3) << 24);
-    reinterpret_cast<uint32_t*>(values)[t] = packed;
-  }
+  if (values) reinterpret_cast<uint32_t*>(values)[t] = pack_q4(q);
   int sub = static_cast<int>(t & 7);
   uint64_t blk = t >> 3;
-  if (scales && sub == 0) scales[blk] = d;
-  if (sums && (sub & 3) == 0) sums[2 * blk + (sub >> 2)] = hs;
+  if (scales && sub == 0) scales[blk] = q.d;
+  if (sums && (sub & 3) == 0) sums[2 * blk + (sub >> 2)] = q.half_sum;
   if (a16) {
     float f0, f1, f2, f3;
     if (int8) {
-      f0 = static_cast<float>(q0) * d;
-      f1 = static_cast<float>(q1) * d;
-      f2 = static_cast<float>(q2) * d;
-      f3 = static_cast<float>(q3) * d;
+      f0 = static_cast<float>(q.q0) * q.d;
+      f1 = static_cast<float>(q.q1) * q.d;
+      f2 = static_cast<float>(q.q2) * q.d;
+      f3 = static_cast<float>(q.q3) * q.d;
     } else {
       f0 = v.x;
       f1 = v.y;
@@ -578,18 +596,148 @@ __global__ __launch_bounds__(512) void gemv_rows_iq4xs_int8_kernel(
 // LDS bytes: m * (k + 8 * k / 32) for Q4_K, m * (k + 4 * k / 32) for IQ4_XS.
 // ---------------------------------------------------------------------------
 
+// Split-K epilogue across work-groups, deterministic: each work-group
+// writes its (acc, mins) for its 64 rows to partials[ks], then takes a
+// ticket on its row block's counter; the work-group that takes the last
+// ticket adds the KS partials in ks order, writes y and resets the counter
+// to zero for the next call. No work-group waits on another.
+//
+// Visibility without an L2 flush: the partials are written and read with
+// relaxed agent-scope atomic stores/loads (global_store/load ... sc1, which
+// are coherent across the XCDs' L2s), and the stores are waited on
+// (s_waitcnt vmcnt(0)) before the ticket is taken, so every partial is at
+// the coherence point before its work-group's ticket. A release/acquire
+// fence at agent scope would do the same for plain stores, but costs a
+// write-back and an invalidation of the whole L2 (buffer_wbl2 / buffer_inv),
+// which stalls every other work-group on the XCD.
+constexpr int kWaitVmcnt0 = 0x0F70;  // s_waitcnt vmcnt(0) expcnt(7) lgkmcnt(15): stores only
+
+template <int M>
+__device__ inline void splitk_finish(float (&acc)[M], float (&mins)[M], uint64_t rows, float* y,
+                                     const float* addend, uint64_t addend_stride, float* partials,
+                                     uint32_t* counters, int KS) {
+  const int lane = threadIdx.x & 63;
+  const uint64_t rb = blockIdx.x, ks = blockIdx.y;
+  const uint64_t rows64 = static_cast<uint64_t>(gridDim.x) * 64;
+  const uint64_t row = rb * 64 + lane;
+  // layout: partials[ks][m][2][rows64]
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    __hip_atomic_store(&partials[((ks * M + m) * 2 + 0) * rows64 + row], acc[m], __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&partials[((ks * M + m) * 2 + 1) * rows64 + row], mins[m], __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+  uint32_t ticket = 0;
+  if (lane == 0) ticket = __hip_atomic_fetch_add(&counters[rb], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  ticket = __shfl(ticket, 0);
+  if (ticket != static_cast<uint32_t>(KS - 1)) return;
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    float a = 0.0f, mn = 0.0f;
+    for (int i = 0; i < KS; ++i) {
+      a += __hip_atomic_load(&partials[((i * M + m) * 2 + 0) * rows64 + row], __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+      mn += __hip_atomic_load(&partials[((i * M + m) * 2 + 1) * rows64 + row], __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (row < rows) {
+      float v = a - mn;
+      if (addend) v = v + addend[m * addend_stride + row];
+      y[m * rows + row] = v;
+    }
+  }
+  if (lane == 0) __hip_atomic_store(&counters[rb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Cross-wave (within a work-group) reduction through the kernel's dynamic
+// LDS, then either the store of y (KS == 1) or the split-K epilogue.
+template <int M>
+__device__ inline void finish_rows(float (&acc)[M], float (&mins)[M], uint64_t rows, float* y, const float* addend,
+                                   uint64_t addend_stride, float* red, float* partials, uint32_t* counters, int KS) {
+  const int lane = threadIdx.x & 63, s = threadIdx.x >> 6, S = blockDim.x >> 6;
+  if (S > 1) {
+    __syncthreads();  // every wave is done reading activations
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      red[((s * M + m) * 2 + 0) * 64 + lane] = acc[m];
+      red[((s * M + m) * 2 + 1) * 64 + lane] = mins[m];
+    }
+    __syncthreads();
+    if (s != 0) return;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      float a = red[(m * 2 + 0) * 64 + lane], mn = red[(m * 2 + 1) * 64 + lane];
+      for (int i = 1; i < S; ++i) {
+        a += red[((i * M + m) * 2 + 0) * 64 + lane];
+        mn += red[((i * M + m) * 2 + 1) * 64 + lane];
+      }
+      acc[m] = a;
+      mins[m] = mn;
+    }
+  }
+  if (KS > 1) {
+    splitk_finish<M>(acc, mins, rows, y, addend, addend_stride, partials, counters, KS);
+    return;
+  }
+  const uint64_t row = static_cast<uint64_t>(blockIdx.x) * 64 + lane;
+  if (row >= rows) return;
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    float v = acc[m] - mins[m];
+    if (addend) v = v + addend[m * addend_stride + row];
+    y[m * rows + row] = v;
+  }
+}
+
+// The fused form: quantize the work-group's K range [k0, k0 + kn) of m rows
+// of f32 activations straight into LDS with the same per-block arithmetic
+// as quantize_act_kernel (bit-identical values, scales and sums). Every
+// thread runs the same number of iterations so the 8-lane groups shuffle
+// together. LDS: int8 [m][kn], then per run f32 (d) or (d, d * sum).
+template <int TYPE, int M>
+__device__ inline void stage_quantized(const float* __restrict__ xf, uint64_t K, uint64_t k0, int kn,
+                                       uint8_t* lds) {
+  const int n4 = M * kn / 4, per_row4 = kn / 4;
+  float* rs = reinterpret_cast<float*>(lds + M * kn);
+  for (int i0 = 0; i0 < n4; i0 += blockDim.x) {
+    const int i = i0 + static_cast<int>(threadIdx.x);
+    const bool act = i < n4;
+    const int m = act ? i / per_row4 : 0, c4 = act ? i - m * per_row4 : 0;
+    const float4 v = act ? *reinterpret_cast<const float4*>(xf + m * K + k0 + 4 * c4) : make_float4(0.f, 0.f, 0.f, 0.f);
+    const Quant4 q = quantize4(v);
+    if (!act) continue;
+    reinterpret_cast<uint32_t*>(lds)[i] = pack_q4(q);
+    if ((i & 7) == 0) {
+      const int run = i >> 3;  // m * (kn / 32) + run within the range
+      if (TYPE == kTypeQ4K) {
+        rs[2 * run] = q.d;
+        rs[2 * run + 1] = q.d * static_cast<float>(q.run_sum);
+      } else {
+        rs[run] = q.d;
+      }
+    }
+  }
+}
+
 template <int TYPE, int M>
 __device__ inline void stage_activations(const int8_t* __restrict__ xv, const float* __restrict__ xs,
-                                         const int32_t* __restrict__ xsum, uint64_t K, uint8_t* lds) {
-  const int runs = static_cast<int>(K / 32);
-  const int n16 = static_cast<int>(M * K / 16);
-  for (int i = threadIdx.x; i < n16; i += blockDim.x)
-    reinterpret_cast<uint4*>(lds)[i] = reinterpret_cast<const uint4*>(xv)[i];
-  float* rs = reinterpret_cast<float*>(lds + M * K);
-  for (int i = threadIdx.x; i < M * runs; i += blockDim.x) {
-    const float d = xs[i];
+                                         const int32_t* __restrict__ xsum, uint64_t K, uint64_t k0, int kn,
+                                         uint8_t* lds) {
+  const int per_row16 = kn / 16, kruns = kn / 32;
+  const int runs = static_cast<int>(K / 32), r0 = static_cast<int>(k0 / 32);
+  for (int i = threadIdx.x; i < M * per_row16; i += blockDim.x) {
+    const int m = i / per_row16, c = i - m * per_row16;
+    reinterpret_cast<uint4*>(lds)[i] = *reinterpret_cast<const uint4*>(xv + m * K + k0 + 16 * c);
+  }
+  float* rs = reinterpret_cast<float*>(lds + M * kn);
+  for (int i = threadIdx.x; i < M * kruns; i += blockDim.x) {
+    const int m = i / kruns, u = i - m * kruns;
+    const int src = m * runs + r0 + u;
+    const float d = xs[src];
     if (TYPE == kTypeQ4K) {
-      const int2 sm = reinterpret_cast<const int2*>(xsum)[i];
+      const int2 sm = reinterpret_cast<const int2*>(xsum)[src];
       rs[2 * i] = d;
       rs[2 * i + 1] = d * static_cast<float>(sm.x + sm.y);
     } else {
@@ -598,47 +746,72 @@ __device__ inline void stage_activations(const int8_t* __restrict__ xv, const fl
   }
 }
 
-template <int M>
-__global__ __launch_bounds__(1024) void gemv_lds_q4k_int8_kernel(
+// ---------------------------------------------------------------------------
+// Decode GEMV, row-per-lane with the activations staged in LDS (m <= 8).
+// Grid: (row blocks of 64 stored rows) x KS K-splits. A work-group takes
+// the super-blocks [b0, b1) of its split, its waves interleaved over them
+// (wave s: b0 + s, b0 + s + S, ...). It first stages its K range of the
+// activations in LDS (int8 values + two f32 per run, d_act and
+// d_act * (s0 + s1)) -- or quantizes them there itself (FUSED) -- while the
+// first block's weight loads are in flight; the block loop reads them as
+// LDS broadcasts. Per run the integer dot is scaled by the 6-bit scale in
+// integer arithmetic (exact), then by d_act in f32; d and dmin once per
+// block.
+// ---------------------------------------------------------------------------
+
+struct SplitK {
+  float* partials;
+  uint32_t* counters;
+  int ks;
+};
+
+template <int M, bool FUSED>
+__global__ __launch_bounds__(M <= 4 ? 1024 : 512) void gemv_lds_q4k_int8_kernel(
     const uint8_t* __restrict__ w, int nb, uint64_t rows, const int8_t* __restrict__ xv,
-    const float* __restrict__ xs, const int32_t* __restrict__ xsum, float* __restrict__ y,
-    const float* __restrict__ addend, uint64_t addend_stride) {
+    const float* __restrict__ xs, const int32_t* __restrict__ xsum, const float* __restrict__ xf,
+    float* __restrict__ y, const float* __restrict__ addend, uint64_t addend_stride, SplitK sk) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int lane = threadIdx.x & 63;
   const int s = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int S = blockDim.x >> 6;
+  // balanced partition of the super-blocks: every split gets >= 1 (ks <= nb)
+  const int b0 = static_cast<int>(blockIdx.y * nb / sk.ks), b1 = static_cast<int>((blockIdx.y + 1) * nb / sk.ks);
   const uint64_t g = static_cast<uint64_t>(blockIdx.x) * 8 + (lane >> 3);
   const bool live = g < (rows + 7) / 8;
   const int r = lane & 7;
   const uint64_t K = static_cast<uint64_t>(nb) * 256;
-  const int runs = nb * 8;
+  const int kn = (b1 - b0) * 256, kruns = kn / 32;
   const uint8_t* base = w + g * nb * kQ4kTileBytes + r * 16;
   uint4 nhdr = make_uint4(0, 0, 0, 0), nq[8];
 #pragma unroll
   for (int p = 0; p < 8; ++p) nq[p] = make_uint4(0, 0, 0, 0);
-  if (live && s < nb) {
-    const uint8_t* tile = base + static_cast<uint64_t>(s) * kQ4kTileBytes;
+  if (live && b0 + s < b1) {
+    const uint8_t* tile = base + static_cast<uint64_t>(b0 + s) * kQ4kTileBytes;
     nhdr = ld16(tile);
 #pragma unroll
     for (int p = 0; p < 8; ++p) nq[p] = ld16(tile + 128 * (p + 1));
   }
-  stage_activations<kTypeQ4K, M>(xv, xs, xsum, K, lds);
+  if (FUSED)
+    stage_quantized<kTypeQ4K, M>(xf, K, static_cast<uint64_t>(b0) * 256, kn, lds);
+  else
+    stage_activations<kTypeQ4K, M>(xv, xs, xsum, K, static_cast<uint64_t>(b0) * 256, kn, lds);
   __syncthreads();
-  const float2* rs = reinterpret_cast<const float2*>(lds + M * K);
+  const float2* rs = reinterpret_cast<const float2*>(lds + M * kn);
   float acc[M], mins[M];
 #pragma unroll
   for (int m = 0; m < M; ++m) acc[m] = mins[m] = 0.0f;
-  for (int b = s; b < nb; b += S) {
+  for (int b = b0 + s; b < b1; b += S) {
     const uint4 hdr = nhdr;
     uint4 q[8];
 #pragma unroll
     for (int p = 0; p < 8; ++p) q[p] = nq[p];
-    if (live && b + S < nb) {
+    if (live && b + S < b1) {
       const uint8_t* tile = base + static_cast<uint64_t>(b + S) * kQ4kTileBytes;
       nhdr = ld16(tile);
 #pragma unroll
       for (int p = 0; p < 8; ++p) nq[p] = ld16(tile + 128 * (p + 1));
     }
+    const int bl = b - b0;  // block within the staged range
     const Q4kSixBit six = q4k_six_bit(hdr);
     float accb[M], minb[M];
 #pragma unroll
@@ -657,7 +830,7 @@ __global__ __launch_bounds__(1024) void gemv_lds_q4k_int8_kernel(
                                 (qq.z >> 4) & 0x0F0F0F0Fu, (qq.w >> 4) & 0x0F0F0F0Fu};
 #pragma unroll
         for (int m = 0; m < M; ++m) {
-          const uint4* xa = reinterpret_cast<const uint4*>(lds + m * K + b * 256 + 64 * c + 16 * h);
+          const uint4* xa = reinterpret_cast<const uint4*>(lds + m * kn + bl * 256 + 64 * c + 16 * h);
           const uint4 x0 = xa[0], x1 = xa[2];
           dlo[m] = sdot4(lo[0], x0.x, dlo[m]);
           dlo[m] = sdot4(lo[1], x0.y, dlo[m]);
@@ -674,7 +847,7 @@ __global__ __launch_bounds__(1024) void gemv_lds_q4k_int8_kernel(
       q4k_sc_m(six, 2 * c + 1, sc1, m1);
 #pragma unroll
       for (int m = 0; m < M; ++m) {
-        const float2 r0 = rs[m * runs + b * 8 + 2 * c], r1 = rs[m * runs + b * 8 + 2 * c + 1];
+        const float2 r0 = rs[m * kruns + bl * 8 + 2 * c], r1 = rs[m * kruns + bl * 8 + 2 * c + 1];
         accb[m] = fmaf(static_cast<float>(__mul24(dlo[m], static_cast<int>(sc0))), r0.x, accb[m]);
         accb[m] = fmaf(static_cast<float>(__mul24(dhi[m], static_cast<int>(sc1))), r1.x, accb[m]);
         minb[m] = fmaf(static_cast<float>(m0), r0.y, minb[m]);
@@ -688,51 +861,58 @@ __global__ __launch_bounds__(1024) void gemv_lds_q4k_int8_kernel(
       mins[m] = fmaf(dmin, minb[m], mins[m]);
     }
   }
-  reduce_waves_and_store<M>(acc, mins, rows, y, addend, addend_stride);
+  finish_rows<M>(acc, mins, rows, y, addend, addend_stride, reinterpret_cast<float*>(lds), sk.partials,
+                 sk.counters, sk.ks);
 }
 
-template <int M>
-__global__ __launch_bounds__(1024) void gemv_lds_iq4xs_int8_kernel(
+template <int M, bool FUSED>
+__global__ __launch_bounds__(M <= 4 ? 1024 : 512) void gemv_lds_iq4xs_int8_kernel(
     const uint8_t* __restrict__ w, int nb, uint64_t rows, const int8_t* __restrict__ xv,
-    const float* __restrict__ xs, float* __restrict__ y, const float* __restrict__ addend,
-    uint64_t addend_stride) {
+    const float* __restrict__ xs, const float* __restrict__ xf, float* __restrict__ y,
+    const float* __restrict__ addend, uint64_t addend_stride, SplitK sk) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int lane = threadIdx.x & 63;
   const int s = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int S = blockDim.x >> 6;
+  // balanced partition of the super-blocks: every split gets >= 1 (ks <= nb)
+  const int b0 = static_cast<int>(blockIdx.y * nb / sk.ks), b1 = static_cast<int>((blockIdx.y + 1) * nb / sk.ks);
   const uint64_t g = static_cast<uint64_t>(blockIdx.x) * 8 + (lane >> 3);
   const bool live = g < (rows + 7) / 8;
   const int r = lane & 7;
   const uint64_t K = static_cast<uint64_t>(nb) * 256;
-  const int runs = nb * 8;
+  const int kn = (b1 - b0) * 256, kruns = kn / 32;
   const uint8_t* base = w + g * nb * kIq4xsTileBytes;
   uint2 nhdr = make_uint2(0, 0);
   uint4 nq[8];
 #pragma unroll
   for (int p = 0; p < 8; ++p) nq[p] = make_uint4(0, 0, 0, 0);
-  if (live && s < nb) {
-    const uint8_t* tile = base + static_cast<uint64_t>(s) * kIq4xsTileBytes;
+  if (live && b0 + s < b1) {
+    const uint8_t* tile = base + static_cast<uint64_t>(b0 + s) * kIq4xsTileBytes;
     nhdr = ld8(tile + r * 8);
 #pragma unroll
     for (int p = 0; p < 8; ++p) nq[p] = ld16(tile + 64 + 128 * p + r * 16);
   }
-  stage_activations<kTypeIq4Xs, M>(xv, xs, nullptr, K, lds);
+  if (FUSED)
+    stage_quantized<kTypeIq4Xs, M>(xf, K, static_cast<uint64_t>(b0) * 256, kn, lds);
+  else
+    stage_activations<kTypeIq4Xs, M>(xv, xs, nullptr, K, static_cast<uint64_t>(b0) * 256, kn, lds);
   __syncthreads();
-  const float* rs = reinterpret_cast<const float*>(lds + M * K);
+  const float* rs = reinterpret_cast<const float*>(lds + M * kn);
   float acc[M], mins[M];
 #pragma unroll
   for (int m = 0; m < M; ++m) acc[m] = mins[m] = 0.0f;
-  for (int b = s; b < nb; b += S) {
+  for (int b = b0 + s; b < b1; b += S) {
     const uint2 hdr = nhdr;
     uint4 q[8];
 #pragma unroll
     for (int p = 0; p < 8; ++p) q[p] = nq[p];
-    if (live && b + S < nb) {
+    if (live && b + S < b1) {
       const uint8_t* tile = base + static_cast<uint64_t>(b + S) * kIq4xsTileBytes;
       nhdr = ld8(tile + r * 8);
 #pragma unroll
       for (int p = 0; p < 8; ++p) nq[p] = ld16(tile + 64 + 128 * p + r * 16);
     }
+    const int bl = b - b0;
     float accb[M];
 #pragma unroll
     for (int m = 0; m < M; ++m) accb[m] = 0.0f;
@@ -746,7 +926,7 @@ __global__ __launch_bounds__(1024) void gemv_lds_iq4xs_int8_kernel(
                               iq4_lookup4((qq.z >> 4) & 0x0F0F0F0Fu), iq4_lookup4((qq.w >> 4) & 0x0F0F0F0Fu)};
 #pragma unroll
       for (int m = 0; m < M; ++m) {
-        const uint4* xa = reinterpret_cast<const uint4*>(lds + m * K + b * 256 + 32 * j);
+        const uint4* xa = reinterpret_cast<const uint4*>(lds + m * kn + bl * 256 + 32 * j);
         const uint4 x0 = xa[0], x1 = xa[1];
         int dot = sdot4(lo[0], x0.x, 0);
         dot = sdot4(lo[1], x0.y, dot);
@@ -756,14 +936,15 @@ __global__ __launch_bounds__(1024) void gemv_lds_iq4xs_int8_kernel(
         dot = sdot4(hi[1], x1.y, dot);
         dot = sdot4(hi[2], x1.z, dot);
         dot = sdot4(hi[3], x1.w, dot);
-        accb[m] = fmaf(static_cast<float>(__mul24(dot, ls)), rs[m * runs + b * 8 + j], accb[m]);
+        accb[m] = fmaf(static_cast<float>(__mul24(dot, ls)), rs[m * kruns + bl * 8 + j], accb[m]);
       }
     }
     const float d = half_bits(hdr.x);
 #pragma unroll
     for (int m = 0; m < M; ++m) acc[m] = fmaf(d, accb[m], acc[m]);
   }
-  reduce_waves_and_store<M>(acc, mins, rows, y, addend, addend_stride);
+  finish_rows<M>(acc, mins, rows, y, addend, addend_stride, reinterpret_cast<float*>(lds), sk.partials,
+                 sk.counters, sk.ks);
 }
 
 // f32 activations: per run half, sum(q * x) and sum(x) in f32, then
@@ -1028,12 +1209,115 @@ __global__ __launch_bounds__(256) void gemm_kernel(const uint8_t* __restrict__ w
 // fragments from the tiled bytes straight into MFMA operand registers (f32
 // scale * q - min, rounded once to f16), so B never touches LDS. The f16
 // activation tile is the only LDS traffic: double-buffered, one barrier per
-// 64-wide K-step (one Q4_K quant chunk = two runs).
+// 64-wide K-step (one Q4_K quant chunk = two runs). The weight bytes of the
+// next super-block (4 K-steps) are in flight while the current one is
+// multiplied, to cover HBM latency.
 //
 // Operand lanes: lane = i + 16 * kq holds rows/columns i and k = 8 kq .. 8 kq + 7
 // of the 32-wide MFMA K, for A and B alike; the weight bytes 8 kq .. 8 kq + 7
 // of a chunk give run 2c's k-slot (low nibbles) and run 2c+1's (high).
 // ---------------------------------------------------------------------------
+
+// One lane's raw weight bytes for one super-block and NF fragments.
+template <int TYPE, int NF>
+struct RawB {
+  uint4 hdr[NF];
+  uint2 qa[4][NF];  // Q4_K: chunk c bytes 8kq..8kq+7; IQ4_XS: run 2c's 8 index bytes
+  uint2 qb[4][NF];  // IQ4_XS: run 2c+1's 8 index bytes (unused for Q4_K)
+};
+
+template <int TYPE, int NF>
+__device__ inline void load_raw_b(RawB<TYPE, NF>& r, const uint8_t* const (&tile0)[NF], const bool (&live)[NF],
+                                  uint64_t b, int kq) {
+#pragma unroll
+  for (int f = 0; f < NF; ++f) {
+    if (!live[f]) {
+      r.hdr[f] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) r.qa[c][f] = r.qb[c][f] = make_uint2(0, 0);
+      continue;
+    }
+    const uint8_t* tile = tile0[f] + b * tile_bytes(TYPE);
+    if (TYPE == kTypeQ4K) {
+      r.hdr[f] = ld16(tile);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) r.qa[c][f] = ld8(tile + 128 * (1 + 2 * c + (kq >> 1)) + 8 * (kq & 1));
+    } else {
+      // tile0 points at this row's header; planes start 64 bytes into the
+      // tile at 16 bytes per row (the row index is folded into tile0).
+      const uint2 h = ld8(tile);
+      r.hdr[f] = make_uint4(h.x, h.y, 0, 0);
+    }
+  }
+}
+
+template <int NF>
+__device__ inline void load_raw_b_iq4(RawB<kTypeIq4Xs, NF>& r, const uint8_t* const (&planes0)[NF],
+                                      const bool (&live)[NF], uint64_t b) {
+#pragma unroll
+  for (int f = 0; f < NF; ++f) {
+    if (!live[f]) continue;
+    const uint8_t* pl = planes0[f] + b * kIq4xsTileBytes;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      r.qa[c][f] = ld8(pl + 128 * (2 * c));
+      r.qb[c][f] = ld8(pl + 128 * (2 * c + 1));
+    }
+  }
+}
+
+template <int TYPE, int NF, int C>
+__device__ inline void dequant_b(const RawB<TYPE, NF>& r, int kq, half8 (&bop)[2][NF]) {
+#pragma unroll
+  for (int f = 0; f < NF; ++f) {
+    uint32_t p0[4], p1[4];
+    if (TYPE == kTypeQ4K) {
+      const Q4kSixBit six = q4k_six_bit(r.hdr[f]);
+      uint32_t sc0, mm0, sc1, mm1;
+      q4k_sc_m(six, 2 * C, sc0, mm0);
+      q4k_sc_m(six, 2 * C + 1, sc1, mm1);
+      const float d = half_bits(r.hdr[f].x), dmin = half_bits(r.hdr[f].x >> 16);
+      const float s0 = d * static_cast<float>(sc0), s1 = d * static_cast<float>(sc1);
+      const float n0m = -(dmin * static_cast<float>(mm0)), n1m = -(dmin * static_cast<float>(mm1));
+      const uint2 qa = r.qa[C][f];
+      const uint32_t lo[2] = {qa.x & 0x0F0F0F0Fu, qa.y & 0x0F0F0F0Fu};
+      const uint32_t hi[2] = {(qa.x >> 4) & 0x0F0F0F0Fu, (qa.y >> 4) & 0x0F0F0F0Fu};
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        p0[2 * t] = pack_f16x2(fmaf(s0, static_cast<float>(lo[t] & 0xFFu), n0m),
+                               fmaf(s0, static_cast<float>((lo[t] >> 8) & 0xFFu), n0m));
+        p0[2 * t + 1] = pack_f16x2(fmaf(s0, static_cast<float>((lo[t] >> 16) & 0xFFu), n0m),
+                                   fmaf(s0, static_cast<float>(lo[t] >> 24), n0m));
+        p1[2 * t] = pack_f16x2(fmaf(s1, static_cast<float>(hi[t] & 0xFFu), n1m),
+                               fmaf(s1, static_cast<float>((hi[t] >> 8) & 0xFFu), n1m));
+        p1[2 * t + 1] = pack_f16x2(fmaf(s1, static_cast<float>((hi[t] >> 16) & 0xFFu), n1m),
+                                   fmaf(s1, static_cast<float>(hi[t] >> 24), n1m));
+      }
+    } else {
+      const uint2 h2 = make_uint2(r.hdr[f].x, r.hdr[f].y);
+      const float d = half_bits(h2.x);
+      const float sa = d * static_cast<float>(iq4xs_ls(h2, 2 * C));
+      const float sb = d * static_cast<float>(iq4xs_ls(h2, 2 * C + 1));
+      const int sh = 4 * (kq >> 1);  // low nibbles hold weights 0..15, high 16..31
+      const uint2 qa = r.qa[C][f], qb = r.qb[C][f];
+      const uint32_t ia[2] = {iq4_lookup4((qa.x >> sh) & 0x0F0F0F0Fu), iq4_lookup4((qa.y >> sh) & 0x0F0F0F0Fu)};
+      const uint32_t ib[2] = {iq4_lookup4((qb.x >> sh) & 0x0F0F0F0Fu), iq4_lookup4((qb.y >> sh) & 0x0F0F0F0Fu)};
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        p0[2 * t] = pack_f16x2(sa * static_cast<float>(static_cast<int8_t>(ia[t] & 0xFFu)),
+                               sa * static_cast<float>(static_cast<int8_t>((ia[t] >> 8) & 0xFFu)));
+        p0[2 * t + 1] = pack_f16x2(sa * static_cast<float>(static_cast<int8_t>((ia[t] >> 16) & 0xFFu)),
+                                   sa * static_cast<float>(static_cast<int8_t>(ia[t] >> 24)));
+        p1[2 * t] = pack_f16x2(sb * static_cast<float>(static_cast<int8_t>(ib[t] & 0xFFu)),
+                               sb * static_cast<float>(static_cast<int8_t>((ib[t] >> 8) & 0xFFu)));
+        p1[2 * t + 1] = pack_f16x2(sb * static_cast<float>(static_cast<int8_t>((ib[t] >> 16) & 0xFFu)),
+                                   sb * static_cast<float>(static_cast<int8_t>(ib[t] >> 24)));
+      }
+    }
+    bop[0][f] = *reinterpret_cast<half8*>(p0);
+    bop[1][f] = *reinterpret_cast<half8*>(p1);
+  }
+}
 
 template <int TYPE, int MF, int NF>
 __global__ __launch_bounds__(256) void gemm_rb_kernel(const uint8_t* __restrict__ w, int nb, uint64_t rows,
@@ -1057,15 +1341,19 @@ __global__ __launch_bounds__(256) void gemm_rb_kernel(const uint8_t* __restrict_
 #pragma unroll
     for (int f = 0; f < NF; ++f) acc[i][f] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  // this lane's weight row per fragment
-  const uint8_t* wrow[NF];
+  // this lane's weight row per fragment: header address in super-block 0,
+  // and (IQ4_XS) the start of its quant planes
+  const uint8_t* tile0[NF];
+  const uint8_t* planes0[NF];
   bool wlive[NF];
 #pragma unroll
   for (int f = 0; f < NF; ++f) {
     const uint64_t n = n0 + 16 * f + li;
     wlive[f] = n < rows_padded;
     const uint64_t nn = wlive[f] ? n : 0;
-    wrow[f] = w + (nn >> 3) * nb * tile_bytes(TYPE) + (nn & 7) * (TYPE == kTypeQ4K ? 16 : 8);
+    const uint8_t* t = w + (nn >> 3) * nb * tile_bytes(TYPE);
+    tile0[f] = t + (nn & 7) * (TYPE == kTypeQ4K ? 16 : 8);
+    planes0[f] = t + 64 + (nn & 7) * 16 + 8 * (kq & 1);
   }
 
   auto load_a = [&](int kb, uint4 (&regs)[A_CHUNKS]) {
@@ -1085,107 +1373,18 @@ __global__ __launch_bounds__(256) void gemm_rb_kernel(const uint8_t* __restrict_
     }
   };
 
-  // raw B bytes for one K-step: Q4_K: 8 quant bytes per fragment (+ the
-  // 16-byte header, reloaded at each new super-block); IQ4_XS: 8 index bytes
-  // of each of the two runs (+ the 8-byte header).
-  uint4 hdr[NF];
-  uint2 qa[NF], qb[NF];
-  auto load_b = [&](int kb) {
-    const int b = kb >> 2, c = kb & 3;
-#pragma unroll
-    for (int f = 0; f < NF; ++f) {
-      const uint8_t* tile = wrow[f] + static_cast<uint64_t>(b) * tile_bytes(TYPE);
-      if (!wlive[f]) {
-        qa[f] = qb[f] = make_uint2(0, 0);
-        if (c == 0) hdr[f] = make_uint4(0, 0, 0, 0);
-        continue;
-      }
-      if (TYPE == kTypeQ4K) {
-        if (c == 0) hdr[f] = ld16(tile);
-        qa[f] = ld8(tile + 128 * (1 + 2 * c + (kq >> 1)) + 8 * (kq & 1));
-      } else {
-        if (c == 0) {
-          const uint2 h = ld8(tile);
-          hdr[f] = make_uint4(h.x, h.y, 0, 0);
-        }
-        // wrow points at this row's 8 header bytes; the quant planes start
-        // 64 bytes into the tile, 16 bytes per row.
-        const int rsub = static_cast<int>((n0 + 16 * f + li) & 7);
-        const uint8_t* planes = tile - rsub * 8 + 64 + rsub * 16 + 8 * (kq & 1);
-        qa[f] = ld8(planes + 128 * (2 * c));
-        qb[f] = ld8(planes + 128 * (2 * c + 1));
-      }
-    }
-  };
-
+  RawB<TYPE, NF> cur, nxt;
+  load_raw_b<TYPE, NF>(nxt, tile0, wlive, 0, kq);
+  if (TYPE == kTypeIq4Xs) load_raw_b_iq4<NF>(reinterpret_cast<RawB<kTypeIq4Xs, NF>&>(nxt), planes0, wlive, 0);
   uint4 areg[A_CHUNKS];
   load_a(0, areg);
   store_a(0, areg);
-  load_b(0);
   __syncthreads();
 
-  for (int kb = 0; kb < ksteps; ++kb) {
+  auto kstep = [&](int kb, const half8 (&bop)[2][NF]) {
     const int buf = kb & 1;
-    const int c = kb & 3;
-    // dequantize this step's B fragments into operand registers
-    half8 bop[2][NF];
-#pragma unroll
-    for (int f = 0; f < NF; ++f) {
-      if (TYPE == kTypeQ4K) {
-        const Q4kSixBit six = q4k_six_bit(hdr[f]);
-        uint32_t sc0, mm0, sc1, mm1;
-        q4k_sc_m(six, 2 * c, sc0, mm0);
-        q4k_sc_m(six, 2 * c + 1, sc1, mm1);
-        const float d = half_bits(hdr[f].x), dmin = half_bits(hdr[f].x >> 16);
-        const float s0 = d * static_cast<float>(sc0), s1 = d * static_cast<float>(sc1);
-        const float n0m = -(dmin * static_cast<float>(mm0)), n1m = -(dmin * static_cast<float>(mm1));
-        uint32_t lo[2] = {qa[f].x & 0x0F0F0F0Fu, qa[f].y & 0x0F0F0F0Fu};
-        uint32_t hi[2] = {(qa[f].x >> 4) & 0x0F0F0F0Fu, (qa[f].y >> 4) & 0x0F0F0F0Fu};
-        uint32_t p0[4], p1[4];
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          p0[2 * t] = pack_f16x2(fmaf(s0, static_cast<float>(lo[t] & 0xFFu), n0m),
-                                 fmaf(s0, static_cast<float>((lo[t] >> 8) & 0xFFu), n0m));
-          p0[2 * t + 1] = pack_f16x2(fmaf(s0, static_cast<float>((lo[t] >> 16) & 0xFFu), n0m),
-                                     fmaf(s0, static_cast<float>(lo[t] >> 24), n0m));
-          p1[2 * t] = pack_f16x2(fmaf(s1, static_cast<float>(hi[t] & 0xFFu), n1m),
-                                 fmaf(s1, static_cast<float>((hi[t] >> 8) & 0xFFu), n1m));
-          p1[2 * t + 1] = pack_f16x2(fmaf(s1, static_cast<float>((hi[t] >> 16) & 0xFFu), n1m),
-                                     fmaf(s1, static_cast<float>(hi[t] >> 24), n1m));
-        }
-        bop[0][f] = *reinterpret_cast<half8*>(p0);
-        bop[1][f] = *reinterpret_cast<half8*>(p1);
-      } else {
-        const uint2 h2 = make_uint2(hdr[f].x, hdr[f].y);
-        const float d = half_bits(h2.x);
-        const float sa = d * static_cast<float>(iq4xs_ls(h2, 2 * c));
-        const float sb = d * static_cast<float>(iq4xs_ls(h2, 2 * c + 1));
-        const int sh = 4 * (kq >> 1);  // low nibbles hold weights 0..15, high 16..31
-        uint32_t ia[2] = {iq4_lookup4((qa[f].x >> sh) & 0x0F0F0F0Fu), iq4_lookup4((qa[f].y >> sh) & 0x0F0F0F0Fu)};
-        uint32_t ib[2] = {iq4_lookup4((qb[f].x >> sh) & 0x0F0F0F0Fu), iq4_lookup4((qb[f].y >> sh) & 0x0F0F0F0Fu)};
-        uint32_t p0[4], p1[4];
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          p0[2 * t] = pack_f16x2(sa * static_cast<float>(static_cast<int8_t>(ia[t] & 0xFFu)),
-                                 sa * static_cast<float>(static_cast<int8_t>((ia[t] >> 8) & 0xFFu)));
-          p0[2 * t + 1] = pack_f16x2(sa * static_cast<float>(static_cast<int8_t>((ia[t] >> 16) & 0xFFu)),
-                                     sa * static_cast<float>(static_cast<int8_t>(ia[t] >> 24)));
-          p1[2 * t] = pack_f16x2(sb * static_cast<float>(static_cast<int8_t>(ib[t] & 0xFFu)),
-                                 sb * static_cast<float>(static_cast<int8_t>((ib[t] >> 8) & 0xFFu)));
-          p1[2 * t + 1] = pack_f16x2(sb * static_cast<float>(static_cast<int8_t>((ib[t] >> 16) & 0xFFu)),
-                                     sb * static_cast<float>(static_cast<int8_t>(ib[t] >> 24)));
-        }
-        bop[0][f] = *reinterpret_cast<half8*>(p0);
-        bop[1][f] = *reinterpret_cast<half8*>(p1);
-      }
-    }
-    // prefetch the next step's A tile and B bytes
     const bool more = kb + 1 < ksteps;
-    if (more) {
-      load_a(kb + 1, areg);
-      load_b(kb + 1);
-    }
-    // 2 runs x MF x NF MFMAs from the current A buffer
+    if (more) load_a(kb + 1, areg);
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
 #pragma unroll
@@ -1198,6 +1397,25 @@ __global__ __launch_bounds__(256) void gemm_rb_kernel(const uint8_t* __restrict_
     }
     if (more) store_a(buf ^ 1, areg);
     __syncthreads();
+  };
+
+  for (int b = 0; b < nb; ++b) {
+    cur = nxt;
+    if (b + 1 < nb) {
+      load_raw_b<TYPE, NF>(nxt, tile0, wlive, static_cast<uint64_t>(b + 1), kq);
+      if (TYPE == kTypeIq4Xs)
+        load_raw_b_iq4<NF>(reinterpret_cast<RawB<kTypeIq4Xs, NF>&>(nxt), planes0, wlive,
+                           static_cast<uint64_t>(b + 1));
+    }
+    half8 bop[2][NF];
+    dequant_b<TYPE, NF, 0>(cur, kq, bop);
+    kstep(4 * b + 0, bop);
+    dequant_b<TYPE, NF, 1>(cur, kq, bop);
+    kstep(4 * b + 1, bop);
+    dequant_b<TYPE, NF, 2>(cur, kq, bop);
+    kstep(4 * b + 2, bop);
+    dequant_b<TYPE, NF, 3>(cur, kq, bop);
+    kstep(4 * b + 3, bop);
   }
 
 #pragma unroll
@@ -1262,7 +1480,7 @@ void launch_activations_f16(const float* x, uint64_t m, uint64_t k, uint16_t* a1
 }
 
 int gemv_default_splits(uint64_t rows, uint64_t nb, uint64_t m, int variant) {
-  if (variant == 0) variant = m <= 4 ? 3 : 1;
+  if (variant == 0) variant = 3;
   if (variant >= 2) {
     // waves per 64-row group: split the super-blocks, at least one each
     int splits = 1;
@@ -1277,41 +1495,88 @@ int gemv_default_splits(uint64_t rows, uint64_t nb, uint64_t m, int variant) {
 
 #define MQ_GEMV_CASES(X) X(1) X(2) X(3) X(4) X(5) X(6) X(7) X(8)
 
+namespace {
+
+// Bytes of dynamic LDS the LDS-staged GEMV needs for a K range of nbk
+// super-blocks: the activations (int8 values + per-run f32) or the
+// cross-wave reduction, whichever is larger.
+size_t gemv_lds_bytes(int type, uint64_t nbk, uint64_t m, int splits) {
+  const size_t act = type == kTypeQ4K ? m * nbk * 256 + m * nbk * 8 * 8 : m * nbk * 256 + m * nbk * 8 * 4;
+  const size_t red = static_cast<size_t>(splits) * m * 2 * 64 * 4;
+  return act > red ? act : red;
+}
+
+int lds_form_max_splits(uint64_t m) { return m <= 4 ? 16 : 8; }  // launch bounds 1024 / 512
+
+template <bool FUSED>
+void launch_gemv_lds(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, const int8_t* values,
+                     const float* scales, const int32_t* sums, const float* x, uint64_t m, float* y,
+                     const float* addend, uint64_t addend_stride, int splits, const GemvSplitK& sk, size_t lds,
+                     hipStream_t stream) {
+  dim3 grid(static_cast<unsigned>((rows + 63) / 64), static_cast<unsigned>(sk.ks)), block(64 * splits);
+  const int inb = static_cast<int>(nb);
+  const SplitK k{sk.partials, sk.counters, sk.ks};
+  if (type == kTypeQ4K) {
+    switch (m) {
+#define X(MM)                                                                                               \
+  case MM:                                                                                                  \
+    hipLaunchKernelGGL((gemv_lds_q4k_int8_kernel<MM, FUSED>), grid, block, lds, stream, tiled, inb, rows, values, \
+                       scales, sums, x, y, addend, addend_stride, k);                                       \
+    break;
+      MQ_GEMV_CASES(X)
+#undef X
+      default:
+        break;
+    }
+  } else {
+    switch (m) {
+#define X(MM)                                                                                                 \
+  case MM:                                                                                                    \
+    hipLaunchKernelGGL((gemv_lds_iq4xs_int8_kernel<MM, FUSED>), grid, block, lds, stream, tiled, inb, rows, values, \
+                       scales, x, y, addend, addend_stride, k);                                               \
+    break;
+      MQ_GEMV_CASES(X)
+#undef X
+      default:
+        break;
+    }
+  }
+}
+
+// The LDS form's launch shape, or false when its LDS would exceed 64 KiB.
+bool lds_form_shape(int type, uint64_t rows, uint64_t nb, uint64_t m, int splits_hint, int ks, int& splits,
+                    size_t& lds) {
+  if (m < 1 || m > 8 || ks < 1) return false;
+  const uint64_t nbk = (nb + ks - 1) / ks;
+  splits = splits_hint;
+  if (splits < 1) {
+    splits = 1;
+    while (splits < 8 && static_cast<uint64_t>(2 * splits) <= nbk) splits *= 2;
+  }
+  if (splits > lds_form_max_splits(m)) splits = lds_form_max_splits(m);
+  lds = gemv_lds_bytes(type, nbk, m, splits);
+  return lds <= 65536;
+}
+
+}  // namespace
+
 void launch_gemv_int8(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, const int8_t* values,
                       const float* scales, const int32_t* sums, uint64_t m, float* y, const float* addend,
-                      uint64_t addend_stride, int splits, int variant, hipStream_t stream) {
+                      uint64_t addend_stride, int splits, int variant, const GemvSplitK& sk,
+                      hipStream_t stream) {
   const int inb = static_cast<int>(nb);
-  const size_t lds_need = type == kTypeQ4K ? m * nb * 256 + m * nb * 8 * 8 : m * nb * 256 + m * nb * 8 * 4;
-  if (variant == 0) variant = m <= 4 ? (lds_need <= 65536 ? 3 : 2) : 1;
-  if (variant == 3 && m <= 4 && lds_need <= 65536) {
-    dim3 grid(static_cast<unsigned>((rows + 63) / 64)), block(64 * splits);
-    if (type == kTypeQ4K) {
-      switch (m) {
-#define X(MM)                                                                                         \
-  case MM:                                                                                            \
-    hipLaunchKernelGGL(gemv_lds_q4k_int8_kernel<MM>, grid, block, lds_need, stream, tiled, inb, rows, \
-                       values, scales, sums, y, addend, addend_stride);                               \
-    break;
-        X(1) X(2) X(3) X(4)
-#undef X
-        default:
-          break;
-      }
-    } else {
-      switch (m) {
-#define X(MM)                                                                                           \
-  case MM:                                                                                              \
-    hipLaunchKernelGGL(gemv_lds_iq4xs_int8_kernel<MM>, grid, block, lds_need, stream, tiled, inb, rows, \
-                       values, scales, y, addend, addend_stride);                                       \
-    break;
-        X(1) X(2) X(3) X(4)
-#undef X
-        default:
-          break;
-      }
-    }
+  // Waves per work-group never exceed what each kernel is built for.
+  int lds_splits = 0;
+  size_t lds = 0;
+  const bool lds_fits = lds_form_shape(type, rows, nb, m, splits, sk.ks, lds_splits, lds);
+  if (variant == 0) variant = lds_fits ? 3 : (m <= 4 ? 2 : 1);
+  if (variant == 3 && lds_fits) {
+    launch_gemv_lds<false>(type, tiled, rows, nb, values, scales, sums, nullptr, m, y, addend, addend_stride,
+                           lds_splits, sk, lds, stream);
     return;
   }
+  if (splits < 1) splits = gemv_default_splits(rows, nb, m, variant);
+  splits = splits > 8 ? 8 : splits;  // the other forms: launch bound 512, 8 reduction slots
   if (variant >= 2 && m <= 4) {
     dim3 grid(static_cast<unsigned>((rows + 63) / 64)), block(64 * splits);
     if (type == kTypeQ4K) {
@@ -1369,8 +1634,31 @@ void launch_gemv_int8(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb
   }
 }
 
+bool launch_gemv_fused(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, const float* x, uint64_t m,
+                       float* y, const float* addend, uint64_t addend_stride, int splits, const GemvSplitK& sk,
+                       hipStream_t stream) {
+  int lds_splits = 0;
+  size_t lds = 0;
+  if (!lds_form_shape(type, rows, nb, m, splits, sk.ks, lds_splits, lds)) return false;
+  launch_gemv_lds<true>(type, tiled, rows, nb, nullptr, nullptr, nullptr, x, m, y, addend, addend_stride,
+                        lds_splits, sk, lds, stream);
+  return true;
+}
+
+// K-splits for the LDS form: only when the row blocks alone leave most of
+// the 256 CUs idle (4096 rows: 64 blocks -> 4 splits; 14336 rows: 224
+// blocks -> none, where the split-K epilogue costs more than the last 32
+// CUs would bring).
+int gemv_default_ksplit(uint64_t rows, uint64_t nb) {
+  const uint64_t blocks = (rows + 63) / 64;
+  int ks = 1;
+  while (blocks * 2 * ks <= 320 && static_cast<uint64_t>(2 * ks) <= nb && ks < 16) ks *= 2;
+  return ks;
+}
+
 void launch_gemv_f32(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, const float* x, uint64_t m,
                      float* y, const float* addend, uint64_t addend_stride, int splits, hipStream_t stream) {
+  splits = splits < 1 ? 1 : splits > 8 ? 8 : splits;  // launch bound 512, 8 reduction slots
   dim3 grid(static_cast<unsigned>((rows + 7) / 8)), block(64 * splits);
   const int inb = static_cast<int>(nb);
   if (type == kTypeQ4K) {

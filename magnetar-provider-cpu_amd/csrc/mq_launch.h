@@ -27,16 +27,35 @@ void launch_quantize_activations(const float* x, uint64_t m, uint64_t k, int8_t*
 void launch_activations_f16(const float* x, uint64_t m, uint64_t k, uint16_t* a16,
                             hipStream_t stream);
 
+// Split-K across work-groups for the LDS-staged GEMV: ks work-groups share
+// each 64-row block; partials holds ks * m * 2 * (row blocks * 64) f32 and
+// counters one zero-initialised u32 per row block (each launch leaves them
+// zero again). ks == 1 needs neither.
+struct GemvSplitK {
+  float* partials = nullptr;
+  uint32_t* counters = nullptr;
+  int ks = 1;
+};
+int gemv_default_ksplit(uint64_t rows, uint64_t nb);
+
 // The matmul kernels write y[i][n] = product [+ addend[i * addend_stride + n]]
 // (addend may be null; stride 0 broadcasts one row, as a bias).
 
 // Decode GEMV, m in 1..8, int8 activations. variant 1: 8 lanes per row
 // (any m); variant 2: one row per lane, activations through scalar loads
-// (m <= 4); 0: choose. `splits` = waves per work-group.
+// (m <= 4); 3: row per lane with the activations staged in LDS (m <= 8,
+// split-K per `sk`); 0: choose. `splits` = waves per work-group (< 1: choose).
 void launch_gemv_int8(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb,
                       const int8_t* values, const float* scales, const int32_t* sums,
                       uint64_t m, float* y, const float* addend, uint64_t addend_stride, int splits,
-                      int variant, hipStream_t stream);
+                      int variant, const GemvSplitK& sk, hipStream_t stream);
+
+// Decode GEMV with the int8 quantization fused in (m <= 8, LDS need <= 64 KiB):
+// the work-group quantizes x into LDS and multiplies, one launch. Returns
+// false (nothing launched) when the shape does not fit.
+bool launch_gemv_fused(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, const float* x,
+                       uint64_t m, float* y, const float* addend, uint64_t addend_stride, int splits,
+                       const GemvSplitK& sk, hipStream_t stream);
 
 // Decode GEMV, m in 1..8, f32 activations.
 void launch_gemv_f32(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb,

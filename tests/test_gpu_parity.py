@@ -336,3 +336,49 @@ def test_non_finite_activations(ctx):
             assert row_tolerance_violation(y8, exp) <= 1.0
     finally:
         h.release()
+
+
+# ---- every decode-GEMV form and K-split ------------------------------------------
+
+def _context_with(env):
+    """A Context whose launch choices are forced through the environment
+    (read once, at creation)."""
+    import os
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update({k: str(v) for k, v in env.items()})
+    try:
+        return mg.Context(0)
+    finally:
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+
+
+@pytest.mark.parametrize("fmt", [Q4_K, IQ4_XS])
+@pytest.mark.parametrize("variant,ksplit,splits", [(0, 1, 0), (0, 2, 0), (0, 3, 4), (0, 5, 8), (0, 16, 16),
+                                                   (3, 4, 2), (3, 7, 0), (2, 1, 8), (1, 1, 4)])
+def test_gemv_forms_and_k_splits(fmt, variant, ksplit, splits):
+    """Every decode form (fused, LDS-staged, row-per-lane, 8 lanes per row)
+    at K-splits that do and do not divide the super-block count (5 and 8
+    blocks), ragged row counts, m = 1..8: within the reference's tolerance
+    of the dense oracle, and bit-identical when repeated (the split-K
+    epilogue adds the partials in a fixed order)."""
+    c = _context_with({"MQ_GEMV_VARIANT": variant, "MQ_GEMV_KSPLIT": ksplit, "MQ_GEMV_SPLITS": splits})
+    try:
+        for n, k in ((1000, 2048), (37, 1280)):
+            w = mg.quantize(fmt, mg.gaussian(n + k, 0.02, n * k).reshape(n, k))
+            h = c.upload(fmt, n, k, w)
+            try:
+                for m in (1, 4, 5, 8):
+                    a = mg.gaussian(300 + m, 1.0, m * k).reshape(m, k)
+                    got = c.matmul(h, a)
+                    again = c.matmul(h, a)
+                    np.testing.assert_array_equal(got.view(np.uint32), again.view(np.uint32))
+                    exp = expected(fmt, w, n, k, a, True)
+                    assert_close_reference(got, exp, f"n {n} k {k} m {m}")
+            finally:
+                h.release()
+    finally:
+        c.close()
