@@ -99,4 +99,28 @@ __device__ inline int sdot4(uint32_t a, uint32_t b, int c) {
   return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), c, false);
 }
 
+// Raw buffer loads (MUBUF) over a wave-uniform base: an offset at or past
+// `bytes` reads zeros without a memory access. Kernels use this to issue a
+// fixed sequence of loads on every path (predicating by offset instead of
+// branching), which keeps the compiler's vmcnt waits exact.
+constexpr uint32_t kBufferDword3 = 0x00020000u;  // gfx9 raw buffer: 32-bit data format
+constexpr uint32_t kBufferNone = 0x80000000u;    // an offset past every resource this code builds
+
+__device__ inline __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes),
+                                           static_cast<int>(kBufferDword3));
+}
+
+__device__ inline uint4 buffer_ld16(__amdgpu_buffer_rsrc_t r, uint32_t offset) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(offset), 0, 0);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ inline uint2 buffer_ld8(__amdgpu_buffer_rsrc_t r, uint32_t offset) {
+  typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+  const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, static_cast<int>(offset), 0, 0);
+  return make_uint2(v.x, v.y);
+}
+
 }  // namespace mq

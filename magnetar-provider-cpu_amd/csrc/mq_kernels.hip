@@ -584,18 +584,6 @@ __global__ __launch_bounds__(512) void gemv_rows_iq4xs_int8_kernel(
   reduce_waves_and_store<M>(acc, mins, rows, y, addend, addend_stride);
 }
 
-// ---------------------------------------------------------------------------
-// Decode GEMV, row-per-lane with the activations staged in LDS (m <= 4).
-// Same work split as above; the work-group first copies its activations
-// (int8 values) into LDS together with two f32 per run, d_act and
-// d_act * (s0 + s1), while the first block's weight loads are in flight.
-// The block loop then reads them as LDS broadcasts. Per run the integer dot
-// is scaled by the 6-bit scale in integer arithmetic (exact), so a block
-// costs one f32 multiply-add per run for the scales and one for the mins,
-// then one multiply by d and one by dmin.
-// LDS bytes: m * (k + 8 * k / 32) for Q4_K, m * (k + 4 * k / 32) for IQ4_XS.
-// ---------------------------------------------------------------------------
-
 // Split-K epilogue across work-groups, deterministic: each work-group
 // writes its (acc, mins) for its 64 rows to partials[ks], then takes a
 // ticket on its row block's counter; the work-group that takes the last
@@ -691,23 +679,43 @@ __device__ inline void finish_rows(float (&acc)[M], float (&mins)[M], uint64_t r
   }
 }
 
-// The fused form: quantize the work-group's K range [k0, k0 + kn) of m rows
-// of f32 activations straight into LDS with the same per-block arithmetic
-// as quantize_act_kernel (bit-identical values, scales and sums). Every
-// thread runs the same number of iterations so the 8-lane groups shuffle
-// together. LDS: int8 [m][kn], then per run f32 (d) or (d, d * sum).
+// ---------------------------------------------------------------------------
+// Activation staging of the LDS form. Staging is split in two phases so the
+// work-group's activation loads are issued before its weight loads: vector
+// memory returns in issue order per wave, and the staging barrier would
+// otherwise wait behind the first weight blocks. Phase 1 (load) issues the
+// first kPre per-thread loads into registers; phase 2 (store) writes them
+// to LDS, then loads and writes whatever the registers did not cover.
+//
+// LDS layout of the K range [k0, k0 + kn) for m rows: int8 values [m][kn],
+// then per run f32 pairs (d, d * (s0 + s1)) for Q4_K, or f32 d for IQ4_XS,
+// indexed [m][kn / 32].
+// ---------------------------------------------------------------------------
+
+// Fused form: quantize the f32 activations straight into LDS with the same
+// per-block arithmetic as quantize_act_kernel (bit-identical values, scales
+// and sums). Every thread runs the same iterations so the 8-lane groups of
+// quantize4 shuffle together.
 template <int TYPE, int M>
-__device__ inline void stage_quantized(const float* __restrict__ xf, uint64_t K, uint64_t k0, int kn,
-                                       uint8_t* lds) {
-  const int n4 = M * kn / 4, per_row4 = kn / 4;
-  float* rs = reinterpret_cast<float*>(lds + M * kn);
-  for (int i0 = 0; i0 < n4; i0 += blockDim.x) {
-    const int i = i0 + static_cast<int>(threadIdx.x);
-    const bool act = i < n4;
-    const int m = act ? i / per_row4 : 0, c4 = act ? i - m * per_row4 : 0;
-    const float4 v = act ? *reinterpret_cast<const float4*>(xf + m * K + k0 + 4 * c4) : make_float4(0.f, 0.f, 0.f, 0.f);
-    const Quant4 q = quantize4(v);
-    if (!act) continue;
+struct FusedStage {
+  static constexpr int kPre = 4;
+  float4 v[kPre];
+
+  __device__ void load(const float* __restrict__ xf, uint64_t K, uint64_t k0, int kn) {
+    const int n4 = M * kn / 4, per_row4 = kn / 4;
+#pragma unroll
+    for (int j = 0; j < kPre; ++j) {
+      const int i = j * static_cast<int>(blockDim.x) + static_cast<int>(threadIdx.x);
+      v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (i < n4) {
+        const int m = M == 1 ? 0 : i / per_row4, c4 = i - m * per_row4;
+        v[j] = *reinterpret_cast<const float4*>(xf + m * K + k0 + 4 * c4);
+      }
+    }
+  }
+
+  __device__ static void put(const Quant4& q, int i, uint8_t* lds, int M_kn) {
+    float* rs = reinterpret_cast<float*>(lds + M_kn);
     reinterpret_cast<uint32_t*>(lds)[i] = pack_q4(q);
     if ((i & 7) == 0) {
       const int run = i >> 3;  // m * (kn / 32) + run within the range
@@ -719,44 +727,121 @@ __device__ inline void stage_quantized(const float* __restrict__ xf, uint64_t K,
       }
     }
   }
-}
 
-template <int TYPE, int M>
-__device__ inline void stage_activations(const int8_t* __restrict__ xv, const float* __restrict__ xs,
-                                         const int32_t* __restrict__ xsum, uint64_t K, uint64_t k0, int kn,
-                                         uint8_t* lds) {
-  const int per_row16 = kn / 16, kruns = kn / 32;
-  const int runs = static_cast<int>(K / 32), r0 = static_cast<int>(k0 / 32);
-  for (int i = threadIdx.x; i < M * per_row16; i += blockDim.x) {
-    const int m = i / per_row16, c = i - m * per_row16;
-    reinterpret_cast<uint4*>(lds)[i] = *reinterpret_cast<const uint4*>(xv + m * K + k0 + 16 * c);
+  __device__ void store(const float* __restrict__ xf, uint64_t K, uint64_t k0, int kn, uint8_t* lds) const {
+    const int n4 = M * kn / 4, per_row4 = kn / 4;
+#pragma unroll
+    for (int j = 0; j < kPre; ++j) {
+      const int i = j * static_cast<int>(blockDim.x) + static_cast<int>(threadIdx.x);
+      const Quant4 q = quantize4(v[j]);
+      if (i < n4) put(q, i, lds, M * kn);
+    }
+    for (int i0 = kPre * static_cast<int>(blockDim.x); i0 < n4; i0 += blockDim.x) {
+      const int i = i0 + static_cast<int>(threadIdx.x);
+      const bool act = i < n4;
+      const int m = act ? i / per_row4 : 0, c4 = act ? i - m * per_row4 : 0;
+      const float4 x = act ? *reinterpret_cast<const float4*>(xf + m * K + k0 + 4 * c4) : make_float4(0.f, 0.f, 0.f, 0.f);
+      const Quant4 q = quantize4(x);
+      if (act) put(q, i, lds, M * kn);
+    }
   }
-  float* rs = reinterpret_cast<float*>(lds + M * kn);
-  for (int i = threadIdx.x; i < M * kruns; i += blockDim.x) {
-    const int m = i / kruns, u = i - m * kruns;
-    const int src = m * runs + r0 + u;
-    const float d = xs[src];
+};
+
+// Pre-quantized activations: copy values and per-run scales (and Q4_K's
+// d * (s0 + s1)) into LDS.
+template <int TYPE, int M>
+struct QuantizedStage {
+  static constexpr int kPre = 2;
+  uint4 v[kPre];
+  float d;
+  int hs;
+
+  __device__ void load(const int8_t* __restrict__ xv, const float* __restrict__ xs, const int32_t* __restrict__ xsum,
+                       uint64_t K, uint64_t k0, int kn) {
+    const int per_row16 = kn / 16, kruns = kn / 32;
+    const int runs = static_cast<int>(K / 32), r0 = static_cast<int>(k0 / 32);
+    const int t = static_cast<int>(threadIdx.x);
+#pragma unroll
+    for (int j = 0; j < kPre; ++j) {
+      const int i = j * static_cast<int>(blockDim.x) + t;
+      v[j] = make_uint4(0, 0, 0, 0);
+      if (i < M * per_row16) {
+        const int m = M == 1 ? 0 : i / per_row16, c = i - m * per_row16;
+        v[j] = *reinterpret_cast<const uint4*>(xv + m * K + k0 + 16 * c);
+      }
+    }
+    d = 0.0f;
+    hs = 0;
+    if (t < M * kruns) {
+      const int m = M == 1 ? 0 : t / kruns, u = t - m * kruns;
+      const int src = m * runs + r0 + u;
+      d = xs[src];
+      if (TYPE == kTypeQ4K) {
+        const int2 sm = reinterpret_cast<const int2*>(xsum)[src];
+        hs = sm.x + sm.y;
+      }
+    }
+  }
+
+  __device__ static void put_run(float* rs, int i, float d, int hs) {
     if (TYPE == kTypeQ4K) {
-      const int2 sm = reinterpret_cast<const int2*>(xsum)[src];
       rs[2 * i] = d;
-      rs[2 * i + 1] = d * static_cast<float>(sm.x + sm.y);
+      rs[2 * i + 1] = d * static_cast<float>(hs);
     } else {
       rs[i] = d;
     }
   }
-}
+
+  __device__ void store(const int8_t* __restrict__ xv, const float* __restrict__ xs, const int32_t* __restrict__ xsum,
+                        uint64_t K, uint64_t k0, int kn, uint8_t* lds) const {
+    const int per_row16 = kn / 16, kruns = kn / 32;
+    const int runs = static_cast<int>(K / 32), r0 = static_cast<int>(k0 / 32);
+    const int t = static_cast<int>(threadIdx.x);
+#pragma unroll
+    for (int j = 0; j < kPre; ++j) {
+      const int i = j * static_cast<int>(blockDim.x) + t;
+      if (i < M * per_row16) reinterpret_cast<uint4*>(lds)[i] = v[j];
+    }
+    for (int i = kPre * static_cast<int>(blockDim.x) + t; i < M * per_row16; i += blockDim.x) {
+      const int m = i / per_row16, c = i - m * per_row16;
+      reinterpret_cast<uint4*>(lds)[i] = *reinterpret_cast<const uint4*>(xv + m * K + k0 + 16 * c);
+    }
+    float* rs = reinterpret_cast<float*>(lds + M * kn);
+    if (t < M * kruns) put_run(rs, t, d, hs);
+    for (int i = static_cast<int>(blockDim.x) + t; i < M * kruns; i += blockDim.x) {
+      const int m = i / kruns, u = i - m * kruns;
+      const int src = m * runs + r0 + u;
+      int h = 0;
+      if (TYPE == kTypeQ4K) {
+        const int2 sm = reinterpret_cast<const int2*>(xsum)[src];
+        h = sm.x + sm.y;
+      }
+      put_run(rs, i, xs[src], h);
+    }
+  }
+};
 
 // ---------------------------------------------------------------------------
 // Decode GEMV, row-per-lane with the activations staged in LDS (m <= 8).
 // Grid: (row blocks of 64 stored rows) x KS K-splits. A work-group takes
 // the super-blocks [b0, b1) of its split, its waves interleaved over them
-// (wave s: b0 + s, b0 + s + S, ...). It first stages its K range of the
-// activations in LDS (int8 values + two f32 per run, d_act and
-// d_act * (s0 + s1)) -- or quantizes them there itself (FUSED) -- while the
-// first block's weight loads are in flight; the block loop reads them as
-// LDS broadcasts. Per run the integer dot is scaled by the 6-bit scale in
-// integer arithmetic (exact), then by d_act in f32; d and dmin once per
-// block.
+// (wave s: b0 + s, b0 + s + S, ...). Each lane owns one stored row; a wave
+// reads the row group tiles of its 8 row groups plane by plane (eight whole
+// 128-byte lines per load).
+//
+// Schedule: activation loads, then the wave's first weight block, then the
+// activations are written to LDS (or quantized there, FUSED) and the
+// work-group synchronises once; each block's compute runs while the next
+// block is loading. The weight loads are raw buffer loads predicated by
+// offset, so every path issues the same loads and the waits stay exact.
+//
+// For m == 1 the LDS reads of chunk c + 1 (64 activation bytes and the
+// chunk's two run scales) are issued before chunk c is computed, so the
+// LDS latency is covered; with more rows the other rows' work covers it,
+// and the reads happen at their use.
+//
+// Per run the integer dot is scaled by the 6-bit scale in integer
+// arithmetic (exact), then by d_act in f32; d and dmin once per block.
 // ---------------------------------------------------------------------------
 
 struct SplitK {
@@ -765,183 +850,308 @@ struct SplitK {
   int ks;
 };
 
-template <int M, bool FUSED>
-__global__ __launch_bounds__(M <= 4 ? 1024 : 512) void gemv_lds_q4k_int8_kernel(
-    const uint8_t* __restrict__ w, int nb, uint64_t rows, const int8_t* __restrict__ xv,
-    const float* __restrict__ xs, const int32_t* __restrict__ xsum, const float* __restrict__ xf,
-    float* __restrict__ y, const float* __restrict__ addend, uint64_t addend_stride, SplitK sk) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  const int lane = threadIdx.x & 63;
-  const int s = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int S = blockDim.x >> 6;
-  // balanced partition of the super-blocks: every split gets >= 1 (ks <= nb)
-  const int b0 = static_cast<int>(blockIdx.y * nb / sk.ks), b1 = static_cast<int>((blockIdx.y + 1) * nb / sk.ks);
-  const uint64_t g = static_cast<uint64_t>(blockIdx.x) * 8 + (lane >> 3);
-  const bool live = g < (rows + 7) / 8;
-  const int r = lane & 7;
-  const uint64_t K = static_cast<uint64_t>(nb) * 256;
-  const int kn = (b1 - b0) * 256, kruns = kn / 32;
-  const uint8_t* base = w + g * nb * kQ4kTileBytes + r * 16;
-  uint4 nhdr = make_uint4(0, 0, 0, 0), nq[8];
+// One super-block of one row as loaded: the header (Q4_K: 16 bytes; IQ4_XS:
+// 8 bytes in .x/.y) and 8 planes of 16 quant bytes.
+struct RawRowBlock {
+  uint4 hdr;
+  uint4 q[8];
+};
+
+// Loads one row's super-block from the work-group's weight resource:
+// `offset` is the row group's tile of that block (kBufferNone: zeros, no
+// access), `r` the row within the group.
+template <int TYPE>
+__device__ inline void load_row_block(RawRowBlock& a, __amdgpu_buffer_rsrc_t rsrc, uint32_t offset, int r) {
+  if (TYPE == kTypeQ4K) {
+    const uint32_t o = offset == kBufferNone ? kBufferNone : offset + r * 16;
+    a.hdr = buffer_ld16(rsrc, o);
 #pragma unroll
-  for (int p = 0; p < 8; ++p) nq[p] = make_uint4(0, 0, 0, 0);
-  if (live && b0 + s < b1) {
-    const uint8_t* tile = base + static_cast<uint64_t>(b0 + s) * kQ4kTileBytes;
-    nhdr = ld16(tile);
+    for (int p = 0; p < 8; ++p) a.q[p] = buffer_ld16(rsrc, o == kBufferNone ? o : o + 128 * (p + 1));
+  } else {
+    const bool none = offset == kBufferNone;
+    const uint2 h = buffer_ld8(rsrc, none ? kBufferNone : offset + r * 8);
+    a.hdr = make_uint4(h.x, h.y, 0, 0);
 #pragma unroll
-    for (int p = 0; p < 8; ++p) nq[p] = ld16(tile + 128 * (p + 1));
+    for (int p = 0; p < 8; ++p) a.q[p] = buffer_ld16(rsrc, none ? kBufferNone : offset + 64 + 128 * p + r * 16);
   }
-  if (FUSED)
-    stage_quantized<kTypeQ4K, M>(xf, K, static_cast<uint64_t>(b0) * 256, kn, lds);
-  else
-    stage_activations<kTypeQ4K, M>(xv, xs, xsum, K, static_cast<uint64_t>(b0) * 256, kn, lds);
-  __syncthreads();
-  const float2* rs = reinterpret_cast<const float2*>(lds + M * kn);
-  float acc[M], mins[M];
+}
+
+// An LDS address the compiler cannot relate to its neighbours: the chunks'
+// reads are adjacent in LDS, and without this the load-store vectorizer
+// merges them across chunks and hoists every chunk's reads to the first,
+// which only raises register pressure. The offsets are wave-uniform, so
+// the read-first-lane changes no value.
+__device__ inline const uint8_t* opaque(const uint8_t* base, int offset) {
+  return base + __builtin_amdgcn_readfirstlane(offset);
+}
+
+// The activations of one chunk (64 values: Q4_K runs 2c and 2c + 1 are the
+// low and high nibbles of 32 quant bytes; IQ4_XS runs 2c and 2c + 1 are 16
+// quant bytes each) for M rows, as LDS broadcasts: 4 x 16 int8 and the two
+// runs' scales (Q4_K: (d, d * sum) x 2; IQ4_XS: d x 2 in .x/.y).
+template <int M>
+struct Chunk {
+  uint4 x[M][4];
+  float4 s[M];
+};
+
+template <int TYPE, int M>
+__device__ inline void read_chunk(Chunk<M>& ch, const uint8_t* lds, int kn, int kruns, int bl, int c) {
 #pragma unroll
-  for (int m = 0; m < M; ++m) acc[m] = mins[m] = 0.0f;
-  for (int b = b0 + s; b < b1; b += S) {
-    const uint4 hdr = nhdr;
-    uint4 q[8];
-#pragma unroll
-    for (int p = 0; p < 8; ++p) q[p] = nq[p];
-    if (live && b + S < b1) {
-      const uint8_t* tile = base + static_cast<uint64_t>(b + S) * kQ4kTileBytes;
-      nhdr = ld16(tile);
-#pragma unroll
-      for (int p = 0; p < 8; ++p) nq[p] = ld16(tile + 128 * (p + 1));
+  for (int m = 0; m < M; ++m) {
+    const uint4* xa = reinterpret_cast<const uint4*>(opaque(lds, m * kn + bl * 256 + 64 * c));
+    ch.x[m][0] = xa[0];
+    ch.x[m][1] = xa[1];
+    ch.x[m][2] = xa[2];
+    ch.x[m][3] = xa[3];
+    if (TYPE == kTypeQ4K) {
+      ch.s[m] = reinterpret_cast<const float4*>(lds + M * kn)[m * (kruns / 2) + bl * 4 + c];
+    } else {
+      const float2 v = reinterpret_cast<const float2*>(lds + M * kn)[m * (kruns / 2) + bl * 4 + c];
+      ch.s[m] = make_float4(v.x, v.y, 0.f, 0.f);
     }
-    const int bl = b - b0;  // block within the staged range
-    const Q4kSixBit six = q4k_six_bit(hdr);
-    float accb[M], minb[M];
+  }
+}
+
+// Chunk c of one Q4_K row block: accumulates sc * dot * d_act into accb and
+// m * d_act * sum into minb.
+template <int M>
+__device__ inline void q4k_chunk(const RawRowBlock& a, const Q4kSixBit& six, int c, const Chunk<M>& ch,
+                                 float (&accb)[M], float (&minb)[M]) {
+  int dlo[M], dhi[M];
 #pragma unroll
-    for (int m = 0; m < M; ++m) accb[m] = minb[m] = 0.0f;
+  for (int m = 0; m < M; ++m) dlo[m] = dhi[m] = 0;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      int dlo[M], dhi[M];
+  for (int h = 0; h < 2; ++h) {
+    const uint4 qq = a.q[2 * c + h];
+    const uint32_t lo[4] = {qq.x & 0x0F0F0F0Fu, qq.y & 0x0F0F0F0Fu, qq.z & 0x0F0F0F0Fu, qq.w & 0x0F0F0F0Fu};
+    const uint32_t hi[4] = {(qq.x >> 4) & 0x0F0F0F0Fu, (qq.y >> 4) & 0x0F0F0F0Fu, (qq.z >> 4) & 0x0F0F0F0Fu,
+                            (qq.w >> 4) & 0x0F0F0F0Fu};
 #pragma unroll
-      for (int m = 0; m < M; ++m) dlo[m] = dhi[m] = 0;
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const uint4 qq = q[2 * c + h];
-        const uint32_t lo[4] = {qq.x & 0x0F0F0F0Fu, qq.y & 0x0F0F0F0Fu, qq.z & 0x0F0F0F0Fu,
-                                qq.w & 0x0F0F0F0Fu};
-        const uint32_t hi[4] = {(qq.x >> 4) & 0x0F0F0F0Fu, (qq.y >> 4) & 0x0F0F0F0Fu,
-                                (qq.z >> 4) & 0x0F0F0F0Fu, (qq.w >> 4) & 0x0F0F0F0Fu};
-#pragma unroll
-        for (int m = 0; m < M; ++m) {
-          const uint4* xa = reinterpret_cast<const uint4*>(lds + m * kn + bl * 256 + 64 * c + 16 * h);
-          const uint4 x0 = xa[0], x1 = xa[2];
-          dlo[m] = sdot4(lo[0], x0.x, dlo[m]);
-          dlo[m] = sdot4(lo[1], x0.y, dlo[m]);
-          dlo[m] = sdot4(lo[2], x0.z, dlo[m]);
-          dlo[m] = sdot4(lo[3], x0.w, dlo[m]);
-          dhi[m] = sdot4(hi[0], x1.x, dhi[m]);
-          dhi[m] = sdot4(hi[1], x1.y, dhi[m]);
-          dhi[m] = sdot4(hi[2], x1.z, dhi[m]);
-          dhi[m] = sdot4(hi[3], x1.w, dhi[m]);
-        }
-      }
-      uint32_t sc0, m0, sc1, m1;
-      q4k_sc_m(six, 2 * c, sc0, m0);
-      q4k_sc_m(six, 2 * c + 1, sc1, m1);
-#pragma unroll
-      for (int m = 0; m < M; ++m) {
-        const float2 r0 = rs[m * kruns + bl * 8 + 2 * c], r1 = rs[m * kruns + bl * 8 + 2 * c + 1];
-        accb[m] = fmaf(static_cast<float>(__mul24(dlo[m], static_cast<int>(sc0))), r0.x, accb[m]);
-        accb[m] = fmaf(static_cast<float>(__mul24(dhi[m], static_cast<int>(sc1))), r1.x, accb[m]);
-        minb[m] = fmaf(static_cast<float>(m0), r0.y, minb[m]);
-        minb[m] = fmaf(static_cast<float>(m1), r1.y, minb[m]);
-      }
+    for (int m = 0; m < M; ++m) {
+      const uint4 x0 = ch.x[m][h], x1 = ch.x[m][2 + h];
+      dlo[m] = sdot4(lo[0], x0.x, dlo[m]);
+      dlo[m] = sdot4(lo[1], x0.y, dlo[m]);
+      dlo[m] = sdot4(lo[2], x0.z, dlo[m]);
+      dlo[m] = sdot4(lo[3], x0.w, dlo[m]);
+      dhi[m] = sdot4(hi[0], x1.x, dhi[m]);
+      dhi[m] = sdot4(hi[1], x1.y, dhi[m]);
+      dhi[m] = sdot4(hi[2], x1.z, dhi[m]);
+      dhi[m] = sdot4(hi[3], x1.w, dhi[m]);
     }
-    const float d = half_bits(hdr.x), dmin = half_bits(hdr.x >> 16);
+  }
+  uint32_t sc0, m0, sc1, m1;
+  q4k_sc_m(six, 2 * c, sc0, m0);
+  q4k_sc_m(six, 2 * c + 1, sc1, m1);
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    const float4 r = ch.s[m];
+    accb[m] = fmaf(static_cast<float>(__mul24(dlo[m], static_cast<int>(sc0))), r.x, accb[m]);
+    accb[m] = fmaf(static_cast<float>(__mul24(dhi[m], static_cast<int>(sc1))), r.z, accb[m]);
+    minb[m] = fmaf(static_cast<float>(m0), r.y, minb[m]);
+    minb[m] = fmaf(static_cast<float>(m1), r.w, minb[m]);
+  }
+}
+
+// Chunk c of one IQ4_XS row block (runs 2c, 2c + 1): accumulates
+// ls * dot * d_act into accb.
+template <int M>
+__device__ inline void iq4xs_chunk(const RawRowBlock& a, int c, const Chunk<M>& ch, float (&accb)[M]) {
+  const uint2 hdr = make_uint2(a.hdr.x, a.hdr.y);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int j = 2 * c + h;
+    const int ls = iq4xs_ls(hdr, j);
+    const uint4 qq = a.q[j];
+    const uint32_t lo[4] = {iq4_lookup4(qq.x & 0x0F0F0F0Fu), iq4_lookup4(qq.y & 0x0F0F0F0Fu),
+                            iq4_lookup4(qq.z & 0x0F0F0F0Fu), iq4_lookup4(qq.w & 0x0F0F0F0Fu)};
+    const uint32_t hi[4] = {iq4_lookup4((qq.x >> 4) & 0x0F0F0F0Fu), iq4_lookup4((qq.y >> 4) & 0x0F0F0F0Fu),
+                            iq4_lookup4((qq.z >> 4) & 0x0F0F0F0Fu), iq4_lookup4((qq.w >> 4) & 0x0F0F0F0Fu)};
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const uint4 x0 = ch.x[m][2 * h], x1 = ch.x[m][2 * h + 1];
+      int dot = sdot4(lo[0], x0.x, 0);
+      dot = sdot4(lo[1], x0.y, dot);
+      dot = sdot4(lo[2], x0.z, dot);
+      dot = sdot4(lo[3], x0.w, dot);
+      dot = sdot4(hi[0], x1.x, dot);
+      dot = sdot4(hi[1], x1.y, dot);
+      dot = sdot4(hi[2], x1.z, dot);
+      dot = sdot4(hi[3], x1.w, dot);
+      accb[m] = fmaf(static_cast<float>(__mul24(dot, ls)), h == 0 ? ch.s[m].x : ch.s[m].y, accb[m]);
+    }
+  }
+}
+
+// The same chunks with the activations read from LDS at their use (for
+// m >= 2, where holding a whole chunk per row would spill registers).
+template <int M>
+__device__ inline void q4k_chunk_direct(const RawRowBlock& a, const Q4kSixBit& six, int c, const uint8_t* lds,
+                                        int kn, int kruns, int bl, float (&accb)[M], float (&minb)[M]) {
+  int dlo[M], dhi[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) dlo[m] = dhi[m] = 0;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint4 qq = a.q[2 * c + h];
+    const uint32_t lo[4] = {qq.x & 0x0F0F0F0Fu, qq.y & 0x0F0F0F0Fu, qq.z & 0x0F0F0F0Fu, qq.w & 0x0F0F0F0Fu};
+    const uint32_t hi[4] = {(qq.x >> 4) & 0x0F0F0F0Fu, (qq.y >> 4) & 0x0F0F0F0Fu, (qq.z >> 4) & 0x0F0F0F0Fu,
+                            (qq.w >> 4) & 0x0F0F0F0Fu};
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const uint4* xa = reinterpret_cast<const uint4*>(opaque(lds, m * kn + bl * 256 + 64 * c + 16 * h));
+      const uint4 x0 = xa[0], x1 = xa[2];
+      dlo[m] = sdot4(lo[0], x0.x, dlo[m]);
+      dlo[m] = sdot4(lo[1], x0.y, dlo[m]);
+      dlo[m] = sdot4(lo[2], x0.z, dlo[m]);
+      dlo[m] = sdot4(lo[3], x0.w, dlo[m]);
+      dhi[m] = sdot4(hi[0], x1.x, dhi[m]);
+      dhi[m] = sdot4(hi[1], x1.y, dhi[m]);
+      dhi[m] = sdot4(hi[2], x1.z, dhi[m]);
+      dhi[m] = sdot4(hi[3], x1.w, dhi[m]);
+    }
+  }
+  uint32_t sc0, m0, sc1, m1;
+  q4k_sc_m(six, 2 * c, sc0, m0);
+  q4k_sc_m(six, 2 * c + 1, sc1, m1);
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    const float4 r = reinterpret_cast<const float4*>(lds + M * kn)[m * (kruns / 2) + bl * 4 + c];
+    accb[m] = fmaf(static_cast<float>(__mul24(dlo[m], static_cast<int>(sc0))), r.x, accb[m]);
+    accb[m] = fmaf(static_cast<float>(__mul24(dhi[m], static_cast<int>(sc1))), r.z, accb[m]);
+    minb[m] = fmaf(static_cast<float>(m0), r.y, minb[m]);
+    minb[m] = fmaf(static_cast<float>(m1), r.w, minb[m]);
+  }
+}
+
+template <int M>
+__device__ inline void iq4xs_chunk_direct(const RawRowBlock& a, int c, const uint8_t* lds, int kn, int kruns, int bl,
+                                          float (&accb)[M]) {
+  const uint2 hdr = make_uint2(a.hdr.x, a.hdr.y);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int j = 2 * c + h;
+    const int ls = iq4xs_ls(hdr, j);
+    const uint4 qq = a.q[j];
+    const uint32_t lo[4] = {iq4_lookup4(qq.x & 0x0F0F0F0Fu), iq4_lookup4(qq.y & 0x0F0F0F0Fu),
+                            iq4_lookup4(qq.z & 0x0F0F0F0Fu), iq4_lookup4(qq.w & 0x0F0F0F0Fu)};
+    const uint32_t hi[4] = {iq4_lookup4((qq.x >> 4) & 0x0F0F0F0Fu), iq4_lookup4((qq.y >> 4) & 0x0F0F0F0Fu),
+                            iq4_lookup4((qq.z >> 4) & 0x0F0F0F0Fu), iq4_lookup4((qq.w >> 4) & 0x0F0F0F0Fu)};
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const uint4* xa = reinterpret_cast<const uint4*>(opaque(lds, m * kn + bl * 256 + 32 * j));
+      const uint4 x0 = xa[0], x1 = xa[1];
+      int dot = sdot4(lo[0], x0.x, 0);
+      dot = sdot4(lo[1], x0.y, dot);
+      dot = sdot4(lo[2], x0.z, dot);
+      dot = sdot4(lo[3], x0.w, dot);
+      dot = sdot4(hi[0], x1.x, dot);
+      dot = sdot4(hi[1], x1.y, dot);
+      dot = sdot4(hi[2], x1.z, dot);
+      dot = sdot4(hi[3], x1.w, dot);
+      accb[m] = fmaf(static_cast<float>(__mul24(dot, ls)), reinterpret_cast<const float*>(lds + M * kn)[m * kruns + bl * 8 + j],
+                     accb[m]);
+    }
+  }
+}
+
+// One row block through all 4 chunks. With PIPE, `next` holds chunk 0 of
+// this block on entry and chunk 0 of block bl_next (when has_next) on exit.
+template <int TYPE, int M, bool PIPE>
+__device__ inline void row_block(const RawRowBlock& a, const uint8_t* lds, int kn, int kruns, int bl, int bl_next,
+                                 bool has_next, Chunk<M>& next, float (&acc)[M], float (&mins)[M]) {
+  float accb[M], minb[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) accb[m] = minb[m] = 0.0f;
+  Q4kSixBit six;
+  if (TYPE == kTypeQ4K) six = q4k_six_bit(a.hdr);
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    if (PIPE) {
+      const Chunk<M> cur = next;
+      if (c < 3)
+        read_chunk<TYPE, M>(next, lds, kn, kruns, bl, c + 1);
+      else if (has_next)
+        read_chunk<TYPE, M>(next, lds, kn, kruns, bl_next, 0);
+      if (TYPE == kTypeQ4K)
+        q4k_chunk<M>(a, six, c, cur, accb, minb);
+      else
+        iq4xs_chunk<M>(a, c, cur, accb);
+    } else if (TYPE == kTypeQ4K) {
+      q4k_chunk_direct<M>(a, six, c, lds, kn, kruns, bl, accb, minb);
+    } else {
+      iq4xs_chunk_direct<M>(a, c, lds, kn, kruns, bl, accb);
+    }
+  }
+  if (TYPE == kTypeQ4K) {
+    const float d = half_bits(a.hdr.x), dmin = half_bits(a.hdr.x >> 16);
 #pragma unroll
     for (int m = 0; m < M; ++m) {
       acc[m] = fmaf(d, accb[m], acc[m]);
       mins[m] = fmaf(dmin, minb[m], mins[m]);
     }
+  } else {
+    const float d = half_bits(a.hdr.x);
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[m] = fmaf(d, accb[m], acc[m]);
   }
-  finish_rows<M>(acc, mins, rows, y, addend, addend_stride, reinterpret_cast<float*>(lds), sk.partials,
-                 sk.counters, sk.ks);
 }
 
-template <int M, bool FUSED>
-__global__ __launch_bounds__(M <= 4 ? 1024 : 512) void gemv_lds_iq4xs_int8_kernel(
+template <int TYPE, int M, bool FUSED>
+__global__ __launch_bounds__(512) void gemv_lds_int8_kernel(
     const uint8_t* __restrict__ w, int nb, uint64_t rows, const int8_t* __restrict__ xv,
-    const float* __restrict__ xs, const float* __restrict__ xf, float* __restrict__ y,
-    const float* __restrict__ addend, uint64_t addend_stride, SplitK sk) {
+    const float* __restrict__ xs, const int32_t* __restrict__ xsum, const float* __restrict__ xf,
+    float* __restrict__ y, const float* __restrict__ addend, uint64_t addend_stride, SplitK sk) {
+  constexpr bool PIPE = M == 1;
+  constexpr int kTile = TYPE == kTypeQ4K ? kQ4kTileBytes : kIq4xsTileBytes;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int lane = threadIdx.x & 63;
   const int s = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int S = blockDim.x >> 6;
   // balanced partition of the super-blocks: every split gets >= 1 (ks <= nb)
   const int b0 = static_cast<int>(blockIdx.y * nb / sk.ks), b1 = static_cast<int>((blockIdx.y + 1) * nb / sk.ks);
-  const uint64_t g = static_cast<uint64_t>(blockIdx.x) * 8 + (lane >> 3);
-  const bool live = g < (rows + 7) / 8;
   const int r = lane & 7;
   const uint64_t K = static_cast<uint64_t>(nb) * 256;
+  const uint64_t k0 = static_cast<uint64_t>(b0) * 256;
   const int kn = (b1 - b0) * 256, kruns = kn / 32;
-  const uint8_t* base = w + g * nb * kIq4xsTileBytes;
-  uint2 nhdr = make_uint2(0, 0);
-  uint4 nq[8];
-#pragma unroll
-  for (int p = 0; p < 8; ++p) nq[p] = make_uint4(0, 0, 0, 0);
-  if (live && b0 + s < b1) {
-    const uint8_t* tile = base + static_cast<uint64_t>(b0 + s) * kIq4xsTileBytes;
-    nhdr = ld8(tile + r * 8);
-#pragma unroll
-    for (int p = 0; p < 8; ++p) nq[p] = ld16(tile + 64 + 128 * p + r * 16);
-  }
+  // The work-group's 8 row groups as one buffer resource: rows past the
+  // matrix read as zeros (their results are not stored).
+  const uint64_t groups = (rows + 7) / 8, group_bytes = static_cast<uint64_t>(nb) * kTile;
+  const uint64_t g0 = static_cast<uint64_t>(blockIdx.x) * 8;
+  const uint64_t span = (groups - g0 < 8 ? groups - g0 : 8) * group_bytes;
+  const __amdgpu_buffer_rsrc_t rsrc = buffer_rsrc(w + g0 * group_bytes, static_cast<uint32_t>(span));
+  const uint32_t lane_off = static_cast<uint32_t>((lane >> 3) * group_bytes);
+  auto block_off = [&](int b) { return b < b1 ? lane_off + static_cast<uint32_t>(b) * kTile : kBufferNone; };
+
+  // 1. activation loads
+  FusedStage<TYPE, M> fs;
+  QuantizedStage<TYPE, M> qs;
   if (FUSED)
-    stage_quantized<kTypeIq4Xs, M>(xf, K, static_cast<uint64_t>(b0) * 256, kn, lds);
+    fs.load(xf, K, k0, kn);
   else
-    stage_activations<kTypeIq4Xs, M>(xv, xs, nullptr, K, static_cast<uint64_t>(b0) * 256, kn, lds);
+    qs.load(xv, xs, xsum, K, k0, kn);
+  // 2. the wave's first weight block
+  RawRowBlock A;
+  const int bA = b0 + s;
+  load_row_block<TYPE>(A, rsrc, block_off(bA), r);
+  // 3. activations into LDS
+  if (FUSED)
+    fs.store(xf, K, k0, kn, lds);
+  else
+    qs.store(xv, xs, xsum, K, k0, kn, lds);
   __syncthreads();
-  const float* rs = reinterpret_cast<const float*>(lds + M * kn);
+
   float acc[M], mins[M];
 #pragma unroll
   for (int m = 0; m < M; ++m) acc[m] = mins[m] = 0.0f;
-  for (int b = b0 + s; b < b1; b += S) {
-    const uint2 hdr = nhdr;
-    uint4 q[8];
-#pragma unroll
-    for (int p = 0; p < 8; ++p) q[p] = nq[p];
-    if (live && b + S < b1) {
-      const uint8_t* tile = base + static_cast<uint64_t>(b + S) * kIq4xsTileBytes;
-      nhdr = ld8(tile + r * 8);
-#pragma unroll
-      for (int p = 0; p < 8; ++p) nq[p] = ld16(tile + 64 + 128 * p + r * 16);
-    }
-    const int bl = b - b0;
-    float accb[M];
-#pragma unroll
-    for (int m = 0; m < M; ++m) accb[m] = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int ls = iq4xs_ls(hdr, j);
-      const uint4 qq = q[j];
-      const uint32_t lo[4] = {iq4_lookup4(qq.x & 0x0F0F0F0Fu), iq4_lookup4(qq.y & 0x0F0F0F0Fu),
-                              iq4_lookup4(qq.z & 0x0F0F0F0Fu), iq4_lookup4(qq.w & 0x0F0F0F0Fu)};
-      const uint32_t hi[4] = {iq4_lookup4((qq.x >> 4) & 0x0F0F0F0Fu), iq4_lookup4((qq.y >> 4) & 0x0F0F0F0Fu),
-                              iq4_lookup4((qq.z >> 4) & 0x0F0F0F0Fu), iq4_lookup4((qq.w >> 4) & 0x0F0F0F0Fu)};
-#pragma unroll
-      for (int m = 0; m < M; ++m) {
-        const uint4* xa = reinterpret_cast<const uint4*>(lds + m * kn + bl * 256 + 32 * j);
-        const uint4 x0 = xa[0], x1 = xa[1];
-        int dot = sdot4(lo[0], x0.x, 0);
-        dot = sdot4(lo[1], x0.y, dot);
-        dot = sdot4(lo[2], x0.z, dot);
-        dot = sdot4(lo[3], x0.w, dot);
-        dot = sdot4(hi[0], x1.x, dot);
-        dot = sdot4(hi[1], x1.y, dot);
-        dot = sdot4(hi[2], x1.z, dot);
-        dot = sdot4(hi[3], x1.w, dot);
-        accb[m] = fmaf(static_cast<float>(__mul24(dot, ls)), rs[m * kruns + bl * 8 + j], accb[m]);
-      }
-    }
-    const float d = half_bits(hdr.x);
-#pragma unroll
-    for (int m = 0; m < M; ++m) acc[m] = fmaf(d, accb[m], acc[m]);
+  Chunk<M> next;
+  if (PIPE && bA < b1) read_chunk<TYPE, M>(next, lds, kn, kruns, bA - b0, 0);
+  for (int b = bA; b < b1; b += S) {
+    const RawRowBlock cur = A;
+    load_row_block<TYPE>(A, rsrc, block_off(b + S), r);
+    // with more rows the scheduler would sink the prefetch below the math
+    if (!PIPE) __builtin_amdgcn_sched_barrier(0);
+    row_block<TYPE, M, PIPE>(cur, lds, kn, kruns, b - b0, b + S - b0, b + S < b1, next, acc, mins);
   }
   finish_rows<M>(acc, mins, rows, y, addend, addend_stride, reinterpret_cast<float*>(lds), sk.partials,
                  sk.counters, sk.ks);
@@ -1506,7 +1716,7 @@ size_t gemv_lds_bytes(int type, uint64_t nbk, uint64_t m, int splits) {
   return act > red ? act : red;
 }
 
-int lds_form_max_splits(uint64_t m) { return m <= 4 ? 16 : 8; }  // launch bounds 1024 / 512
+int lds_form_max_splits(uint64_t) { return 8; }  // launch bound 512
 
 template <bool FUSED>
 void launch_gemv_lds(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, const int8_t* values,
@@ -1518,10 +1728,10 @@ void launch_gemv_lds(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb,
   const SplitK k{sk.partials, sk.counters, sk.ks};
   if (type == kTypeQ4K) {
     switch (m) {
-#define X(MM)                                                                                               \
-  case MM:                                                                                                  \
-    hipLaunchKernelGGL((gemv_lds_q4k_int8_kernel<MM, FUSED>), grid, block, lds, stream, tiled, inb, rows, values, \
-                       scales, sums, x, y, addend, addend_stride, k);                                       \
+#define X(MM)                                                                                                  \
+  case MM:                                                                                                     \
+    hipLaunchKernelGGL((gemv_lds_int8_kernel<kTypeQ4K, MM, FUSED>), grid, block, lds, stream, tiled, inb, rows, \
+                       values, scales, sums, x, y, addend, addend_stride, k);                                  \
     break;
       MQ_GEMV_CASES(X)
 #undef X
@@ -1530,10 +1740,10 @@ void launch_gemv_lds(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb,
     }
   } else {
     switch (m) {
-#define X(MM)                                                                                                 \
-  case MM:                                                                                                    \
-    hipLaunchKernelGGL((gemv_lds_iq4xs_int8_kernel<MM, FUSED>), grid, block, lds, stream, tiled, inb, rows, values, \
-                       scales, x, y, addend, addend_stride, k);                                               \
+#define X(MM)                                                                                                    \
+  case MM:                                                                                                       \
+    hipLaunchKernelGGL((gemv_lds_int8_kernel<kTypeIq4Xs, MM, FUSED>), grid, block, lds, stream, tiled, inb, rows, \
+                       values, scales, nullptr, x, y, addend, addend_stride, k);                                 \
     break;
       MQ_GEMV_CASES(X)
 #undef X
