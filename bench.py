@@ -99,6 +99,22 @@ def round_up(v, m):
     return (v + m - 1) // m * m
 
 
+def recorded_traffic(name):
+    """HBM bytes per launch of kernel `name` as measured by the two
+    rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE, calibrated against a
+    plain copy) summarised under profiles/, or None if not recorded."""
+    import glob
+    import re
+
+    pat = re.compile(rf"^traffic_bytes_per_launch {re.escape(name)} = (\d+)\s*$")
+    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*.md"))):
+        for line in open(path):
+            m = pat.match(line)
+            if m:
+                return int(m.group(1))
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -292,7 +308,7 @@ def gemm_part(ctx, torch, workloads, use_graph, args):
         "ms_per_step": round(t_gstep * 1e3, 4),
         "roofline": {"bound": "mfma", "achieved": round(flops / t_gkern / 1e12, 2), "peak": F16_MFMA_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(flops / t_gkern / 1e12 / F16_MFMA_PEAK_TFLOPS, 4),
-                     "traffic": None, "kernel_us": round(t_gkern * 1e6, 2),
+                     "traffic": recorded_traffic("gemm_q4k_512x14336x4096"), "kernel_us": round(t_gkern * 1e6, 2),
                      "peak_basis": "dense f16 MFMA (f16 activations x f16-dequantized weights, f32 accumulate)"},
     }
     log(f"gemm m=512: step {t_gstep * 1e6:.1f} us ({flops / t_gstep / 1e12:.1f} TFLOP/s), "
@@ -357,7 +373,9 @@ def emit(args, value, steps, warmup, ms_per_step, n, k, weight_bytes, use_graph,
         },
         "roofline": {
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel_us": round(kernel_us, 3),
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": recorded_traffic("gemv_q4k_m1_fused"),
+            "traffic_unit": "HBM bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
+            "algorithmic_bytes": weight_bytes + 4 * k + 4 * n, "kernel_us": round(kernel_us, 3),
             "kernel": "gemv_lds_q4k_int8_kernel<1, fused>: int8 quantization of x in LDS + Q4_K GEMV, one launch",
         },
         "cpu_baseline": cpu,
