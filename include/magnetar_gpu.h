@@ -153,6 +153,62 @@ int mq_dequantize(mq_ctx *ctx, uint64_t handle, int logical, float *out);
 int mq_dequantize_dev(mq_ctx *ctx, uint64_t handle, int logical, float *out_dev,
                       void *stream);
 
+/* ---- Decoder-layer operators ------------------------------------------------
+ * Device memory, enqueued on `stream` (a hipStream_t; NULL is the null
+ * stream). f32, row-major. Floating-point results follow the reference's
+ * operators step by step; reductions add in a fixed tree order, so they
+ * differ from the reference's left-to-right sums by rounding only. */
+
+#define MQ_ROPE_INTERLEAVED 0 /* pairs (2i, 2i + 1) */
+#define MQ_ROPE_HALF_SPLIT 1  /* pairs (i, i + dimension / 2) */
+
+/* out[r] = x[r] * (1 / sqrt(mean(x[r]^2) + epsilon)) * w, w one row
+ * (w_rows 1) or one per row (w_rows == rows). Replaces `rmsnorm`
+ * (src/lib.rs:348-402) behind the `rmsnorm` Kernel (src/lib.rs:2679-2726). */
+int mq_rmsnorm_dev(mq_ctx *ctx, const float *x_dev, uint64_t rows, uint64_t cols,
+                   const float *w_dev, uint64_t w_rows, float epsilon, float *out_dev,
+                   void *stream);
+
+/* Rotary embedding of `dimension / 2` pairs in each of head_count blocks of
+ * every row, at position (position_offset + row) * scale, frequencies
+ * base^(-2i/dimension); columns past `dimension` are copied. out may equal
+ * x. Replaces `rope_with_pairing` (src/lib.rs:427-687) behind the `rope`
+ * Kernel (src/lib.rs:2728-2817) without frequency scaling or a partial
+ * rotary factor. */
+int mq_rope_dev(mq_ctx *ctx, const float *x_dev, uint64_t rows, uint64_t cols, float base,
+                float scale, uint64_t dimension, uint64_t position_offset,
+                uint64_t head_count, int pairing, float *out_dev, void *stream);
+
+/* Writes `count` rows of `width` over rows row_offset.. of a store of
+ * `capacity` rows, in place. Replaces `kv_write_in_place`
+ * (src/lib.rs:740-768) behind the `kv-write` Kernel (src/lib.rs:2531-2537). */
+int mq_kv_write_dev(mq_ctx *ctx, float *store_dev, uint64_t capacity, uint64_t width,
+                    const float *rows_dev, uint64_t count, uint64_t row_offset, void *stream);
+
+/* Scaled dot-product attention of `seq` query rows q[seq][heads * head_dim]
+ * over the first key_count rows of k and v ([kv_rows][kv_heads * head_dim]),
+ * the queries being the last `seq` positions; causal masking; grouped-query
+ * heads (heads / kv_heads queries share a kv head); score_scale NaN means
+ * 1 / sqrt(head_dim). out is [seq][heads * head_dim]. Replaces
+ * `attention_with_value_width` (src/lib.rs:780-990) behind the `attention`
+ * Kernel with `key_count` (src/lib.rs:2819-2950). head_dim 128 with
+ * heads / kv_heads in {1, 2, 4, 8} has a GPU path; other shapes return
+ * MQ_DECLINED. */
+int mq_attention_dev(mq_ctx *ctx, const float *q_dev, uint64_t seq, const float *k_dev,
+                     const float *v_dev, uint64_t kv_rows, uint64_t key_count, uint64_t heads,
+                     uint64_t head_dim, uint64_t kv_heads, int causal, float score_scale,
+                     float *out_dev, void *stream);
+
+/* out = silu(gate) * up, silu(x) = x * (1 / (1 + exp(-x))). Replaces the
+ * `silu-mul` Kernel (src/lib.rs:2592-2596). */
+int mq_silu_mul_dev(mq_ctx *ctx, const float *gate_dev, const float *up_dev, uint64_t n,
+                    float *out_dev, void *stream);
+
+/* out[i] = a[i] + b[i % b_n], b_n == n or one row broadcast. Replaces `add`
+ * / `residual_add` (src/lib.rs:1019-1075, 1128-1133). */
+int mq_add_dev(mq_ctx *ctx, const float *a_dev, uint64_t n, const float *b_dev, uint64_t b_n,
+               float *out_dev, void *stream);
+
 /* Library version string. */
 const char *mq_version(void);
 

@@ -4,9 +4,12 @@
 // launch grids are validated here before any kernel runs.
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <map>
 #include <mutex>
+#include <vector>
 #include <string>
 #include <thread>
 #include <unordered_map>
@@ -14,6 +17,7 @@
 #include "magnetar_gpu.h"
 #include "mq_device.h"
 #include "mq_launch.h"
+#include "mq_layer.h"
 
 namespace {
 
@@ -54,6 +58,12 @@ struct mq_ctx {
   int gemv_splits_override = 0;
   int gemv_variant = 0;
   int gemm_variant = 0;
+  // Attention split-key partials (stream-ordered like the workspace).
+  void* attn = nullptr;
+  size_t attn_bytes = 0;
+  // RoPE frequency tables by (base bits, dimension), computed on the host
+  // with the platform's powf as the reference does.
+  std::map<std::pair<uint32_t, uint64_t>, float*> rope_tables;
   std::mutex err_mu;
   std::unordered_map<std::thread::id, std::string> errors;
 };
@@ -282,6 +292,8 @@ void mq_destroy(mq_ctx* ctx) {
   if (ctx->ws) (void)hipFree(ctx->ws);
   if (ctx->io) (void)hipFree(ctx->io);
   if (ctx->sk) (void)hipFree(ctx->sk);
+  if (ctx->attn) (void)hipFree(ctx->attn);
+  for (auto& kv : ctx->rope_tables) (void)hipFree(kv.second);
   (void)hipEventDestroy(ctx->ws_event);
   (void)hipStreamDestroy(ctx->stream);
   delete ctx;
@@ -556,6 +568,154 @@ int mq_dequantize(mq_ctx* ctx, uint64_t handle, int logical, float* out) {
   if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
   (void)hipFree(dev);
   if (e != hipSuccess) return hip_fail(ctx, e, "mq_dequantize");
+  return MQ_OK;
+}
+
+
+// ---- decoder-layer operators ----------------------------------------------------
+
+int mq_rmsnorm_dev(mq_ctx* ctx, const float* x_dev, uint64_t rows, uint64_t cols, const float* w_dev,
+                   uint64_t w_rows, float epsilon, float* out_dev, void* stream) {
+  if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_rmsnorm_dev: null context");
+  if (cols == 0) return fail(ctx, MQ_ERR_SHAPE, "RMSNorm hidden dimension must be non-zero");
+  if (!(epsilon > 0.0f)) return fail(ctx, MQ_ERR_SHAPE, "RMSNorm epsilon must be positive");
+  if (w_rows != 1 && w_rows != rows)
+    return fail(ctx, MQ_ERR_SHAPE, "RMSNorm weight shape must be [" + std::to_string(cols) + "] or [" +
+                                       std::to_string(rows) + ", " + std::to_string(cols) + "]");
+  if (rows == 0) return MQ_OK;
+  if (!x_dev || !w_dev || !out_dev) return fail(ctx, MQ_ERR_ARGUMENT, "mq_rmsnorm_dev: null pointer");
+  DeviceGuard guard(ctx->device);
+  mq::launch_rmsnorm(x_dev, rows, cols, w_dev, w_rows == 1 ? 0 : cols, epsilon, out_dev,
+                     static_cast<hipStream_t>(stream));
+  MQ_HIP(ctx, hipGetLastError());
+  return MQ_OK;
+}
+
+int mq_rope_dev(mq_ctx* ctx, const float* x_dev, uint64_t rows, uint64_t cols, float base, float scale,
+                uint64_t dimension, uint64_t position_offset, uint64_t head_count, int pairing, float* out_dev,
+                void* stream) {
+  if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_rope_dev: null context");
+  if (head_count == 0 || cols % head_count)
+    return fail(ctx, MQ_ERR_SHAPE, "RoPE head_count " + std::to_string(head_count) +
+                                       " must be positive and evenly divide the row width " + std::to_string(cols));
+  const uint64_t head_width = cols / head_count;
+  if (dimension == 0 || dimension % 2 || dimension > head_width)
+    return fail(ctx, MQ_ERR_SHAPE, "RoPE dimension " + std::to_string(dimension) +
+                                       " must be positive, even, and at most the head width " +
+                                       std::to_string(head_width));
+  if (!std::isfinite(base) || base <= 0.0f) return fail(ctx, MQ_ERR_SHAPE, "RoPE base must be finite and positive");
+  if (!std::isfinite(scale) || scale <= 0.0f)
+    return fail(ctx, MQ_ERR_SHAPE, "RoPE scale must be finite and positive");
+  if (pairing != MQ_ROPE_INTERLEAVED && pairing != MQ_ROPE_HALF_SPLIT)
+    return fail(ctx, MQ_ERR_ARGUMENT, "unknown RoPE pairing " + std::to_string(pairing));
+  if (rows == 0) return MQ_OK;
+  if (!x_dev || !out_dev) return fail(ctx, MQ_ERR_ARGUMENT, "mq_rope_dev: null pointer");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  DeviceGuard guard(ctx->device);
+  uint32_t base_bits;
+  std::memcpy(&base_bits, &base, sizeof base_bits);
+  const auto key = std::make_pair(base_bits, dimension);
+  auto it = ctx->rope_tables.find(key);
+  if (it == ctx->rope_tables.end()) {
+    // the reference's table: base.powf(-2.0 * (pair as f32) / dimension as f32), in f32
+    std::vector<float> table(dimension / 2);
+    for (uint64_t p = 0; p < dimension / 2; ++p)
+      table[p] = std::pow(base, -2.0f * static_cast<float>(p) / static_cast<float>(dimension));
+    float* dev = nullptr;
+    MQ_HIP(ctx, hipMalloc(&dev, table.size() * sizeof(float)));
+    hipError_t e = hipMemcpy(dev, table.data(), table.size() * sizeof(float), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+      (void)hipFree(dev);
+      return hip_fail(ctx, e, "hipMemcpy(rope table)");
+    }
+    it = ctx->rope_tables.emplace(key, dev).first;
+  }
+  mq::launch_rope(x_dev, rows, cols, head_count, dimension, scale, position_offset, pairing, it->second, out_dev,
+                  static_cast<hipStream_t>(stream));
+  MQ_HIP(ctx, hipGetLastError());
+  return MQ_OK;
+}
+
+int mq_kv_write_dev(mq_ctx* ctx, float* store_dev, uint64_t capacity, uint64_t width, const float* rows_dev,
+                    uint64_t count, uint64_t row_offset, void* stream) {
+  if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_kv_write_dev: null context");
+  if (row_offset + count < row_offset || row_offset + count > capacity)
+    return fail(ctx, MQ_ERR_SHAPE, "kv-write of " + std::to_string(count) + " rows at " +
+                                       std::to_string(row_offset) + " exceeds the store's " +
+                                       std::to_string(capacity) + " rows");
+  if (count == 0 || width == 0) return MQ_OK;
+  if (!store_dev || !rows_dev) return fail(ctx, MQ_ERR_ARGUMENT, "mq_kv_write_dev: null pointer");
+  DeviceGuard guard(ctx->device);
+  MQ_HIP(ctx, hipMemcpyAsync(store_dev + row_offset * width, rows_dev, count * width * sizeof(float),
+                             hipMemcpyDeviceToDevice, static_cast<hipStream_t>(stream)));
+  return MQ_OK;
+}
+
+int mq_attention_dev(mq_ctx* ctx, const float* q_dev, uint64_t seq, const float* k_dev, const float* v_dev,
+                     uint64_t kv_rows, uint64_t key_count, uint64_t heads, uint64_t head_dim, uint64_t kv_heads,
+                     int causal, float score_scale, float* out_dev, void* stream) {
+  if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_attention_dev: null context");
+  if (heads == 0 || head_dim == 0 || kv_heads == 0)
+    return fail(ctx, MQ_ERR_SHAPE, "head_count, kv_head_count, and head_dimension must all be positive");
+  if (heads % kv_heads)
+    return fail(ctx, MQ_ERR_SHAPE, "head_count " + std::to_string(heads) + " must be an exact multiple of kv_head_count " +
+                                       std::to_string(kv_heads));
+  if (key_count > kv_rows)
+    return fail(ctx, MQ_ERR_SHAPE, "key_count " + std::to_string(key_count) + " exceeds the " +
+                                       std::to_string(kv_rows) + " rows of K/V");
+  if (seq > key_count)
+    return fail(ctx, MQ_ERR_SHAPE, "q sequence length " + std::to_string(seq) +
+                                       " cannot exceed k/v sequence length " + std::to_string(key_count));
+  if (!std::isnan(score_scale) && !std::isfinite(score_scale))
+    return fail(ctx, MQ_ERR_SHAPE, "attention scale must be finite");
+  const uint64_t group = heads / kv_heads;
+  if (head_dim != 128 || (group != 1 && group != 2 && group != 4 && group != 8))
+    return fail(ctx, MQ_DECLINED, "attention with head_dim " + std::to_string(head_dim) + " and " +
+                                      std::to_string(group) + " query heads per kv head has no GPU path");
+  if (seq == 0) return MQ_OK;
+  if (!q_dev || !k_dev || !v_dev || !out_dev) return fail(ctx, MQ_ERR_ARGUMENT, "mq_attention_dev: null pointer");
+  const float scale = std::isnan(score_scale) ? 1.0f / std::sqrt(static_cast<float>(head_dim)) : score_scale;
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  DeviceGuard guard(ctx->device);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int rc = order_stream(ctx, s);
+  if (rc) return rc;
+  const size_t need = seq * heads * mq::attention_chunks(key_count) * (2 + head_dim) * sizeof(float);
+  if (need > ctx->attn_bytes) {
+    MQ_HIP(ctx, hipStreamSynchronize(s));
+    if (ctx->attn) MQ_HIP(ctx, hipFree(ctx->attn));
+    ctx->attn = nullptr;
+    ctx->attn_bytes = 0;
+    MQ_HIP(ctx, hipMalloc(&ctx->attn, need));
+    ctx->attn_bytes = need;
+  }
+  if (!mq::launch_attention(q_dev, k_dev, v_dev, seq, key_count, heads, head_dim, kv_heads, causal ? 1 : 0, scale,
+                            static_cast<float*>(ctx->attn), out_dev, s))
+    return fail(ctx, MQ_DECLINED, "attention shape has no GPU path");
+  MQ_HIP(ctx, hipGetLastError());
+  return MQ_OK;
+}
+
+int mq_silu_mul_dev(mq_ctx* ctx, const float* gate_dev, const float* up_dev, uint64_t n, float* out_dev,
+                    void* stream) {
+  if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_silu_mul_dev: null context");
+  if (n == 0) return MQ_OK;
+  if (!gate_dev || !up_dev || !out_dev) return fail(ctx, MQ_ERR_ARGUMENT, "mq_silu_mul_dev: null pointer");
+  DeviceGuard guard(ctx->device);
+  mq::launch_silu_mul(gate_dev, up_dev, n, out_dev, static_cast<hipStream_t>(stream));
+  MQ_HIP(ctx, hipGetLastError());
+  return MQ_OK;
+}
+
+int mq_add_dev(mq_ctx* ctx, const float* a_dev, uint64_t n, const float* b_dev, uint64_t b_n, float* out_dev,
+               void* stream) {
+  if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_add_dev: null context");
+  if (b_n == 0 || n % b_n) return fail(ctx, MQ_ERR_SHAPE, "add: b must match a or be one row of a");
+  if (n == 0) return MQ_OK;
+  if (!a_dev || !b_dev || !out_dev) return fail(ctx, MQ_ERR_ARGUMENT, "mq_add_dev: null pointer");
+  DeviceGuard guard(ctx->device);
+  mq::launch_add(a_dev, n, b_dev, b_n, out_dev, static_cast<hipStream_t>(stream));
+  MQ_HIP(ctx, hipGetLastError());
   return MQ_OK;
 }
 

@@ -1,0 +1,254 @@
+// gfx950 kernels for the decoder-layer operators around the packed matmul:
+// rmsnorm, rope, attention (split-key decode), silu-mul and add. All
+// tensors are row-major f32 in device memory. Built with
+// -ffp-contract=off: each multiply and add rounds separately, as in the
+// reference's operators; reductions run in a fixed tree order, so results
+// are deterministic, and differ from the reference's left-to-right sums
+// only by rounding.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "mq_layer.h"
+
+namespace mq {
+namespace {
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+__device__ inline float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// rmsnorm (src/lib.rs:348-402): one work-group of 256 threads per row. The
+// sum of squares is a per-thread partial over a strided range, then a wave
+// and a cross-wave tree; scale = 1 / sqrt(mean + eps) with correctly
+// rounded sqrt and division; out = v * scale * w.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x, uint64_t cols,
+                                                      const float* __restrict__ w, uint64_t w_stride, float eps,
+                                                      float* __restrict__ out) {
+  __shared__ float part[4];
+  const uint64_t row = blockIdx.x;
+  const float* v = x + row * cols;
+  const float* wv = w + row * w_stride;
+  float s = 0.0f;
+  for (uint64_t c = threadIdx.x; c < cols; c += 256) s += v[c] * v[c];
+  s = wave_sum(s);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+  __syncthreads();
+  const float total = (part[0] + part[1]) + (part[2] + part[3]);
+  const float scale = 1.0f / sqrtf(total / static_cast<float>(cols) + eps);
+  for (uint64_t c = threadIdx.x; c < cols; c += 256) out[row * cols + c] = v[c] * scale * wv[c];
+}
+
+// ---------------------------------------------------------------------------
+// rope (src/lib.rs:616-687): one thread per (row, head, rotated pair),
+// angle = position * freq[pair] (the frequency table comes from the host,
+// computed with the platform's powf as the reference does). Columns past
+// `dimension` in each head are not touched here: the launcher copies them
+// when out is not x.
+// ---------------------------------------------------------------------------
+// (x and out may be the same buffer: each thread reads its pair, then writes it)
+__global__ __launch_bounds__(256) void rope_kernel(const float* x, uint64_t rows, uint64_t cols,
+                                                   uint64_t head_count, uint64_t dimension, float scale,
+                                                   uint64_t position_offset, int half_split,
+                                                   const float* __restrict__ freq, float* out) {
+  const uint64_t head_width = cols / head_count, half = dimension / 2;
+  const uint64_t t = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= rows * head_count * half) return;
+  const uint64_t row = t / (head_count * half);
+  const uint64_t rem = t - row * head_count * half;
+  const uint64_t head = rem / half, p = rem - head * half;
+  const uint64_t base = row * cols + head * head_width;
+  const float position = static_cast<float>(position_offset + row) * scale;
+  const float angle = position * freq[p];
+  const float s = sinf(angle), c = cosf(angle);
+  const uint64_t first = half_split ? base + p : base + 2 * p;
+  const uint64_t second = half_split ? base + p + half : base + 2 * p + 1;
+  const float a = x[first], b = x[second];
+  out[first] = a * c - b * s;
+  out[second] = a * s + b * c;
+}
+
+// ---------------------------------------------------------------------------
+// Attention, split over keys (src/lib.rs:780-990). Work-group = one wave =
+// one (kv head, chunk of 64 keys, query row). Scores: lane j owns key j of
+// the chunk and computes the dot with each of the group's query heads;
+// the query values arrive as wave-uniform scalar loads. Softmax partials
+// per chunk and head: m = max score, p = exp(s - m), l = sum p; then
+// lane pairs of value dimensions accumulate o = sum_j p_j v_j with p read
+// from LDS. attention_combine_kernel merges the chunks:
+// out = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c.
+// ---------------------------------------------------------------------------
+constexpr int kChunk = 64;
+
+template <int GROUP, int HD>
+__global__ __launch_bounds__(64) void attention_partial_kernel(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v, uint64_t seq,
+    uint64_t key_count, uint64_t heads, uint64_t kv_heads, int causal, float scale,
+    float* __restrict__ part) {
+  __shared__ float p_lds[GROUP][kChunk];
+  const int lane = threadIdx.x;
+  const uint64_t kvh = blockIdx.x, chunk = blockIdx.y, t = blockIdx.z;
+  const uint64_t chunks = gridDim.y;
+  const uint64_t q_dim = heads * HD, kv_dim = kv_heads * HD;
+  const uint64_t upper = causal ? key_count - seq + t + 1 : key_count;
+  const uint64_t j0 = chunk * kChunk;
+  const uint64_t j = j0 + lane;
+  const bool live = j < upper;
+  // scores for the GROUP heads of this kv head
+  float s[GROUP];
+#pragma unroll
+  for (int g = 0; g < GROUP; ++g) s[g] = 0.0f;
+  const float* krow = k + (live ? j : 0) * kv_dim + kvh * HD;
+  const float* qrow = q + t * q_dim + kvh * GROUP * HD;
+#pragma unroll 4
+  for (int d = 0; d < HD; d += 4) {
+    const float4 kk = *reinterpret_cast<const float4*>(krow + d);
+#pragma unroll
+    for (int g = 0; g < GROUP; ++g) {
+      const float4 qq = *reinterpret_cast<const float4*>(qrow + g * HD + d);
+      s[g] += qq.x * kk.x;
+      s[g] += qq.y * kk.y;
+      s[g] += qq.z * kk.z;
+      s[g] += qq.w * kk.w;
+    }
+  }
+  float m[GROUP], l[GROUP];
+#pragma unroll
+  for (int g = 0; g < GROUP; ++g) {
+    const float sc = live ? s[g] * scale : -INFINITY;
+    m[g] = wave_max(sc);
+    const float p = live ? expf(sc - m[g]) : 0.0f;
+    l[g] = wave_sum(p);
+    p_lds[g][lane] = p;
+  }
+  __syncthreads();
+  // o: lane owns dims 2 lane, 2 lane + 1 (HD == 128)
+  float o[GROUP][2];
+#pragma unroll
+  for (int g = 0; g < GROUP; ++g) o[g][0] = o[g][1] = 0.0f;
+  const uint64_t jn = upper > j0 ? (upper - j0 < kChunk ? upper - j0 : kChunk) : 0;
+  for (uint64_t jj = 0; jj < jn; ++jj) {
+    const float2 vv = *reinterpret_cast<const float2*>(v + (j0 + jj) * kv_dim + kvh * HD + 2 * lane);
+#pragma unroll
+    for (int g = 0; g < GROUP; ++g) {
+      const float p = p_lds[g][jj];
+      o[g][0] += p * vv.x;
+      o[g][1] += p * vv.y;
+    }
+  }
+  // part layout: [t][head][chunk][2 + HD]
+#pragma unroll
+  for (int g = 0; g < GROUP; ++g) {
+    const uint64_t h = kvh * GROUP + g;
+    float* dst = part + ((t * heads + h) * chunks + chunk) * (2 + HD);
+    if (lane == 0) {
+      dst[0] = jn ? m[g] : -INFINITY;
+      dst[1] = jn ? l[g] : 0.0f;
+    }
+    dst[2 + 2 * lane] = o[g][0];
+    dst[3 + 2 * lane] = o[g][1];
+  }
+}
+
+template <int HD>
+__global__ __launch_bounds__(HD) void attention_combine_kernel(const float* __restrict__ part, uint64_t heads,
+                                                              uint64_t chunks, float* __restrict__ out) {
+  const uint64_t h = blockIdx.x, t = blockIdx.y;
+  const int d = threadIdx.x;
+  const float* base = part + (t * heads + h) * chunks * (2 + HD);
+  float mx = -INFINITY;
+  for (uint64_t c = 0; c < chunks; ++c) mx = fmaxf(mx, base[c * (2 + HD)]);
+  float num = 0.0f, den = 0.0f;
+  for (uint64_t c = 0; c < chunks; ++c) {
+    const float mc = base[c * (2 + HD)];
+    if (mc == -INFINITY) continue;
+    const float e = expf(mc - mx);
+    den += e * base[c * (2 + HD) + 1];
+    num += e * base[c * (2 + HD) + 2 + d];
+  }
+  out[t * heads * HD + h * HD + d] = num / den;
+}
+
+// ---------------------------------------------------------------------------
+// silu-mul (src/lib.rs:2592-2596, 993-1004): g * (1 / (1 + exp(-g))) * u.
+// add (src/lib.rs:1019-1075): a + b[i % b_n].
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void silu_mul_kernel(const float* __restrict__ g, const float* __restrict__ u,
+                                                       uint64_t n, float* __restrict__ out) {
+  const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float x = g[i];
+  const float s = x * (1.0f / (1.0f + expf(-x)));
+  out[i] = s * u[i];
+}
+
+__global__ __launch_bounds__(256) void add_kernel(const float* __restrict__ a, uint64_t n,
+                                                  const float* __restrict__ b, uint64_t b_n,
+                                                  float* __restrict__ out) {
+  const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  out[i] = a[i] + b[i % b_n];
+}
+
+unsigned blocks_for(uint64_t n, unsigned per) { return static_cast<unsigned>((n + per - 1) / per); }
+
+}  // namespace
+
+void launch_rmsnorm(const float* x, uint64_t rows, uint64_t cols, const float* w, uint64_t w_stride, float eps,
+                    float* out, hipStream_t stream) {
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(static_cast<unsigned>(rows)), dim3(256), 0, stream, x, cols, w, w_stride,
+                     eps, out);
+}
+
+void launch_rope(const float* x, uint64_t rows, uint64_t cols, uint64_t head_count, uint64_t dimension, float scale,
+                 uint64_t position_offset, int half_split, const float* freq, float* out, hipStream_t stream) {
+  if (out != x && dimension < cols / head_count)
+    (void)hipMemcpyAsync(out, x, rows * cols * sizeof(float), hipMemcpyDeviceToDevice, stream);
+  const uint64_t n = rows * head_count * (dimension / 2);
+  hipLaunchKernelGGL(rope_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, x, rows, cols, head_count,
+                     dimension, scale, position_offset, half_split, freq, out);
+}
+
+uint64_t attention_chunks(uint64_t key_count) { return (key_count + kChunk - 1) / kChunk; }
+
+bool launch_attention(const float* q, const float* k, const float* v, uint64_t seq, uint64_t key_count,
+                      uint64_t heads, uint64_t head_dim, uint64_t kv_heads, int causal, float scale, float* part,
+                      float* out, hipStream_t stream) {
+  if (head_dim != 128) return false;
+  const uint64_t group = heads / kv_heads, chunks = attention_chunks(key_count);
+  dim3 grid(static_cast<unsigned>(kv_heads), static_cast<unsigned>(chunks), static_cast<unsigned>(seq));
+  switch (group) {
+#define X(G)                                                                                                   \
+  case G:                                                                                                      \
+    hipLaunchKernelGGL((attention_partial_kernel<G, 128>), grid, dim3(64), 0, stream, q, k, v, seq, key_count, \
+                       heads, kv_heads, causal, scale, part);                                                  \
+    break;
+    X(1) X(2) X(4) X(8)
+#undef X
+    default:
+      return false;
+  }
+  hipLaunchKernelGGL((attention_combine_kernel<128>), dim3(static_cast<unsigned>(heads), static_cast<unsigned>(seq)),
+                     dim3(128), 0, stream, part, heads, chunks, out);
+  return true;
+}
+
+void launch_silu_mul(const float* g, const float* u, uint64_t n, float* out, hipStream_t stream) {
+  hipLaunchKernelGGL(silu_mul_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, g, u, n, out);
+}
+
+void launch_add(const float* a, uint64_t n, const float* b, uint64_t b_n, float* out, hipStream_t stream) {
+  hipLaunchKernelGGL(add_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, a, n, b, b_n, out);
+}
+
+}  // namespace mq

@@ -82,6 +82,15 @@ def gpu_lib():
         L.mq_matmul_f16_dev.argtypes = [_vp, _u64, _vp, _u64, _u64, _vp, _vp]
         L.mq_dequantize.argtypes = [_vp, _u64, ctypes.c_int, _f32p]
         L.mq_dequantize_dev.argtypes = [_vp, _u64, ctypes.c_int, _vp, _vp]
+        L.mq_matmul_add_dev.argtypes = [_vp, _u64, _vp, _u64, _u64, ctypes.c_uint32, _vp, _u64, _vp, _vp]
+        f32 = ctypes.c_float
+        L.mq_rmsnorm_dev.argtypes = [_vp, _vp, _u64, _u64, _vp, _u64, f32, _vp, _vp]
+        L.mq_rope_dev.argtypes = [_vp, _vp, _u64, _u64, f32, f32, _u64, _u64, _u64, ctypes.c_int, _vp, _vp]
+        L.mq_kv_write_dev.argtypes = [_vp, _vp, _u64, _u64, _vp, _u64, _u64, _vp]
+        L.mq_attention_dev.argtypes = [_vp, _vp, _u64, _vp, _vp, _u64, _u64, _u64, _u64, _u64, ctypes.c_int, f32,
+                                       _vp, _vp]
+        L.mq_silu_mul_dev.argtypes = [_vp, _vp, _vp, _u64, _vp, _vp]
+        L.mq_add_dev.argtypes = [_vp, _vp, _u64, _vp, _u64, _vp, _vp]
         _gpu = L
     return _gpu
 
@@ -238,3 +247,35 @@ class Context:
 
     def dequantize_dev(self, weight, out_ptr, logical=False, stream=None):
         self._check(gpu_lib().mq_dequantize_dev(self.ptr, weight.handle, int(logical), out_ptr, stream))
+
+    def matmul_add_dev(self, weight, x_ptr, m, k, addend_ptr, addend_rows, y_ptr, int8=True, stream=None):
+        """y = x . W^T + addend (addend_rows 1: a bias row; m: a residual)."""
+        self._check(gpu_lib().mq_matmul_add_dev(self.ptr, weight.handle, x_ptr, m, k,
+                                                INT8_ACTIVATIONS if int8 else 0, addend_ptr, addend_rows, y_ptr,
+                                                stream))
+
+    # ---- decoder-layer operators (device pointers) ----------------------------
+
+    def rmsnorm_dev(self, x_ptr, rows, cols, w_ptr, w_rows, epsilon, out_ptr, stream=None):
+        self._check(gpu_lib().mq_rmsnorm_dev(self.ptr, x_ptr, rows, cols, w_ptr, w_rows, epsilon, out_ptr, stream))
+
+    def rope_dev(self, x_ptr, rows, cols, base, scale, dimension, position_offset, head_count, out_ptr,
+                 half_split=False, stream=None):
+        self._check(gpu_lib().mq_rope_dev(self.ptr, x_ptr, rows, cols, base, scale, dimension, position_offset,
+                                          head_count, 1 if half_split else 0, out_ptr, stream))
+
+    def kv_write_dev(self, store_ptr, capacity, width, rows_ptr, count, row_offset, stream=None):
+        self._check(gpu_lib().mq_kv_write_dev(self.ptr, store_ptr, capacity, width, rows_ptr, count, row_offset,
+                                              stream))
+
+    def attention_dev(self, q_ptr, seq, k_ptr, v_ptr, kv_rows, key_count, heads, head_dim, kv_heads, out_ptr,
+                      causal=True, scale=None, stream=None):
+        self._check(gpu_lib().mq_attention_dev(self.ptr, q_ptr, seq, k_ptr, v_ptr, kv_rows, key_count, heads,
+                                               head_dim, kv_heads, 1 if causal else 0,
+                                               float("nan") if scale is None else float(scale), out_ptr, stream))
+
+    def silu_mul_dev(self, gate_ptr, up_ptr, n, out_ptr, stream=None):
+        self._check(gpu_lib().mq_silu_mul_dev(self.ptr, gate_ptr, up_ptr, n, out_ptr, stream))
+
+    def add_dev(self, a_ptr, n, b_ptr, b_n, out_ptr, stream=None):
+        self._check(gpu_lib().mq_add_dev(self.ptr, a_ptr, n, b_ptr, b_n, out_ptr, stream))

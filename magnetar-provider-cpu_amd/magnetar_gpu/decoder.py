@@ -1,0 +1,143 @@
+"""A Llama-3-8B-shaped decoder layer decode step, device-resident.
+
+The step is the sequence of Kernels the Runtime submits for one generated
+token, each one an entry point of ``libmagnetar_gpu.so``:
+
+    xn  = rmsnorm(x, g_attn, eps)                     (src/lib.rs:348-402)
+    q, k, v = xn . Wq^T, xn . Wk^T, xn . Wv^T          packed matmul (int8 activations)
+    q, k = rope(q), rope(k) at position `position`     (src/lib.rs:427-687)
+    K[position], V[position] = k, v                    kv-write (src/lib.rs:740-768)
+    a   = attention(q, K, V, key_count = position + 1) (src/lib.rs:780-990)
+    h   = x + a . Wo^T                                 matmul-residual (src/lib.rs:2577-2590)
+    hn  = rmsnorm(h, g_ffn, eps)
+    f   = silu(hn . Wgate^T) * (hn . Wup^T)            silu-mul (src/lib.rs:2592-2596)
+    out = h + f . Wdown^T                              matmul-residual
+
+All intermediates stay in HBM (torch tensors used as device allocations);
+only the projections' packed weights and the f32 KV cache are read from
+HBM in bulk. Shapes: hidden 4096, 32 query / 8 key-value heads of 128,
+FFN 14336, rmsnorm eps 1e-5, rope theta 5e5.
+"""
+
+import numpy as np
+
+from . import Q4_K, gaussian, quantize
+
+HIDDEN = 4096
+HEADS = 32
+KV_HEADS = 8
+HEAD_DIM = 128
+FFN = 14336
+EPS = 1e-5
+THETA = 5e5
+
+# projection name -> (stored rows N, stored cols K)
+PROJECTIONS = {
+    "q": (HEADS * HEAD_DIM, HIDDEN),
+    "k": (KV_HEADS * HEAD_DIM, HIDDEN),
+    "v": (KV_HEADS * HEAD_DIM, HIDDEN),
+    "o": (HIDDEN, HEADS * HEAD_DIM),
+    "gate": (FFN, HIDDEN),
+    "up": (FFN, HIDDEN),
+    "down": (HIDDEN, FFN),
+}
+
+
+class LayerData:
+    """Seeded synthetic layer (host arrays): Q4_K projections from
+    N(0, 0.02), rmsnorm weights 1 + N(0, 0.02), a KV cache of `capacity`
+    rows whose first `prefilled` rows are N(0, 1), and an N(0, 1) input
+    hidden state. Generator seeds 1000 s + 1 + i for the i-th array."""
+
+    def __init__(self, seed=4, capacity=4096, prefilled=4095, quantize_fn=quantize):
+        base = 1000 * seed
+        self.capacity, self.prefilled = capacity, prefilled
+        self.weights = {}
+        for i, (name, (n, k)) in enumerate(PROJECTIONS.items()):
+            self.weights[name] = quantize_fn(Q4_K, gaussian(base + 1 + i, 0.02, n * k).reshape(n, k))
+        self.g_attn = (1.0 + gaussian(base + 11, 0.02, HIDDEN)).astype(np.float32)
+        self.g_ffn = (1.0 + gaussian(base + 12, 0.02, HIDDEN)).astype(np.float32)
+        width = KV_HEADS * HEAD_DIM
+        self.k_cache = np.zeros((capacity, width), np.float32)
+        self.v_cache = np.zeros((capacity, width), np.float32)
+        self.k_cache[:prefilled] = gaussian(base + 13, 1.0, prefilled * width).reshape(prefilled, width)
+        self.v_cache[:prefilled] = gaussian(base + 14, 1.0, prefilled * width).reshape(prefilled, width)
+        self.x = gaussian(base + 500, 1.0, HIDDEN).reshape(1, HIDDEN)
+
+    def weight_bytes(self):
+        return sum(int(w.size) for w in self.weights.values())
+
+
+class DecoderLayer:
+    """The layer on one device: uploads the packed weights and the KV
+    cache, allocates every intermediate once, and runs `step` (all device
+    work enqueued on one stream; nothing allocated per step)."""
+
+    def __init__(self, ctx, torch, data, int8=True):
+        self.ctx, self.torch, self.int8 = ctx, torch, int8
+        dev = "cuda"
+        self.w = {name: ctx.upload(Q4_K, n, k, data.weights[name]) for name, (n, k) in PROJECTIONS.items()}
+        t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+        self.g_attn, self.g_ffn = t(data.g_attn), t(data.g_ffn)
+        self.k_cache, self.v_cache = t(data.k_cache), t(data.v_cache)
+        self.capacity = data.capacity
+        e = lambda n: torch.empty((1, n), dtype=torch.float32, device=dev)  # noqa: E731
+        self.x = t(data.x)
+        self.xn, self.q, self.k, self.v = e(HIDDEN), e(HEADS * HEAD_DIM), e(KV_HEADS * HEAD_DIM), e(KV_HEADS * HEAD_DIM)
+        self.a, self.h, self.hn = e(HEADS * HEAD_DIM), e(HIDDEN), e(HIDDEN)
+        self.g, self.u, self.f, self.out = e(FFN), e(FFN), e(FFN), e(HIDDEN)
+
+    def step(self, position, stream=None):
+        """One decode step for the token at `position` (its K/V row is
+        written there; attention reads rows 0..position)."""
+        c, p = self.ctx, lambda t: t.data_ptr()  # noqa: E731
+        c.rmsnorm_dev(p(self.x), 1, HIDDEN, p(self.g_attn), 1, EPS, p(self.xn), stream=stream)
+        c.matmul_dev(self.w["q"], p(self.xn), 1, HIDDEN, p(self.q), int8=self.int8, stream=stream)
+        c.matmul_dev(self.w["k"], p(self.xn), 1, HIDDEN, p(self.k), int8=self.int8, stream=stream)
+        c.matmul_dev(self.w["v"], p(self.xn), 1, HIDDEN, p(self.v), int8=self.int8, stream=stream)
+        c.rope_dev(p(self.q), 1, HEADS * HEAD_DIM, THETA, 1.0, HEAD_DIM, position, HEADS, p(self.q), stream=stream)
+        c.rope_dev(p(self.k), 1, KV_HEADS * HEAD_DIM, THETA, 1.0, HEAD_DIM, position, KV_HEADS, p(self.k),
+                   stream=stream)
+        width = KV_HEADS * HEAD_DIM
+        c.kv_write_dev(p(self.k_cache), self.capacity, width, p(self.k), 1, position, stream=stream)
+        c.kv_write_dev(p(self.v_cache), self.capacity, width, p(self.v), 1, position, stream=stream)
+        c.attention_dev(p(self.q), 1, p(self.k_cache), p(self.v_cache), self.capacity, position + 1, HEADS,
+                        HEAD_DIM, KV_HEADS, p(self.a), causal=True, stream=stream)
+        c.matmul_add_dev(self.w["o"], p(self.a), 1, HEADS * HEAD_DIM, p(self.x), 1, p(self.h), int8=self.int8,
+                         stream=stream)
+        c.rmsnorm_dev(p(self.h), 1, HIDDEN, p(self.g_ffn), 1, EPS, p(self.hn), stream=stream)
+        c.matmul_dev(self.w["gate"], p(self.hn), 1, HIDDEN, p(self.g), int8=self.int8, stream=stream)
+        c.matmul_dev(self.w["up"], p(self.hn), 1, HIDDEN, p(self.u), int8=self.int8, stream=stream)
+        c.silu_mul_dev(p(self.g), p(self.u), FFN, p(self.f), stream=stream)
+        c.matmul_add_dev(self.w["down"], p(self.f), 1, FFN, p(self.h), 1, p(self.out), int8=self.int8,
+                         stream=stream)
+        return self.out
+
+    def release(self):
+        for w in self.w.values():
+            w.release()
+        self.w = {}
+
+
+def reference_step(data, position, oracle, int8=True):
+    """The same step on the CPU oracle (test infrastructure): the packed
+    matmuls through the reference's scalar column kernel in the same
+    activation mode, the other operators as restated in oracle/layer.c.
+    Returns (out, k_cache, v_cache) with the caches updated."""
+    def mm(name, x):
+        n, k = PROJECTIONS[name]
+        return oracle.columns_scalar(Q4_K, data.weights[name], n, k, x, int8)
+
+    k_cache, v_cache = data.k_cache.copy(), data.v_cache.copy()
+    xn = oracle.rmsnorm(data.x, data.g_attn, EPS)
+    q = oracle.rope(mm("q", xn), THETA, 1.0, HEAD_DIM, position, HEADS)
+    k = oracle.rope(mm("k", xn), THETA, 1.0, HEAD_DIM, position, KV_HEADS)
+    v = mm("v", xn)
+    oracle.kv_write(k_cache, k, position)
+    oracle.kv_write(v_cache, v, position)
+    a = oracle.attention(q, k_cache[:position + 1], v_cache[:position + 1], HEADS, HEAD_DIM, KV_HEADS, True)
+    h = oracle.add(data.x, mm("o", a))
+    hn = oracle.rmsnorm(h, data.g_ffn, EPS)
+    f = oracle.silu_mul(mm("gate", hn), mm("up", hn))
+    out = oracle.add(h, mm("down", f))
+    return out, k_cache, v_cache

@@ -11,6 +11,8 @@ Makefile here) restates, in C, the reference's
  - int8 activation quantizer and scalar dot (quant.rs:340-388),
  - scalar int8 / f32 column kernel (quant.rs:559-597),
  - dense f32 matmul (src/lib.rs:262-318),
+ - the decoder-layer operators rmsnorm, rope, kv-write, attention, silu-mul
+   and add (src/lib.rs:348-402, 427-687, 740-990, 993-1133, 2592-2596),
  - and, as the timed CPU baseline, the AVX2 Q4_K / IQ4_XS column kernels
    with the column chunking and worker pool (quant.rs:666-744, 956-984,
    1364-1433; src/native/mod.rs:110-152; src/native/pool.rs:58-155).
@@ -65,6 +67,14 @@ def lib():
         L.bl_half_f16c.argtypes = [ctypes.c_uint16]
         L.bl_packed_matmul.argtypes = [ctypes.c_int, u8p, u64, u64, f32p, u64,
                                        ctypes.c_int, f32p]
+        f32 = ctypes.c_float
+        L.or_rmsnorm.argtypes = [f32p, u64, u64, f32p, u64, f32, f32p]
+        L.or_rope.argtypes = [f32p, u64, u64, f32, f32, u64, u64, u64, ctypes.c_int, f32p]
+        L.or_kv_write.argtypes = [f32p, u64, u64, f32p, u64, u64]
+        L.or_attention.argtypes = [f32p, u64, f32p, f32p, u64, u64, u64, u64, ctypes.c_int, f32, f32p, f32p]
+        L.or_silu_mul.argtypes = [f32p, f32p, u64, f32p]
+        L.or_silu_mul.restype = None
+        L.or_add.argtypes = [f32p, u64, f32p, u64, f32p]
         _lib = L
     return _lib
 
@@ -179,4 +189,80 @@ def baseline_packed_matmul(fmt, data, n, k, x, threads):
                                 x.shape[0], threads, _p(out, ctypes.c_float))
     if rc:
         raise RuntimeError(f"baseline packed matmul failed ({rc})")
+    return out
+
+
+# ---- decoder-layer operators ----------------------------------------------------
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def rmsnorm(x, w, epsilon):
+    """`rmsnorm` (src/lib.rs:348-402): x [rows, cols], w [cols] or [rows, cols]."""
+    x, w = _f32(x), _f32(w)
+    cols = x.shape[-1]
+    rows = x.size // cols
+    out = np.empty_like(x)
+    rc = lib().or_rmsnorm(_p(x, ctypes.c_float), rows, cols, _p(w, ctypes.c_float), w.size // cols,
+                          float(epsilon), _p(out, ctypes.c_float))
+    if rc:
+        raise ValueError("rmsnorm: unsupported shape or epsilon")
+    return out
+
+
+def rope(x, base, scale, dimension, position_offset, head_count, half_split=False):
+    """`rope` with unscaled frequencies (src/lib.rs:427-447, 616-687)."""
+    x = _f32(x)
+    rows, cols = x.shape
+    out = np.empty_like(x)
+    rc = lib().or_rope(_p(x, ctypes.c_float), rows, cols, float(base), float(scale), dimension, position_offset,
+                       head_count, int(half_split), _p(out, ctypes.c_float))
+    if rc:
+        raise ValueError("rope: unsupported arguments")
+    return out
+
+
+def kv_write(store, rows, row_offset):
+    """`kv-write` in place (src/lib.rs:740-768); returns the store."""
+    assert store.dtype == np.float32 and store.flags.c_contiguous
+    rows = _f32(rows)
+    capacity, width = store.shape
+    rc = lib().or_kv_write(_p(store, ctypes.c_float), capacity, width, _p(rows, ctypes.c_float), rows.shape[0],
+                           row_offset)
+    if rc:
+        raise ValueError("kv-write exceeds the store")
+    return store
+
+
+def attention(q, k, v, head_count, head_dimension, kv_head_count, causal=True, scale=None):
+    """`attention` (src/lib.rs:780-990): q [seq, heads*dim], k/v [kv_seq, kv_heads*dim]."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    seq, kv_seq = q.shape[0], k.shape[0]
+    out = np.empty_like(q)
+    scores = np.empty(kv_seq, np.float32)
+    rc = lib().or_attention(_p(q, ctypes.c_float), seq, _p(k, ctypes.c_float), _p(v, ctypes.c_float), kv_seq,
+                            head_count, head_dimension, kv_head_count, int(causal),
+                            float("nan") if scale is None else float(scale), _p(scores, ctypes.c_float),
+                            _p(out, ctypes.c_float))
+    if rc:
+        raise ValueError("attention: unsupported shape")
+    return out
+
+
+def silu_mul(gate, up):
+    """`silu-mul` (src/lib.rs:2592-2596)."""
+    gate, up = _f32(gate), _f32(up)
+    out = np.empty_like(gate)
+    lib().or_silu_mul(_p(gate, ctypes.c_float), _p(up, ctypes.c_float), gate.size, _p(out, ctypes.c_float))
+    return out
+
+
+def add(a, b):
+    """`add` / `residual-add` (src/lib.rs:1019-1075, 1128-1133)."""
+    a, b = _f32(a), _f32(b)
+    out = np.empty_like(a)
+    rc = lib().or_add(_p(a, ctypes.c_float), a.size, _p(b, ctypes.c_float), b.size, _p(out, ctypes.c_float))
+    if rc:
+        raise ValueError("add: shapes do not broadcast")
     return out

@@ -67,6 +67,21 @@ int bl_packed_matmul(int fmt, const uint8_t *bytes, uint64_t n, uint64_t k,
 int bl_has_avx2(void);
 float bl_half_f16c(uint16_t bits);
 
+/* Decoder-layer operators (layer.c). Return 0, or -1 on a shape or
+ * argument the reference rejects. */
+int or_rmsnorm(const float *x, uint64_t rows, uint64_t cols, const float *w, uint64_t w_rows, float epsilon,
+               float *out);
+int or_rope(const float *x, uint64_t rows, uint64_t cols, float base, float scale, uint64_t dimension,
+            uint64_t position_offset, uint64_t head_count, int half_split, float *out);
+int or_kv_write(float *store, uint64_t capacity, uint64_t width, const float *rows, uint64_t count,
+                uint64_t row_offset);
+/* scores: kv_seq floats of scratch */
+int or_attention(const float *q, uint64_t seq, const float *k, const float *v, uint64_t kv_seq, uint64_t heads,
+                 uint64_t head_dim, uint64_t kv_heads, int causal, float score_scale, float *scores,
+                 float *out);
+void or_silu_mul(const float *gate, const float *up, uint64_t n, float *out);
+int or_add(const float *a, uint64_t n, const float *b, uint64_t b_n, float *out);
+
 #ifdef __cplusplus
 }
 #endif
