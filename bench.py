@@ -10,9 +10,11 @@ launched from HIP graphs (captured once) so host launch cost does not hide
 the device time.
 
 Also reported: the GEMV kernel alone against the 8 TB/s HBM roofline, the
-M=512 prefill GEMM (x[512, 4096] . W[14336, 4096]^T) in TFLOP/s against the
-2.5 PFLOP/s dense f16 MFMA peak, and the reference's CPU path (the
-oracle's AVX2 restatement) timed on this host's cores.
+other decode shapes, one Llama-3-8B-shaped decoder layer decode step
+(device-resident, weights + KV cache bytes per step), the M=512 prefill
+GEMM (x[512, 4096] . W[14336, 4096]^T) in TFLOP/s against the 2.5 PFLOP/s
+dense f16 MFMA peak, and the reference's CPU path (the oracle's AVX2
+restatement) timed on this host's cores.
 """
 
 import argparse
@@ -126,7 +128,7 @@ def main():
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=8.0, help="bound on CPU-baseline timing")
-    ap.add_argument("--parts", default="gemv,shapes,iq4xs,gemm,cpu",
+    ap.add_argument("--parts", default="gemv,shapes,iq4xs,layer,gemm,cpu",
                     help="comma list of parts to run (the headline line needs gemv)")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="also run a plain device copy of this size (counter calibration under rocprofv3)")
@@ -235,6 +237,8 @@ def main():
 
     if "iq4xs" in parts:
         iq4xs_part(ctx, torch, workloads, args, per_graph, use_graph, extra)
+    if "layer" in parts:
+        layer_part(ctx, torch, per_graph, use_graph, extra)
     gemm = gemm_part(ctx, torch, workloads, use_graph, args) if "gemm" in parts else None
     cpu = cpu_part(fmt, wbytes, n, k, x_host, y_gpu, weight_bytes, args) if "cpu" in parts else None
 
@@ -273,6 +277,33 @@ def iq4xs_part(ctx, torch, workloads, args, per_graph, use_graph, extra):
     log(f"iq4xs gemv kernel: {t * 1e6:.2f} us, {ibytes / t / 1e9:.1f} GB/s")
     for h in icopies:
         h.release()
+
+
+def layer_part(ctx, torch, per_graph, use_graph, extra):
+    # ---- one Llama-3-8B-shaped decoder layer decode step (seed 4) ----------------
+    from magnetar_gpu import decoder
+
+    data = decoder.LayerData(seed=4)
+    layer = decoder.DecoderLayer(ctx, torch, data)
+    position = data.prefilled  # the token after the 4095 cached ones
+
+    def step(i, stream):
+        layer.step(position, stream=stream)
+
+    per = max(10, per_graph // 10)
+    r = GraphRunner(torch, step, per, use_graph)
+    r.time(per)
+    calls = 10 * per
+    t = r.time(calls) / calls
+    kv_bytes = 2 * (position + 1) * decoder.KV_HEADS * decoder.HEAD_DIM * 4
+    hbm = data.weight_bytes() + kv_bytes
+    extra["layer_decode_step_us"] = round(t * 1e6, 2)
+    extra["layer_decode_step_bytes"] = hbm
+    extra["layer_decode_step_GBps"] = round(hbm / t / 1e9, 1)
+    extra["layer_decode_step_frac_hbm"] = round(hbm / t / 1e9 / HBM_PEAK_GBS, 4)
+    log(f"decoder layer decode step: {t * 1e6:.1f} us, {hbm} HBM bytes (Q4_K weights {data.weight_bytes()} + "
+        f"f32 K/V {kv_bytes}), {hbm / t / 1e9:.1f} GB/s")
+    layer.release()
 
 
 def gemm_part(ctx, torch, workloads, use_graph, args):

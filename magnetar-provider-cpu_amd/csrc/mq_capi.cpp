@@ -645,9 +645,12 @@ int mq_kv_write_dev(mq_ctx* ctx, float* store_dev, uint64_t capacity, uint64_t w
                                        std::to_string(capacity) + " rows");
   if (count == 0 || width == 0) return MQ_OK;
   if (!store_dev || !rows_dev) return fail(ctx, MQ_ERR_ARGUMENT, "mq_kv_write_dev: null pointer");
+  float* dst = store_dev + row_offset * width;
+  if (dst < rows_dev + count * width && rows_dev < dst + count * width)
+    return fail(ctx, MQ_ERR_ARGUMENT, "kv-write rows overlap the store rows they replace");
   DeviceGuard guard(ctx->device);
-  MQ_HIP(ctx, hipMemcpyAsync(store_dev + row_offset * width, rows_dev, count * width * sizeof(float),
-                             hipMemcpyDeviceToDevice, static_cast<hipStream_t>(stream)));
+  mq::launch_copy(rows_dev, count * width, dst, static_cast<hipStream_t>(stream));
+  MQ_HIP(ctx, hipGetLastError());
   return MQ_OK;
 }
 

@@ -26,6 +26,9 @@ bool launch_attention(const float* q, const float* k, const float* v, uint64_t s
                       uint64_t heads, uint64_t head_dim, uint64_t kv_heads, int causal, float scale, float* part,
                       float* out, hipStream_t stream);
 
+// dst[i] = src[i], i < n (the buffers must not overlap)
+void launch_copy(const float* src, uint64_t n, float* dst, hipStream_t stream);
+
 void launch_silu_mul(const float* g, const float* u, uint64_t n, float* out, hipStream_t stream);
 // out[i] = a[i] + b[i % b_n]
 void launch_add(const float* a, uint64_t n, const float* b, uint64_t b_n, float* out, hipStream_t stream);

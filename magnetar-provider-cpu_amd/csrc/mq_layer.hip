@@ -32,6 +32,7 @@ __device__ inline float wave_max(float v) {
 // and a cross-wave tree; scale = 1 / sqrt(mean + eps) with correctly
 // rounded sqrt and division; out = v * scale * w.
 // ---------------------------------------------------------------------------
+template <bool VEC4>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x, uint64_t cols,
                                                       const float* __restrict__ w, uint64_t w_stride, float eps,
                                                       float* __restrict__ out) {
@@ -39,14 +40,36 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
   const uint64_t row = blockIdx.x;
   const float* v = x + row * cols;
   const float* wv = w + row * w_stride;
+  float* o = out + row * cols;
   float s = 0.0f;
-  for (uint64_t c = threadIdx.x; c < cols; c += 256) s += v[c] * v[c];
+  if (VEC4) {
+#pragma unroll 4
+    for (uint64_t c = 4 * threadIdx.x; c < cols; c += 1024) {
+      const float4 a = *reinterpret_cast<const float4*>(v + c);
+      s += a.x * a.x;
+      s += a.y * a.y;
+      s += a.z * a.z;
+      s += a.w * a.w;
+    }
+  } else {
+    for (uint64_t c = threadIdx.x; c < cols; c += 256) s += v[c] * v[c];
+  }
   s = wave_sum(s);
   if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
   __syncthreads();
   const float total = (part[0] + part[1]) + (part[2] + part[3]);
   const float scale = 1.0f / sqrtf(total / static_cast<float>(cols) + eps);
-  for (uint64_t c = threadIdx.x; c < cols; c += 256) out[row * cols + c] = v[c] * scale * wv[c];
+  if (VEC4) {
+#pragma unroll 4
+    for (uint64_t c = 4 * threadIdx.x; c < cols; c += 1024) {
+      const float4 a = *reinterpret_cast<const float4*>(v + c);
+      const float4 g = *reinterpret_cast<const float4*>(wv + c);
+      *reinterpret_cast<float4*>(o + c) =
+          make_float4(a.x * scale * g.x, a.y * scale * g.y, a.z * scale * g.z, a.w * scale * g.w);
+    }
+  } else {
+    for (uint64_t c = threadIdx.x; c < cols; c += 256) o[c] = v[c] * scale * wv[c];
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -80,12 +103,16 @@ __global__ __launch_bounds__(256) void rope_kernel(const float* x, uint64_t rows
 
 // ---------------------------------------------------------------------------
 // Attention, split over keys (src/lib.rs:780-990). Work-group = one wave =
-// one (kv head, chunk of 64 keys, query row). Scores: lane j owns key j of
-// the chunk and computes the dot with each of the group's query heads;
-// the query values arrive as wave-uniform scalar loads. Softmax partials
-// per chunk and head: m = max score, p = exp(s - m), l = sum p; then
-// lane pairs of value dimensions accumulate o = sum_j p_j v_j with p read
-// from LDS. attention_combine_kernel merges the chunks:
+// one (kv head, chunk of 64 keys, query row).
+//  Scores: lane (kk, s), kk = lane / 8, s = lane % 8, takes keys kk, kk + 8,
+//   ... of the chunk and dimensions 4 s + 32 i .. + 3 (i = 0..3), so each
+//   group of 8 lanes reads one whole 512-byte key row in 128-byte pieces;
+//   the 8 partial dots per key meet by three xor-shuffles.
+//  Softmax partials per head over the chunk: m = max score, p = exp(s - m),
+//   l = sum p.
+//  Values: lane owns dimensions 2 lane, 2 lane + 1 and walks the chunk's
+//   keys (one 512-byte row per step), p read from LDS.
+// attention_combine_kernel merges the chunks of each (head, query row):
 // out = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c.
 // ---------------------------------------------------------------------------
 constexpr int kChunk = 64;
@@ -95,53 +122,69 @@ __global__ __launch_bounds__(64) void attention_partial_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v, uint64_t seq,
     uint64_t key_count, uint64_t heads, uint64_t kv_heads, int causal, float scale,
     float* __restrict__ part) {
-  __shared__ float p_lds[GROUP][kChunk];
-  const int lane = threadIdx.x;
+  static_assert(HD == 128, "one 512-byte row per key and head");
+  __shared__ float s_lds[GROUP][kChunk];
+  const int lane = threadIdx.x, kk = lane >> 3, sl = lane & 7;
   const uint64_t kvh = blockIdx.x, chunk = blockIdx.y, t = blockIdx.z;
   const uint64_t chunks = gridDim.y;
   const uint64_t q_dim = heads * HD, kv_dim = kv_heads * HD;
   const uint64_t upper = causal ? key_count - seq + t + 1 : key_count;
   const uint64_t j0 = chunk * kChunk;
-  const uint64_t j = j0 + lane;
-  const bool live = j < upper;
-  // scores for the GROUP heads of this kv head
-  float s[GROUP];
-#pragma unroll
-  for (int g = 0; g < GROUP; ++g) s[g] = 0.0f;
-  const float* krow = k + (live ? j : 0) * kv_dim + kvh * HD;
+  const uint64_t jn = upper > j0 ? (upper - j0 < kChunk ? upper - j0 : kChunk) : 0;
+  // this lane's 16 query values per head
+  float4 qv[GROUP][4];
   const float* qrow = q + t * q_dim + kvh * GROUP * HD;
-#pragma unroll 4
-  for (int d = 0; d < HD; d += 4) {
-    const float4 kk = *reinterpret_cast<const float4*>(krow + d);
+#pragma unroll
+  for (int g = 0; g < GROUP; ++g)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qv[g][i] = *reinterpret_cast<const float4*>(qrow + g * HD + 4 * sl + 32 * i);
+  const float* kbase = k + kvh * HD + 4 * sl;
+#pragma unroll 2
+  for (int it = 0; it < kChunk / 8; ++it) {
+    const int jl = kk + 8 * it;
+    const bool live = static_cast<uint64_t>(jl) < jn;
+    const float* krow = kbase + (j0 + (live ? jl : 0)) * kv_dim;
+    float4 kv4[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) kv4[i] = *reinterpret_cast<const float4*>(krow + 32 * i);
 #pragma unroll
     for (int g = 0; g < GROUP; ++g) {
-      const float4 qq = *reinterpret_cast<const float4*>(qrow + g * HD + d);
-      s[g] += qq.x * kk.x;
-      s[g] += qq.y * kk.y;
-      s[g] += qq.z * kk.z;
-      s[g] += qq.w * kk.w;
+      float d = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        d += qv[g][i].x * kv4[i].x;
+        d += qv[g][i].y * kv4[i].y;
+        d += qv[g][i].z * kv4[i].z;
+        d += qv[g][i].w * kv4[i].w;
+      }
+      d += __shfl_xor(d, 1);
+      d += __shfl_xor(d, 2);
+      d += __shfl_xor(d, 4);
+      if (sl == 0) s_lds[g][jl] = live ? d * scale : -INFINITY;
     }
   }
+  __syncthreads();
   float m[GROUP], l[GROUP];
+  const bool mine = static_cast<uint64_t>(lane) < jn;
 #pragma unroll
   for (int g = 0; g < GROUP; ++g) {
-    const float sc = live ? s[g] * scale : -INFINITY;
+    const float sc = s_lds[g][lane];
     m[g] = wave_max(sc);
-    const float p = live ? expf(sc - m[g]) : 0.0f;
+    const float p = mine ? expf(sc - m[g]) : 0.0f;
     l[g] = wave_sum(p);
-    p_lds[g][lane] = p;
+    s_lds[g][lane] = p;  // each lane rewrites only its own entry
   }
   __syncthreads();
-  // o: lane owns dims 2 lane, 2 lane + 1 (HD == 128)
   float o[GROUP][2];
 #pragma unroll
   for (int g = 0; g < GROUP; ++g) o[g][0] = o[g][1] = 0.0f;
-  const uint64_t jn = upper > j0 ? (upper - j0 < kChunk ? upper - j0 : kChunk) : 0;
+  const float* vbase = v + kvh * HD + 2 * lane;
+#pragma unroll 4
   for (uint64_t jj = 0; jj < jn; ++jj) {
-    const float2 vv = *reinterpret_cast<const float2*>(v + (j0 + jj) * kv_dim + kvh * HD + 2 * lane);
+    const float2 vv = *reinterpret_cast<const float2*>(vbase + (j0 + jj) * kv_dim);
 #pragma unroll
     for (int g = 0; g < GROUP; ++g) {
-      const float p = p_lds[g][jj];
+      const float p = s_lds[g][jj];
       o[g][0] += p * vv.x;
       o[g][1] += p * vv.y;
     }
@@ -155,27 +198,48 @@ __global__ __launch_bounds__(64) void attention_partial_kernel(
       dst[0] = jn ? m[g] : -INFINITY;
       dst[1] = jn ? l[g] : 0.0f;
     }
-    dst[2 + 2 * lane] = o[g][0];
-    dst[3 + 2 * lane] = o[g][1];
+    *reinterpret_cast<float2*>(dst + 2 + 2 * lane) = make_float2(o[g][0], o[g][1]);
   }
 }
 
+// One work-group of HD threads per (head, query row): the chunks' maxima and
+// weights go through LDS once, then each thread adds its dimension over the
+// chunks with independent loads.
 template <int HD>
 __global__ __launch_bounds__(HD) void attention_combine_kernel(const float* __restrict__ part, uint64_t heads,
                                                               uint64_t chunks, float* __restrict__ out) {
+  __shared__ float w_lds[1024];
+  __shared__ float red[HD / 64];
   const uint64_t h = blockIdx.x, t = blockIdx.y;
   const int d = threadIdx.x;
   const float* base = part + (t * heads + h) * chunks * (2 + HD);
+  // maxima
   float mx = -INFINITY;
-  for (uint64_t c = 0; c < chunks; ++c) mx = fmaxf(mx, base[c * (2 + HD)]);
-  float num = 0.0f, den = 0.0f;
-  for (uint64_t c = 0; c < chunks; ++c) {
+  for (uint64_t c = d; c < chunks; c += HD) mx = fmaxf(mx, base[c * (2 + HD)]);
+  mx = wave_max(mx);
+  if ((d & 63) == 0) red[d >> 6] = mx;
+  __syncthreads();
+  mx = red[0];
+#pragma unroll
+  for (int i = 1; i < HD / 64; ++i) mx = fmaxf(mx, red[i]);
+  __syncthreads();
+  // weights e^(m_c - M) (0 for an empty chunk) and the denominator
+  float den = 0.0f;
+  for (uint64_t c = d; c < chunks; c += HD) {
     const float mc = base[c * (2 + HD)];
-    if (mc == -INFINITY) continue;
-    const float e = expf(mc - mx);
+    const float e = mc == -INFINITY ? 0.0f : expf(mc - mx);
+    w_lds[c] = e;
     den += e * base[c * (2 + HD) + 1];
-    num += e * base[c * (2 + HD) + 2 + d];
   }
+  den = wave_sum(den);
+  if ((d & 63) == 0) red[d >> 6] = den;
+  __syncthreads();
+  den = red[0];
+#pragma unroll
+  for (int i = 1; i < HD / 64; ++i) den += red[i];
+  float num = 0.0f;
+#pragma unroll 8
+  for (uint64_t c = 0; c < chunks; ++c) num += w_lds[c] * base[c * (2 + HD) + 2 + d];
   out[t * heads * HD + h * HD + d] = num / den;
 }
 
@@ -200,14 +264,29 @@ __global__ __launch_bounds__(256) void add_kernel(const float* __restrict__ a, u
   out[i] = a[i] + b[i % b_n];
 }
 
+// kv-write: a plain copy of `n` floats (a kernel rather than a DMA copy:
+// its launch costs a fraction of a blit's for the few-KB rows of a decode
+// step)
+__global__ __launch_bounds__(256) void copy_kernel(const float* __restrict__ src, uint64_t n,
+                                                   float* __restrict__ dst) {
+  const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) dst[i] = src[i];
+}
+
 unsigned blocks_for(uint64_t n, unsigned per) { return static_cast<unsigned>((n + per - 1) / per); }
 
 }  // namespace
 
 void launch_rmsnorm(const float* x, uint64_t rows, uint64_t cols, const float* w, uint64_t w_stride, float eps,
                     float* out, hipStream_t stream) {
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(static_cast<unsigned>(rows)), dim3(256), 0, stream, x, cols, w, w_stride,
-                     eps, out);
+  const bool vec4 = cols % 4 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(w) % 16 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0;
+  if (vec4)
+    hipLaunchKernelGGL(rmsnorm_kernel<true>, dim3(static_cast<unsigned>(rows)), dim3(256), 0, stream, x, cols, w,
+                       w_stride, eps, out);
+  else
+    hipLaunchKernelGGL(rmsnorm_kernel<false>, dim3(static_cast<unsigned>(rows)), dim3(256), 0, stream, x, cols, w,
+                       w_stride, eps, out);
 }
 
 void launch_rope(const float* x, uint64_t rows, uint64_t cols, uint64_t head_count, uint64_t dimension, float scale,
@@ -224,7 +303,7 @@ uint64_t attention_chunks(uint64_t key_count) { return (key_count + kChunk - 1) 
 bool launch_attention(const float* q, const float* k, const float* v, uint64_t seq, uint64_t key_count,
                       uint64_t heads, uint64_t head_dim, uint64_t kv_heads, int causal, float scale, float* part,
                       float* out, hipStream_t stream) {
-  if (head_dim != 128) return false;
+  if (head_dim != 128 || attention_chunks(key_count) > 1024) return false;
   const uint64_t group = heads / kv_heads, chunks = attention_chunks(key_count);
   dim3 grid(static_cast<unsigned>(kv_heads), static_cast<unsigned>(chunks), static_cast<unsigned>(seq));
   switch (group) {
@@ -249,6 +328,10 @@ void launch_silu_mul(const float* g, const float* u, uint64_t n, float* out, hip
 
 void launch_add(const float* a, uint64_t n, const float* b, uint64_t b_n, float* out, hipStream_t stream) {
   hipLaunchKernelGGL(add_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, a, n, b, b_n, out);
+}
+
+void launch_copy(const float* src, uint64_t n, float* dst, hipStream_t stream) {
+  hipLaunchKernelGGL(copy_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, src, n, dst);
 }
 
 }  // namespace mq

@@ -83,24 +83,27 @@ class DecoderLayer:
         self.capacity = data.capacity
         e = lambda n: torch.empty((1, n), dtype=torch.float32, device=dev)  # noqa: E731
         self.x = t(data.x)
-        self.xn, self.q, self.k, self.v = e(HIDDEN), e(HEADS * HEAD_DIM), e(KV_HEADS * HEAD_DIM), e(KV_HEADS * HEAD_DIM)
+        self.xn, self.q, self.k = e(HIDDEN), e(HEADS * HEAD_DIM), e(KV_HEADS * HEAD_DIM)
         self.a, self.h, self.hn = e(HEADS * HEAD_DIM), e(HIDDEN), e(HIDDEN)
         self.g, self.u, self.f, self.out = e(FFN), e(FFN), e(FFN), e(HIDDEN)
 
     def step(self, position, stream=None):
         """One decode step for the token at `position` (its K/V row is
         written there; attention reads rows 0..position)."""
+        if not 0 <= position < self.capacity:
+            raise ValueError(f"position {position} outside the {self.capacity}-row KV cache")
         c, p = self.ctx, lambda t: t.data_ptr()  # noqa: E731
         c.rmsnorm_dev(p(self.x), 1, HIDDEN, p(self.g_attn), 1, EPS, p(self.xn), stream=stream)
+        # kv-write fused into the producers: the V projection and K's rope
+        # write straight into the caches' row `position`
+        width = KV_HEADS * HEAD_DIM
+        k_row = p(self.k_cache) + position * width * 4
+        v_row = p(self.v_cache) + position * width * 4
         c.matmul_dev(self.w["q"], p(self.xn), 1, HIDDEN, p(self.q), int8=self.int8, stream=stream)
         c.matmul_dev(self.w["k"], p(self.xn), 1, HIDDEN, p(self.k), int8=self.int8, stream=stream)
-        c.matmul_dev(self.w["v"], p(self.xn), 1, HIDDEN, p(self.v), int8=self.int8, stream=stream)
+        c.matmul_dev(self.w["v"], p(self.xn), 1, HIDDEN, v_row, int8=self.int8, stream=stream)
         c.rope_dev(p(self.q), 1, HEADS * HEAD_DIM, THETA, 1.0, HEAD_DIM, position, HEADS, p(self.q), stream=stream)
-        c.rope_dev(p(self.k), 1, KV_HEADS * HEAD_DIM, THETA, 1.0, HEAD_DIM, position, KV_HEADS, p(self.k),
-                   stream=stream)
-        width = KV_HEADS * HEAD_DIM
-        c.kv_write_dev(p(self.k_cache), self.capacity, width, p(self.k), 1, position, stream=stream)
-        c.kv_write_dev(p(self.v_cache), self.capacity, width, p(self.v), 1, position, stream=stream)
+        c.rope_dev(p(self.k), 1, width, THETA, 1.0, HEAD_DIM, position, KV_HEADS, k_row, stream=stream)
         c.attention_dev(p(self.q), 1, p(self.k_cache), p(self.v_cache), self.capacity, position + 1, HEADS,
                         HEAD_DIM, KV_HEADS, p(self.a), causal=True, stream=stream)
         c.matmul_add_dev(self.w["o"], p(self.a), 1, HEADS * HEAD_DIM, p(self.x), 1, p(self.h), int8=self.int8,
