@@ -1858,11 +1858,13 @@ bool launch_gemv_fused(int type, const uint8_t* tiled, uint64_t rows, uint64_t n
 // K-splits for the LDS form: only when the row blocks alone leave most of
 // the 256 CUs idle (4096 rows: 64 blocks -> 4 splits; 14336 rows: 224
 // blocks -> none, where the split-K epilogue costs more than the last 32
-// CUs would bring).
+// CUs would bring), and at most 4: each work-group's chain of activation
+// staging, barrier, partial stores and ticket is a fixed latency, and
+// measured at 1024 x 4096, 4 splits take 6.9 us where 16 take 12.0 us.
 int gemv_default_ksplit(uint64_t rows, uint64_t nb) {
   const uint64_t blocks = (rows + 63) / 64;
   int ks = 1;
-  while (blocks * 2 * ks <= 320 && static_cast<uint64_t>(2 * ks) <= nb && ks < 16) ks *= 2;
+  while (blocks * 2 * ks <= 320 && static_cast<uint64_t>(2 * ks) <= nb && ks < 4) ks *= 2;
   return ks;
 }
 

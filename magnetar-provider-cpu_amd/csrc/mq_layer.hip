@@ -102,145 +102,173 @@ __global__ __launch_bounds__(256) void rope_kernel(const float* x, uint64_t rows
 }
 
 // ---------------------------------------------------------------------------
-// Attention, split over keys (src/lib.rs:780-990). Work-group = one wave =
-// one (kv head, chunk of 64 keys, query row).
-//  Scores: lane (kk, s), kk = lane / 8, s = lane % 8, takes keys kk, kk + 8,
-//   ... of the chunk and dimensions 4 s + 32 i .. + 3 (i = 0..3), so each
-//   group of 8 lanes reads one whole 512-byte key row in 128-byte pieces;
-//   the 8 partial dots per key meet by three xor-shuffles.
-//  Softmax partials per head over the chunk: m = max score, p = exp(s - m),
-//   l = sum p.
-//  Values: lane owns dimensions 2 lane, 2 lane + 1 and walks the chunk's
-//   keys (one 512-byte row per step), p read from LDS.
+// Attention, split over keys (src/lib.rs:780-990). Work-group = 4 waves =
+// one (kv head, chunk of 64 keys, query row); wave w takes the chunk's keys
+// 16 w .. 16 w + 15, so a chunk's 64 KB of K and V rows are in flight at
+// once over 4 waves.
+//  Scores: lane (kk, s), kk = lane / 8, s = lane % 8, takes keys kk and
+//   kk + 8 of the wave's 16 and dimensions 4 s + 32 i .. + 3 (i = 0..3), so
+//   each group of 8 lanes reads one whole 512-byte key row in 128-byte
+//   pieces; the 8 partial dots per key meet by three xor-shuffles.
+//  Softmax partials per head over the chunk (wave g % 4 takes head g of the
+//   group): m = max score, p = exp(s - m), l = sum p.
+//  Values: lane owns dimensions 2 lane, 2 lane + 1 of the wave's 16 keys;
+//   the 4 waves' sums meet in LDS in wave order.
 // attention_combine_kernel merges the chunks of each (head, query row):
 // out = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c.
+// Every sum is in a fixed order that depends only on the chunk, so the
+// last row of a causal prefill equals the one-row decode step bit for bit.
 // ---------------------------------------------------------------------------
 constexpr int kChunk = 64;
+constexpr int kWaveKeys = 16;
 
 template <int GROUP, int HD>
-__global__ __launch_bounds__(64) void attention_partial_kernel(
+__global__ __launch_bounds__(256) void attention_partial_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v, uint64_t seq,
     uint64_t key_count, uint64_t heads, uint64_t kv_heads, int causal, float scale,
     float* __restrict__ part) {
   static_assert(HD == 128, "one 512-byte row per key and head");
   __shared__ float s_lds[GROUP][kChunk];
-  const int lane = threadIdx.x, kk = lane >> 3, sl = lane & 7;
+  __shared__ float ml_lds[GROUP][2];
+  __shared__ float o_lds[4][GROUP][HD];
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, kk = lane >> 3, sl = lane & 7;
   const uint64_t kvh = blockIdx.x, chunk = blockIdx.y, t = blockIdx.z;
   const uint64_t chunks = gridDim.y;
   const uint64_t q_dim = heads * HD, kv_dim = kv_heads * HD;
   const uint64_t upper = causal ? key_count - seq + t + 1 : key_count;
   const uint64_t j0 = chunk * kChunk;
   const uint64_t jn = upper > j0 ? (upper - j0 < kChunk ? upper - j0 : kChunk) : 0;
-  // this lane's 16 query values per head
-  float4 qv[GROUP][4];
-  const float* qrow = q + t * q_dim + kvh * GROUP * HD;
-#pragma unroll
-  for (int g = 0; g < GROUP; ++g)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) qv[g][i] = *reinterpret_cast<const float4*>(qrow + g * HD + 4 * sl + 32 * i);
+  float* dst0 = part + ((t * heads + kvh * GROUP) * chunks + chunk) * (2 + HD);
+  if (jn == 0) {  // uniform over the work-group: an empty chunk
+    for (int e = threadIdx.x; e < GROUP * (2 + HD); e += 256) {
+      const int g = e / (2 + HD), i = e % (2 + HD);
+      dst0[g * chunks * (2 + HD) + i] = i == 0 ? -INFINITY : 0.0f;
+    }
+    return;
+  }
+  // scores of keys 16 w + kk and 16 w + 8 + kk
+  float4 kv4[2][4];
   const float* kbase = k + kvh * HD + 4 * sl;
-#pragma unroll 2
-  for (int it = 0; it < kChunk / 8; ++it) {
-    const int jl = kk + 8 * it;
-    const bool live = static_cast<uint64_t>(jl) < jn;
-    const float* krow = kbase + (j0 + (live ? jl : 0)) * kv_dim;
-    float4 kv4[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) kv4[i] = *reinterpret_cast<const float4*>(krow + 32 * i);
+  for (int it = 0; it < 2; ++it) {
+    const int jl = kWaveKeys * w + 8 * it + kk;
+    const float* krow = kbase + (j0 + (static_cast<uint64_t>(jl) < jn ? jl : 0)) * kv_dim;
 #pragma unroll
-    for (int g = 0; g < GROUP; ++g) {
+    for (int i = 0; i < 4; ++i) kv4[it][i] = *reinterpret_cast<const float4*>(krow + 32 * i);
+  }
+  const float* qrow = q + t * q_dim + kvh * GROUP * HD + 4 * sl;
+#pragma unroll
+  for (int g = 0; g < GROUP; ++g) {
+    float4 qv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qv[i] = *reinterpret_cast<const float4*>(qrow + g * HD + 32 * i);
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
       float d = 0.0f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        d += qv[g][i].x * kv4[i].x;
-        d += qv[g][i].y * kv4[i].y;
-        d += qv[g][i].z * kv4[i].z;
-        d += qv[g][i].w * kv4[i].w;
+        d += qv[i].x * kv4[it][i].x;
+        d += qv[i].y * kv4[it][i].y;
+        d += qv[i].z * kv4[it][i].z;
+        d += qv[i].w * kv4[it][i].w;
       }
       d += __shfl_xor(d, 1);
       d += __shfl_xor(d, 2);
       d += __shfl_xor(d, 4);
-      if (sl == 0) s_lds[g][jl] = live ? d * scale : -INFINITY;
+      const int jl = kWaveKeys * w + 8 * it + kk;
+      if (sl == 0) s_lds[g][jl] = static_cast<uint64_t>(jl) < jn ? d * scale : -INFINITY;
     }
   }
   __syncthreads();
-  float m[GROUP], l[GROUP];
   const bool mine = static_cast<uint64_t>(lane) < jn;
-#pragma unroll
-  for (int g = 0; g < GROUP; ++g) {
+  for (int g = w; g < GROUP; g += 4) {
     const float sc = s_lds[g][lane];
-    m[g] = wave_max(sc);
-    const float p = mine ? expf(sc - m[g]) : 0.0f;
-    l[g] = wave_sum(p);
+    const float m = wave_max(sc);
+    const float p = mine ? expf(sc - m) : 0.0f;
+    const float l = wave_sum(p);
     s_lds[g][lane] = p;  // each lane rewrites only its own entry
+    if (lane == 0) {
+      ml_lds[g][0] = m;
+      ml_lds[g][1] = l;
+    }
   }
   __syncthreads();
-  float o[GROUP][2];
-#pragma unroll
-  for (int g = 0; g < GROUP; ++g) o[g][0] = o[g][1] = 0.0f;
+  // values of keys 16 w .. 16 w + 15 (rows past jn weigh 0 and read row j0)
+  float2 vv[kWaveKeys];
   const float* vbase = v + kvh * HD + 2 * lane;
-#pragma unroll 4
-  for (uint64_t jj = 0; jj < jn; ++jj) {
-    const float2 vv = *reinterpret_cast<const float2*>(vbase + (j0 + jj) * kv_dim);
 #pragma unroll
-    for (int g = 0; g < GROUP; ++g) {
-      const float p = s_lds[g][jj];
-      o[g][0] += p * vv.x;
-      o[g][1] += p * vv.y;
-    }
+  for (int jj = 0; jj < kWaveKeys; ++jj) {
+    const int jl = kWaveKeys * w + jj;
+    vv[jj] = *reinterpret_cast<const float2*>(vbase + (j0 + (static_cast<uint64_t>(jl) < jn ? jl : 0)) * kv_dim);
   }
-  // part layout: [t][head][chunk][2 + HD]
 #pragma unroll
   for (int g = 0; g < GROUP; ++g) {
-    const uint64_t h = kvh * GROUP + g;
-    float* dst = part + ((t * heads + h) * chunks + chunk) * (2 + HD);
-    if (lane == 0) {
-      dst[0] = jn ? m[g] : -INFINITY;
-      dst[1] = jn ? l[g] : 0.0f;
+    float o0 = 0.0f, o1 = 0.0f;
+#pragma unroll
+    for (int jj = 0; jj < kWaveKeys; ++jj) {
+      const float p = s_lds[g][kWaveKeys * w + jj];
+      o0 += p * vv[jj].x;
+      o1 += p * vv[jj].y;
     }
-    *reinterpret_cast<float2*>(dst + 2 + 2 * lane) = make_float2(o[g][0], o[g][1]);
+    *reinterpret_cast<float2*>(&o_lds[w][g][2 * lane]) = make_float2(o0, o1);
+  }
+  __syncthreads();
+  // part layout: [t][head][chunk][2 + HD]
+  for (int e = threadIdx.x; e < GROUP * HD; e += 256) {
+    const int g = e / HD, d = e % HD;
+    const float o = ((o_lds[0][g][d] + o_lds[1][g][d]) + o_lds[2][g][d]) + o_lds[3][g][d];
+    dst0[g * chunks * (2 + HD) + 2 + d] = o;
+  }
+  if (threadIdx.x < GROUP) {
+    dst0[threadIdx.x * chunks * (2 + HD)] = ml_lds[threadIdx.x][0];
+    dst0[threadIdx.x * chunks * (2 + HD) + 1] = ml_lds[threadIdx.x][1];
   }
 }
 
-// One work-group of HD threads per (head, query row): the chunks' maxima and
-// weights go through LDS once, then each thread adds its dimension over the
-// chunks with independent loads.
+// One work-group of 4 waves per (head, query row). Every wave finds the
+// maximum over the chunks; wave 0 writes the weights e^(m_c - M) to LDS and
+// forms the denominator; wave w then adds chunks w, w + 4, ... for all HD
+// dimensions (2 per lane), and the 4 sums meet in LDS in wave order.
 template <int HD>
-__global__ __launch_bounds__(HD) void attention_combine_kernel(const float* __restrict__ part, uint64_t heads,
+__global__ __launch_bounds__(256) void attention_combine_kernel(const float* __restrict__ part, uint64_t heads,
                                                               uint64_t chunks, float* __restrict__ out) {
   __shared__ float w_lds[1024];
-  __shared__ float red[HD / 64];
+  __shared__ float o_lds[4][HD];
+  __shared__ float den_lds;
   const uint64_t h = blockIdx.x, t = blockIdx.y;
-  const int d = threadIdx.x;
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const float* base = part + (t * heads + h) * chunks * (2 + HD);
-  // maxima
   float mx = -INFINITY;
-  for (uint64_t c = d; c < chunks; c += HD) mx = fmaxf(mx, base[c * (2 + HD)]);
+  for (uint64_t c = lane; c < chunks; c += 64) mx = fmaxf(mx, base[c * (2 + HD)]);
   mx = wave_max(mx);
-  if ((d & 63) == 0) red[d >> 6] = mx;
-  __syncthreads();
-  mx = red[0];
-#pragma unroll
-  for (int i = 1; i < HD / 64; ++i) mx = fmaxf(mx, red[i]);
-  __syncthreads();
-  // weights e^(m_c - M) (0 for an empty chunk) and the denominator
-  float den = 0.0f;
-  for (uint64_t c = d; c < chunks; c += HD) {
-    const float mc = base[c * (2 + HD)];
-    const float e = mc == -INFINITY ? 0.0f : expf(mc - mx);
-    w_lds[c] = e;
-    den += e * base[c * (2 + HD) + 1];
+  if (w == 0) {
+    float den = 0.0f;
+    for (uint64_t c = lane; c < chunks; c += 64) {
+      const float mc = base[c * (2 + HD)];
+      const float e = mc == -INFINITY ? 0.0f : expf(mc - mx);
+      w_lds[c] = e;
+      den += e * base[c * (2 + HD) + 1];
+    }
+    den = wave_sum(den);
+    if (lane == 0) den_lds = den;
   }
-  den = wave_sum(den);
-  if ((d & 63) == 0) red[d >> 6] = den;
   __syncthreads();
-  den = red[0];
-#pragma unroll
-  for (int i = 1; i < HD / 64; ++i) den += red[i];
-  float num = 0.0f;
+  float n0 = 0.0f, n1 = 0.0f;
+  const float* col = base + 2 + 2 * lane;
 #pragma unroll 8
-  for (uint64_t c = 0; c < chunks; ++c) num += w_lds[c] * base[c * (2 + HD) + 2 + d];
-  out[t * heads * HD + h * HD + d] = num / den;
+  for (uint64_t c = w; c < chunks; c += 4) {
+    const float2 o = *reinterpret_cast<const float2*>(col + c * (2 + HD));
+    const float e = w_lds[c];
+    n0 += e * o.x;
+    n1 += e * o.y;
+  }
+  *reinterpret_cast<float2*>(&o_lds[w][2 * lane]) = make_float2(n0, n1);
+  __syncthreads();
+  if (threadIdx.x < HD) {
+    const int d = threadIdx.x;
+    const float num = ((o_lds[0][d] + o_lds[1][d]) + o_lds[2][d]) + o_lds[3][d];
+    out[t * heads * HD + h * HD + d] = num / den_lds;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -309,7 +337,7 @@ bool launch_attention(const float* q, const float* k, const float* v, uint64_t s
   switch (group) {
 #define X(G)                                                                                                   \
   case G:                                                                                                      \
-    hipLaunchKernelGGL((attention_partial_kernel<G, 128>), grid, dim3(64), 0, stream, q, k, v, seq, key_count, \
+    hipLaunchKernelGGL((attention_partial_kernel<G, 128>), grid, dim3(256), 0, stream, q, k, v, seq, key_count, \
                        heads, kv_heads, causal, scale, part);                                                  \
     break;
     X(1) X(2) X(4) X(8)
@@ -318,7 +346,7 @@ bool launch_attention(const float* q, const float* k, const float* v, uint64_t s
       return false;
   }
   hipLaunchKernelGGL((attention_combine_kernel<128>), dim3(static_cast<unsigned>(heads), static_cast<unsigned>(seq)),
-                     dim3(128), 0, stream, part, heads, chunks, out);
+                     dim3(256), 0, stream, part, heads, chunks, out);
   return true;
 }
 

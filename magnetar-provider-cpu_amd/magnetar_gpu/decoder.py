@@ -4,13 +4,15 @@ The step is the sequence of Kernels the Runtime submits for one generated
 token, each one an entry point of ``libmagnetar_gpu.so``:
 
     xn  = rmsnorm(x, g_attn, eps)                     (src/lib.rs:348-402)
-    q, k, v = xn . Wq^T, xn . Wk^T, xn . Wv^T          packed matmul (int8 activations)
+    q, k, v = xn . Wq^T, xn . Wk^T, xn . Wv^T          packed matmul (int8 activations),
+                                                       one launch over the stacked rows
     q, k = rope(q), rope(k) at position `position`     (src/lib.rs:427-687)
     K[position], V[position] = k, v                    kv-write (src/lib.rs:740-768)
     a   = attention(q, K, V, key_count = position + 1) (src/lib.rs:780-990)
     h   = x + a . Wo^T                                 matmul-residual (src/lib.rs:2577-2590)
     hn  = rmsnorm(h, g_ffn, eps)
-    f   = silu(hn . Wgate^T) * (hn . Wup^T)            silu-mul (src/lib.rs:2592-2596)
+    f   = silu(hn . Wgate^T) * (hn . Wup^T)            silu-mul (src/lib.rs:2592-2596),
+                                                       gate and up as one launch
     out = h + f . Wdown^T                              matmul-residual
 
 All intermediates stay in HBM (torch tensors used as device allocations);
@@ -30,6 +32,8 @@ HEAD_DIM = 128
 FFN = 14336
 EPS = 1e-5
 THETA = 5e5
+
+QKV_ROWS = (HEADS + 2 * KV_HEADS) * HEAD_DIM
 
 # projection name -> (stored rows N, stored cols K)
 PROJECTIONS = {
@@ -76,16 +80,22 @@ class DecoderLayer:
     def __init__(self, ctx, torch, data, int8=True):
         self.ctx, self.torch, self.int8 = ctx, torch, int8
         dev = "cuda"
-        self.w = {name: ctx.upload(Q4_K, n, k, data.weights[name]) for name, (n, k) in PROJECTIONS.items()}
+        # Q, K and V share their input, as do gate and up: each trio/pair is
+        # uploaded as one matrix of stacked rows (a row's bytes do not
+        # depend on its neighbours) and runs as one launch.
+        w = data.weights
+        self.w = {name: ctx.upload(Q4_K, *PROJECTIONS[name], w[name]) for name in ("o", "down")}
+        self.w["qkv"] = ctx.upload(Q4_K, QKV_ROWS, HIDDEN, np.concatenate([w["q"], w["k"], w["v"]]))
+        self.w["gate_up"] = ctx.upload(Q4_K, 2 * FFN, HIDDEN, np.concatenate([w["gate"], w["up"]]))
         t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
         self.g_attn, self.g_ffn = t(data.g_attn), t(data.g_ffn)
         self.k_cache, self.v_cache = t(data.k_cache), t(data.v_cache)
         self.capacity = data.capacity
         e = lambda n: torch.empty((1, n), dtype=torch.float32, device=dev)  # noqa: E731
         self.x = t(data.x)
-        self.xn, self.q, self.k = e(HIDDEN), e(HEADS * HEAD_DIM), e(KV_HEADS * HEAD_DIM)
+        self.xn, self.qkv = e(HIDDEN), e(QKV_ROWS)
         self.a, self.h, self.hn = e(HEADS * HEAD_DIM), e(HIDDEN), e(HIDDEN)
-        self.g, self.u, self.f, self.out = e(FFN), e(FFN), e(FFN), e(HIDDEN)
+        self.gu, self.f, self.out = e(2 * FFN), e(FFN), e(HIDDEN)
 
     def step(self, position, stream=None):
         """One decode step for the token at `position` (its K/V row is
@@ -94,24 +104,22 @@ class DecoderLayer:
             raise ValueError(f"position {position} outside the {self.capacity}-row KV cache")
         c, p = self.ctx, lambda t: t.data_ptr()  # noqa: E731
         c.rmsnorm_dev(p(self.x), 1, HIDDEN, p(self.g_attn), 1, EPS, p(self.xn), stream=stream)
-        # kv-write fused into the producers: the V projection and K's rope
-        # write straight into the caches' row `position`
+        c.matmul_dev(self.w["qkv"], p(self.xn), 1, HIDDEN, p(self.qkv), int8=self.int8, stream=stream)
+        # q rotated in place; k rotated straight into the K cache's row
+        # `position`; v copied into the V cache's row (kv-write)
         width = KV_HEADS * HEAD_DIM
-        k_row = p(self.k_cache) + position * width * 4
-        v_row = p(self.v_cache) + position * width * 4
-        c.matmul_dev(self.w["q"], p(self.xn), 1, HIDDEN, p(self.q), int8=self.int8, stream=stream)
-        c.matmul_dev(self.w["k"], p(self.xn), 1, HIDDEN, p(self.k), int8=self.int8, stream=stream)
-        c.matmul_dev(self.w["v"], p(self.xn), 1, HIDDEN, v_row, int8=self.int8, stream=stream)
-        c.rope_dev(p(self.q), 1, HEADS * HEAD_DIM, THETA, 1.0, HEAD_DIM, position, HEADS, p(self.q), stream=stream)
-        c.rope_dev(p(self.k), 1, width, THETA, 1.0, HEAD_DIM, position, KV_HEADS, k_row, stream=stream)
-        c.attention_dev(p(self.q), 1, p(self.k_cache), p(self.v_cache), self.capacity, position + 1, HEADS,
+        q, k, v = p(self.qkv), p(self.qkv) + HIDDEN * 4, p(self.qkv) + (HIDDEN + width) * 4
+        c.rope_dev(q, 1, HIDDEN, THETA, 1.0, HEAD_DIM, position, HEADS, q, stream=stream)
+        c.rope_dev(k, 1, width, THETA, 1.0, HEAD_DIM, position, KV_HEADS, p(self.k_cache) + position * width * 4,
+                   stream=stream)
+        c.kv_write_dev(p(self.v_cache), self.capacity, width, v, 1, position, stream=stream)
+        c.attention_dev(q, 1, p(self.k_cache), p(self.v_cache), self.capacity, position + 1, HEADS,
                         HEAD_DIM, KV_HEADS, p(self.a), causal=True, stream=stream)
         c.matmul_add_dev(self.w["o"], p(self.a), 1, HEADS * HEAD_DIM, p(self.x), 1, p(self.h), int8=self.int8,
                          stream=stream)
         c.rmsnorm_dev(p(self.h), 1, HIDDEN, p(self.g_ffn), 1, EPS, p(self.hn), stream=stream)
-        c.matmul_dev(self.w["gate"], p(self.hn), 1, HIDDEN, p(self.g), int8=self.int8, stream=stream)
-        c.matmul_dev(self.w["up"], p(self.hn), 1, HIDDEN, p(self.u), int8=self.int8, stream=stream)
-        c.silu_mul_dev(p(self.g), p(self.u), FFN, p(self.f), stream=stream)
+        c.matmul_dev(self.w["gate_up"], p(self.hn), 1, HIDDEN, p(self.gu), int8=self.int8, stream=stream)
+        c.silu_mul_dev(p(self.gu), p(self.gu) + FFN * 4, FFN, p(self.f), stream=stream)
         c.matmul_add_dev(self.w["down"], p(self.f), 1, FFN, p(self.h), 1, p(self.out), int8=self.int8,
                          stream=stream)
         return self.out
