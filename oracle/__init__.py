@@ -6,7 +6,8 @@ product library (``magnetar-provider-cpu_amd``) never imports it.
 
 ``liboracle.so`` (built from ``oracle.c`` and ``cpu_baseline.c`` by the
 Makefile here) restates, in C, the reference's
- - packed decode (src/native/quant.rs:46-57, 96-121, 196-206, 284-338),
+ - packed decode of Q8_0, Q4_0, IQ4_NL, Q4_K, Q5_K, Q6_K and IQ4_XS
+   (src/native/quant.rs:46-57, 96-149, 180-206, 284-338),
  - dequantization (quant.rs:1702-1711),
  - int8 activation quantizer and scalar dot (quant.rs:340-388),
  - scalar int8 / f32 column kernel (quant.rs:559-597),
@@ -27,9 +28,15 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
 
+Q4_0 = 2
+Q8_0 = 8
 Q4_K = 12
+Q5_K = 13
+Q6_K = 14
+IQ4_NL = 20
 IQ4_XS = 23
-BLOCK_BYTES = {Q4_K: 144, IQ4_XS: 136}
+BLOCK_BYTES = {Q8_0: 34, Q4_0: 18, IQ4_NL: 18, Q4_K: 144, Q5_K: 176, Q6_K: 210, IQ4_XS: 136}
+BLOCK_ELEMENTS = {Q8_0: 32, Q4_0: 32, IQ4_NL: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, IQ4_XS: 256}
 
 _lib = None
 

@@ -46,14 +46,29 @@ float or_f16_to_f32(uint16_t h) {
 }
 
 /* Block geometry (PackedWeightFormat::{block_bytes, block_elements},
- * external; values fixed by the GGUF layouts decoded at quant.rs:110-121
- * and 196-206). */
+ * external; values fixed by the GGUF layouts the decode arms read at
+ * quant.rs:102-206: Q8_0 = f16 d + 32 i8; Q4_0 / IQ4_NL = f16 d + 16
+ * nibble pairs; Q5_K = d, dmin, 12 scale bytes, 32 high-bit bytes, 128
+ * nibble bytes; Q6_K = 128 low, 64 high, 16 i8 scales, f16 d at 208). */
 int or_block_bytes(int fmt) {
-    return fmt == OR_Q4_K ? 144 : fmt == OR_IQ4_XS ? 136 : 0;
+    switch (fmt) {
+    case OR_Q8_0: return 34;
+    case OR_Q4_0: return 18;
+    case OR_IQ4_NL: return 18;
+    case OR_Q4_K: return 144;
+    case OR_Q5_K: return 176;
+    case OR_Q6_K: return 210;
+    case OR_IQ4_XS: return 136;
+    default: return 0;
+    }
 }
 
 int or_block_elements(int fmt) {
-    return (fmt == OR_Q4_K || fmt == OR_IQ4_XS) ? 256 : 0;
+    switch (fmt) {
+    case OR_Q8_0: case OR_Q4_0: case OR_IQ4_NL: return 32;
+    case OR_Q4_K: case OR_Q5_K: case OR_Q6_K: case OR_IQ4_XS: return 256;
+    default: return 0;
+    }
 }
 
 /* src/native/quant.rs:46-57 (`scale_min_k4`). */
@@ -87,24 +102,67 @@ static const int8_t IQ4NL[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
 
 const int8_t *or_iq4nl_values(void) { return IQ4NL; }
 
-/* src/native/quant.rs:96-121 (Q4K arm) and 196-206 (Iq4Xs arm). */
+/* The external `Q4_0_VALUES` (quant.rs:183, 1626): index i stands for
+ * i - 8 ("its quants standing for `q - 8`", quant.rs:180). */
+static const int8_t Q40[16] = {-8, -7, -6, -5, -4, -3, -2, -1,
+                               0,  1,  2,  3,  4,  5,  6,  7};
+
+const int8_t *or_q4_0_values(void) { return Q40; }
+
+static float half_at(const uint8_t *b, int at) {
+    return or_f16_to_f32((uint16_t)(b[at] | (b[at + 1] << 8)));
+}
+
+/* `decode` (src/native/quant.rs:96-206): the Q8_0 (102-109), Q4K (110-121),
+ * Q5K (122-135), Q6K (136-149), Iq4Nl / Q4_0 (180-195) and Iq4Xs (196-206)
+ * arms. `run` counts within the block (always 0 for 32-value blocks). */
 void or_decode_run(int fmt, const uint8_t *block, int run, int8_t q[OR_RUN],
                    float scale[2], float min[2]) {
-    if (fmt == OR_Q4_K) {
-        float d = or_f16_to_f32((uint16_t)(block[0] | (block[1] << 8)));
-        float dmin = or_f16_to_f32((uint16_t)(block[2] | (block[3] << 8)));
+    min[0] = min[1] = 0.0f;
+    if (fmt == OR_Q8_0) {
+        float d = half_at(block, 0);
+        for (int i = 0; i < OR_RUN; i++) q[i] = (int8_t)block[2 + i];
+        scale[0] = scale[1] = d;
+    } else if (fmt == OR_Q4_K || fmt == OR_Q5_K) {
+        float d = half_at(block, 0);
+        float dmin = half_at(block, 2);
         uint8_t sc, m;
         or_scale_min_k4(run, block + 4, &sc, &m);
         int chunk = run / 2;
         int shift = 4 * (run % 2);
-        const uint8_t *qs = block + 16 + 32 * chunk;
-        for (int i = 0; i < OR_RUN; i++) q[i] = (int8_t)((qs[i] >> shift) & 0xF);
+        if (fmt == OR_Q4_K) {
+            const uint8_t *qs = block + 16 + 32 * chunk;
+            for (int i = 0; i < OR_RUN; i++) q[i] = (int8_t)((qs[i] >> shift) & 0xF);
+        } else {
+            const uint8_t *low = block + 48 + 32 * chunk;
+            const uint8_t *high = block + 16;
+            for (int i = 0; i < OR_RUN; i++)
+                q[i] = (int8_t)(((low[i] >> shift) & 0xF) | (((high[i] >> run) & 1) << 4));
+        }
         float s = d * (float)sc;
         float mn = dmin * (float)m;
         scale[0] = scale[1] = s;
         min[0] = min[1] = mn;
+    } else if (fmt == OR_Q6_K) {
+        float d = half_at(block, 208);
+        int h = run / 4, g = run % 4;
+        const uint8_t *low = block + 64 * h + 32 * (g % 2);
+        const uint8_t *high = block + 128 + 32 * h;
+        int low_shift = 4 * (g / 2), high_shift = 2 * g;
+        for (int i = 0; i < OR_RUN; i++)
+            q[i] = (int8_t)((int)(((low[i] >> low_shift) & 0xF) | (((high[i] >> high_shift) & 3) << 4)) - 32);
+        for (int p = 0; p < 2; p++) scale[p] = d * (float)(int8_t)block[192 + 8 * h + 2 * g + p];
+    } else if (fmt == OR_IQ4_NL || fmt == OR_Q4_0) {
+        const int8_t *table = fmt == OR_Q4_0 ? Q40 : IQ4NL;
+        float d = half_at(block, 0);
+        for (int l = 0; l < 16; l++) {
+            uint8_t byte = block[2 + l];
+            q[l] = table[byte & 0xF];
+            q[l + 16] = table[byte >> 4];
+        }
+        scale[0] = scale[1] = d;
     } else {
-        float d = or_f16_to_f32((uint16_t)(block[0] | (block[1] << 8)));
+        float d = half_at(block, 0);
         int8_t ls[8];
         or_iq4_xs_scales(block + 2, ls);
         float s = d * (float)ls[run];
@@ -114,7 +172,6 @@ void or_decode_run(int fmt, const uint8_t *block, int run, int8_t q[OR_RUN],
             q[l + 16] = IQ4NL[byte >> 4];
         }
         scale[0] = scale[1] = s;
-        min[0] = min[1] = 0.0f;
     }
 }
 
@@ -122,15 +179,16 @@ void or_decode_run(int fmt, const uint8_t *block, int run, int8_t q[OR_RUN],
  * (quant.rs:1702-1711): value = scale[p] * q - min[p], p = i / 16. */
 int or_dequantize_rows(int fmt, const uint8_t *bytes, uint64_t rows,
                        uint64_t cols, float *out) {
-    int bb = or_block_bytes(fmt);
-    if (!bb || cols % 256) return -1;
-    uint64_t row_bytes = cols / 256 * (uint64_t)bb;
+    int bb = or_block_bytes(fmt), be = or_block_elements(fmt);
+    if (!bb || cols % (uint64_t)be) return -1;
+    int rpb = be / OR_RUN;
+    uint64_t row_bytes = cols / be * (uint64_t)bb;
     int8_t q[OR_RUN];
     float scale[2], min[2];
     for (uint64_t r = 0; r < rows; r++) {
         for (uint64_t u = 0; u < cols / OR_RUN; u++) {
-            const uint8_t *block = bytes + r * row_bytes + (u / 8) * bb;
-            or_decode_run(fmt, block, (int)(u % 8), q, scale, min);
+            const uint8_t *block = bytes + r * row_bytes + (u / rpb) * bb;
+            or_decode_run(fmt, block, (int)(u % rpb), q, scale, min);
             float *o = out + r * cols + u * OR_RUN;
             for (int i = 0; i < OR_RUN; i++) {
                 int p = i / 16;
@@ -197,10 +255,11 @@ void or_dot_halves(const int8_t *q, const int8_t *a, int32_t out[2]) {
 int or_columns_scalar(int fmt, const uint8_t *bytes, uint64_t n, uint64_t k,
                       const float *x, uint64_t m, int int8,
                       uint64_t first, uint64_t count, float *out) {
-    int bb = or_block_bytes(fmt);
-    if (!bb || k % 256 || first + count > n) return -1;
+    int bb = or_block_bytes(fmt), be = or_block_elements(fmt);
+    if (!bb || k % (uint64_t)be || first + count > n) return -1;
+    int rpb = be / OR_RUN;
     uint64_t runs = k / OR_RUN;
-    uint64_t row_bytes = k / 256 * (uint64_t)bb;
+    uint64_t row_bytes = k / be * (uint64_t)bb;
     int8_t *qv = 0;
     float *qs = 0;
     int32_t *qsum = 0;
@@ -220,8 +279,8 @@ int or_columns_scalar(int fmt, const uint8_t *bytes, uint64_t n, uint64_t k,
     for (uint64_t c = 0; c < count; c++) {
         for (uint64_t r = 0; r < m; r++) acc[r] = 0.0f;
         for (uint64_t u = 0; u < runs; u++) {
-            const uint8_t *block = bytes + (first + c) * row_bytes + (u / 8) * bb;
-            or_decode_run(fmt, block, (int)(u % 8), q, scale, min);
+            const uint8_t *block = bytes + (first + c) * row_bytes + (u / rpb) * bb;
+            or_decode_run(fmt, block, (int)(u % rpb), q, scale, min);
             for (uint64_t r = 0; r < m; r++) {
                 uint64_t blk = r * runs + u;
                 if (int8) {

@@ -1,5 +1,6 @@
 /*
- * CPU oracle for the GGUF block-quantized matmul path (Q4_K, IQ4_XS).
+ * CPU oracle for the GGUF block-quantized matmul path (Q4_K, IQ4_XS,
+ * Q8_0, Q4_0, IQ4_NL, Q5_K, Q6_K).
  *
  * TEST INFRASTRUCTURE ONLY. This library is the checker: tests, the
  * smoke check and bench.py's CPU-baseline leg load it; the product
@@ -21,7 +22,12 @@ extern "C" {
 #endif
 
 /* ggml type ids (public GGUF spec) */
+#define OR_Q4_0 2
+#define OR_Q8_0 8
 #define OR_Q4_K 12
+#define OR_Q5_K 13
+#define OR_Q6_K 14
+#define OR_IQ4_NL 20
 #define OR_IQ4_XS 23
 
 /* Values per run (src/native/quant.rs:18-19). */
@@ -33,6 +39,7 @@ int or_block_elements(int fmt);
 void or_scale_min_k4(int j, const uint8_t *q, uint8_t *sc, uint8_t *m);
 void or_iq4_xs_scales(const uint8_t *six, int8_t out[8]);
 const int8_t *or_iq4nl_values(void);
+const int8_t *or_q4_0_values(void);
 
 /* Run `run` of one block: 32 signed values, per-half scale and min. */
 void or_decode_run(int fmt, const uint8_t *block, int run, int8_t q[OR_RUN],

@@ -3,9 +3,17 @@
 
 import numpy as np
 
+Q4_0 = 2
+Q8_0 = 8
 Q4_K = 12
+Q5_K = 13
+Q6_K = 14
+IQ4_NL = 20
 IQ4_XS = 23
-BLOCK_BYTES = {Q4_K: 144, IQ4_XS: 136}
+BLOCK_BYTES = {Q8_0: 34, Q4_0: 18, IQ4_NL: 18, Q4_K: 144, Q5_K: 176, Q6_K: 210, IQ4_XS: 136}
+BLOCK_ELEMENTS = {Q8_0: 32, Q4_0: 32, IQ4_NL: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, IQ4_XS: 256}
+# the formats of the generic (planes) GPU path
+PLANE_FORMATS = [Q8_0, Q4_0, IQ4_NL, Q5_K, Q6_K]
 
 
 class Rng:
@@ -25,15 +33,17 @@ class Rng:
 
 def half_offsets(fmt):
     """Byte offsets of each block's f16 scale fields (src/native/tests.rs:24-32)."""
-    return [0, 2] if fmt == Q4_K else [0]
+    if fmt in (Q4_K, Q5_K):
+        return [0, 2]
+    return [208] if fmt == Q6_K else [0]
 
 
 def packed(fmt, rows, cols, seed):
     """A random packed matrix: random bytes, small positive f16 scales with
     exponent 3..7 (src/native/tests.rs:45-67). uint8 [rows, row_bytes]."""
     rng = Rng((seed * 2654435761 + 1) & 0xFFFFFFFF)
-    bb = BLOCK_BYTES[fmt]
-    blocks = rows * cols // 256
+    bb, be = BLOCK_BYTES[fmt], BLOCK_ELEMENTS[fmt]
+    blocks = rows * cols // be
     out = np.empty(blocks * bb, np.uint8)
     for i in range(blocks):
         blk = [rng.next() % 256 for _ in range(bb)]
@@ -43,7 +53,7 @@ def packed(fmt, rows, cols, seed):
             blk[at] = bits & 0xFF
             blk[at + 1] = bits >> 8
         out[i * bb:(i + 1) * bb] = blk
-    return out.reshape(rows, cols // 256 * bb)
+    return out.reshape(rows, cols // be * bb)
 
 
 def activations(rows, cols, seed):
