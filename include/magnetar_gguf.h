@@ -27,13 +27,14 @@ float gg_f16_to_f32(uint16_t h);
  * f64, two values per pair of draws, rounded to f32. */
 void gg_gaussian_f32(uint64_t seed, float sigma, float *out, uint64_t n);
 
-/* Bytes of one stored row of `cols` weights (0: unsupported type, or cols
- * not a multiple of 256). */
+/* Bytes of one stored row of `cols` weights for Q4_0, Q8_0, IQ4_NL (32-value
+ * blocks), Q4_K, Q5_K, Q6_K, IQ4_XS (256-value blocks); 0 for another type
+ * or cols not whole blocks. */
 uint64_t gg_row_bytes(uint32_t gguf_type, uint64_t cols);
 
 /* Encodes rows x cols f32 weights (row-major) into gguf_type blocks, rows
- * stored one after another. Returns 0, or -1 for an unsupported type or
- * shape. */
+ * stored one after another (Q4_K and IQ4_XS only). Returns 0, or -1 for an
+ * unsupported type or shape. */
 int gg_quantize(uint32_t gguf_type, const float *w, uint64_t rows, uint64_t cols,
                 uint8_t *out);
 

@@ -24,8 +24,15 @@
 extern "C" {
 #endif
 
-/* ggml type ids (public GGUF specification). */
+/* ggml type ids (public GGUF specification) of the packed formats with a
+ * GPU path (the reference's PackedWeightFormat variants Q4_0, Q8_0, Q4K,
+ * Q5K, Q6K, Iq4Nl, Iq4Xs; src/native/quant.rs:71-86). */
+#define MQ_TYPE_Q4_0 2u
+#define MQ_TYPE_Q8_0 8u
 #define MQ_TYPE_Q4_K 12u
+#define MQ_TYPE_Q5_K 13u
+#define MQ_TYPE_Q6_K 14u
+#define MQ_TYPE_IQ4_NL 20u
 #define MQ_TYPE_IQ4_XS 23u
 
 /* Status codes. */
@@ -57,8 +64,11 @@ void mq_destroy(mq_ctx *ctx);
 const char *mq_last_error(mq_ctx *ctx);
 
 /* Uploads a packed weight: `stored_rows` rows of `stored_cols` values,
- * `len` = stored_rows * stored_cols / 256 * block_bytes checkpoint bytes.
- * Returns MQ_DECLINED for a type other than Q4_K / IQ4_XS or for
+ * `len` = stored_rows * stored_cols / block_values * block_bytes checkpoint
+ * bytes (Q8_0 32 / 34, Q4_0 and IQ4_NL 32 / 18, Q4_K 256 / 144, Q5_K
+ * 256 / 176, Q6_K 256 / 210, IQ4_XS 256 / 136); stored_cols must be whole
+ * blocks. Returns MQ_DECLINED for a type without a GPU path (Q2_K, Q3_K,
+ * the IQ2 / IQ3 grid formats) or for
  * transposed == 0 (stored rows are the input rows: the axpy layout), so
  * the caller keeps the f32 path. Replaces
  * `write_packed_weight_tensor` -> `PackedWeightWrite::{Stored,Declined}`

@@ -78,10 +78,18 @@ void gg_gaussian_f32(uint64_t seed, float sigma, float *out, uint64_t n) {
 /* ---- geometry ---------------------------------------------------------- */
 
 uint64_t gg_row_bytes(uint32_t gguf_type, uint64_t cols) {
-    if (cols % 256) return 0;
-    if (gguf_type == GG_TYPE_Q4_K) return cols / 256 * 144;
-    if (gguf_type == GG_TYPE_IQ4_XS) return cols / 256 * 136;
-    return 0;
+    uint64_t values = 256, bytes = 0;
+    switch (gguf_type) {
+    case 2: values = 32; bytes = 18; break;   /* Q4_0 */
+    case 8: values = 32; bytes = 34; break;   /* Q8_0 */
+    case 20: values = 32; bytes = 18; break;  /* IQ4_NL */
+    case GG_TYPE_Q4_K: bytes = 144; break;
+    case 13: bytes = 176; break;              /* Q5_K */
+    case 14: bytes = 210; break;              /* Q6_K */
+    case GG_TYPE_IQ4_XS: bytes = 136; break;
+    default: return 0;
+    }
+    return cols % values ? 0 : cols / values * bytes;
 }
 
 static int clampi(int v, int lo, int hi) { return v < lo ? lo : v > hi ? hi : v; }
@@ -197,7 +205,7 @@ static void encode_iq4xs_block(const float *w, uint8_t *blk) {
 int gg_quantize(uint32_t gguf_type, const float *w, uint64_t rows, uint64_t cols,
                 uint8_t *out) {
     uint64_t row_bytes = gg_row_bytes(gguf_type, cols);
-    if (!row_bytes) return -1;
+    if (!row_bytes || cols % 256 || (gguf_type != GG_TYPE_Q4_K && gguf_type != GG_TYPE_IQ4_XS)) return -1;
     for (uint64_t r = 0; r < rows; r++) {
         for (uint64_t b = 0; b < cols / 256; b++) {
             const float *src = w + r * cols + b * 256;

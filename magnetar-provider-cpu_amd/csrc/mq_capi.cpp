@@ -91,9 +91,11 @@ int hip_fail(mq_ctx* ctx, hipError_t e, const char* where) {
     if (e_ != hipSuccess) return hip_fail(ctx, e_, #call); \
   } while (0)
 
-uint64_t block_bytes(uint32_t type) {
-  return type == MQ_TYPE_Q4_K ? 144 : type == MQ_TYPE_IQ4_XS ? 136 : 0;
+bool known_type(uint32_t type) {
+  return type == MQ_TYPE_Q4_K || type == MQ_TYPE_IQ4_XS || mq::is_plane_format(static_cast<int>(type));
 }
+
+bool plane_type(uint32_t type) { return mq::is_plane_format(static_cast<int>(type)); }
 
 class DeviceGuard {
  public:
@@ -140,6 +142,13 @@ int acquire_workspace(mq_ctx* ctx, hipStream_t stream, size_t bytes) {
 int acquire_splitk(mq_ctx* ctx, hipStream_t stream, const Weight& w, uint64_t m, mq::GemvSplitK& sk) {
   sk = mq::GemvSplitK{};
   sk.ks = ctx->gemv_ksplit_override > 0 ? ctx->gemv_ksplit_override : mq::gemv_default_ksplit(w.rows, w.nb);
+  if (plane_type(w.type)) {
+    // the plane GEMV has no other form: its LDS staging must fit
+    const int need = mq::gemv_planes_min_ksplit(w.nb, m);
+    if (need > 16)
+      return fail(ctx, MQ_DECLINED, "packed rows of " + std::to_string(w.cols) + " values exceed the decode GEMV");
+    if (sk.ks < need) sk.ks = need;
+  }
   if (sk.ks > 16) sk.ks = 16;
   if (static_cast<uint64_t>(sk.ks) > w.nb) sk.ks = static_cast<int>(w.nb);
   if (sk.ks <= 1) {
@@ -193,6 +202,56 @@ int gemv_splits(mq_ctx* ctx, const Weight& w, uint64_t m, bool int8) {
 }
 
 constexpr uint64_t kGemvMaxRows = 8;
+// Up to this many activation rows, and for rows shorter than kGemmMinK
+// values, the matmul runs as decode-GEMV launches of 8 rows each: exact
+// integer dots, where the f16 MFMA GEMM rounds every operand to 11 bits
+// (a short row has too few terms for those roundings to average out
+// against the 1e-3 * ||row||_inf output tolerance).
+constexpr uint64_t kGemvChunkRows = 16;
+constexpr uint64_t kGemmMinK = 512;
+
+// The decode GEMV for m <= 8 rows. Caller holds ctx->mu and has validated
+// the arguments.
+int gemv_locked(mq_ctx* ctx, const Weight& w, const float* x, uint64_t m, uint64_t k, bool int8, float* y,
+                hipStream_t stream, const float* addend, uint64_t addend_stride) {
+  mq::GemvSplitK sk;
+  int rc = MQ_OK;
+  if (int8) {
+    rc = order_stream(ctx, stream);
+    if (!rc) rc = acquire_splitk(ctx, stream, w, m, sk);
+    if (rc) return rc;
+  }
+  if (plane_type(w.type)) {
+    if (int8)
+      mq::launch_gemv_planes_int8(static_cast<int>(w.type), w.dev, w.rows, w.nb, k, nullptr, nullptr, nullptr, x, m,
+                                  y, addend, addend_stride, ctx->gemv_splits_override, sk, stream);
+    else
+      mq::launch_gemv_planes_f32(static_cast<int>(w.type), w.dev, w.rows, w.nb, k, x, m, y, addend, addend_stride,
+                                 ctx->gemv_splits_override, stream);
+    return MQ_OK;
+  }
+  const bool fused = int8 && ctx->gemv_variant == 0 &&
+                     mq::launch_gemv_fused(static_cast<int>(w.type), w.dev, w.rows, w.nb, x, m, y, addend,
+                                           addend_stride, ctx->gemv_splits_override, sk, stream);
+  if (fused) {
+    // one launch: quantized into LDS and multiplied
+  } else if (int8) {
+    const size_t vb = align256(m * k), sb = align256(m * k / 32 * 4), hb = align256(m * k / 32 * 8);
+    rc = acquire_workspace(ctx, stream, vb + sb + hb);
+    if (rc) return rc;
+    auto* base = static_cast<uint8_t*>(ctx->ws);
+    auto* values = reinterpret_cast<int8_t*>(base);
+    auto* scales = reinterpret_cast<float*>(base + vb);
+    auto* sums = reinterpret_cast<int32_t*>(base + vb + sb);
+    mq::launch_quantize_activations(x, m, k, values, scales, sums, nullptr, 1, stream);
+    mq::launch_gemv_int8(static_cast<int>(w.type), w.dev, w.rows, w.nb, values, scales, sums, m, y, addend,
+                         addend_stride, ctx->gemv_splits_override, ctx->gemv_variant, sk, stream);
+  } else {
+    mq::launch_gemv_f32(static_cast<int>(w.type), w.dev, w.rows, w.nb, x, m, y, addend, addend_stride,
+                        gemv_splits(ctx, w, m, false), stream);
+  }
+  return MQ_OK;
+}
 
 // Enqueues y = x . W^T [+ addend] on `stream`. Caller holds ctx->mu.
 // addend_rows: 0 (no addend), 1 (one row broadcast) or m.
@@ -209,32 +268,12 @@ int matmul_locked(mq_ctx* ctx, const Weight& w, const float* x, uint64_t m, uint
   const uint64_t addend_stride = addend && addend_rows == m && m > 1 ? w.rows : 0;
   if (!addend) addend_rows = 0;
   const bool int8 = (flags & MQ_INT8_ACTIVATIONS) != 0;
-  if (m <= kGemvMaxRows) {
-    mq::GemvSplitK sk;
-    if (int8) {
-      rc = order_stream(ctx, stream);
-      if (!rc) rc = acquire_splitk(ctx, stream, w, m, sk);
+  if (m <= kGemvChunkRows || k < kGemmMinK) {
+    for (uint64_t r0 = 0; r0 < m; r0 += kGemvMaxRows) {
+      const uint64_t mc = m - r0 < kGemvMaxRows ? m - r0 : kGemvMaxRows;
+      const float* ad = addend ? addend + (addend_stride ? r0 * w.rows : 0) : nullptr;
+      rc = gemv_locked(ctx, w, x + r0 * k, mc, k, int8, y + r0 * w.rows, stream, ad, addend_stride);
       if (rc) return rc;
-    }
-    const bool fused = int8 && ctx->gemv_variant == 0 &&
-                       mq::launch_gemv_fused(static_cast<int>(w.type), w.dev, w.rows, w.nb, x, m, y, addend,
-                                             addend_stride, ctx->gemv_splits_override, sk, stream);
-    if (fused) {
-      // one launch: quantized into LDS and multiplied
-    } else if (int8) {
-      const size_t vb = align256(m * k), sb = align256(m * k / 32 * 4), hb = align256(m * k / 32 * 8);
-      rc = acquire_workspace(ctx, stream, vb + sb + hb);
-      if (rc) return rc;
-      auto* base = static_cast<uint8_t*>(ctx->ws);
-      auto* values = reinterpret_cast<int8_t*>(base);
-      auto* scales = reinterpret_cast<float*>(base + vb);
-      auto* sums = reinterpret_cast<int32_t*>(base + vb + sb);
-      mq::launch_quantize_activations(x, m, k, values, scales, sums, nullptr, 1, stream);
-      mq::launch_gemv_int8(static_cast<int>(w.type), w.dev, w.rows, w.nb, values, scales, sums, m, y, addend,
-                           addend_stride, ctx->gemv_splits_override, ctx->gemv_variant, sk, stream);
-    } else {
-      mq::launch_gemv_f32(static_cast<int>(w.type), w.dev, w.rows, w.nb, x, m, y, addend, addend_stride,
-                          gemv_splits(ctx, w, m, false), stream);
     }
   } else {
     rc = acquire_workspace(ctx, stream, align256(m * k * 2));
@@ -244,7 +283,7 @@ int matmul_locked(mq_ctx* ctx, const Weight& w, const float* x, uint64_t m, uint
       mq::launch_quantize_activations(x, m, k, nullptr, nullptr, nullptr, a16, 1, stream);
     else
       mq::launch_activations_f16(x, m, k, a16, stream);
-    mq::launch_gemm(static_cast<int>(w.type), w.dev, w.rows, w.nb, a16, m, y, addend, addend_stride,
+    mq::launch_gemm(static_cast<int>(w.type), w.dev, w.rows, w.nb, k, a16, m, y, addend, addend_stride,
                     ctx->gemm_variant, stream);
   }
   MQ_HIP(ctx, hipGetLastError());
@@ -309,17 +348,18 @@ int mq_weight_upload(mq_ctx* ctx, uint32_t gguf_type, uint64_t stored_rows, uint
                      const uint8_t* bytes, size_t len, uint64_t* handle) {
   if (!ctx || !handle) return fail(ctx, MQ_ERR_ARGUMENT, "mq_weight_upload: null argument");
   *handle = 0;
-  const uint64_t bb = block_bytes(gguf_type);
-  if (!bb)
+  if (!known_type(gguf_type))
     return fail(ctx, MQ_DECLINED, "packed weight format " + std::to_string(gguf_type) + " has no GPU path");
   if (!transposed)
     return fail(ctx, MQ_DECLINED, "packed weight stores input rows (untransposed): no GPU path");
-  if (stored_rows == 0 || stored_cols == 0 || stored_cols % 256 != 0)
+  const int type = static_cast<int>(gguf_type);
+  const uint64_t be = static_cast<uint64_t>(mq::block_values(type)), bb = static_cast<uint64_t>(mq::block_bytes_of(type));
+  if (stored_rows == 0 || stored_cols == 0 || stored_cols % be != 0)
     return fail(ctx, MQ_ERR_SHAPE,
                 "packed weight: stored shape [" + std::to_string(stored_rows) + ", " + std::to_string(stored_cols) +
-                    "] is not whole 256-value blocks");
-  const uint64_t nb = stored_cols / 256;
-  if (stored_rows > (1ull << 32) || nb > (1ull << 24) || len != stored_rows * nb * bb)
+                    "] is not whole " + std::to_string(be) + "-value blocks");
+  const uint64_t nb = (stored_cols + 255) / 256;
+  if (stored_rows > (1ull << 32) || nb > (1ull << 24) || len != stored_rows * (stored_cols / be) * bb)
     return fail(ctx, MQ_ERR_SHAPE,
                 "packed weight: " + std::to_string(len) + " bytes for " + std::to_string(stored_rows) + " x " +
                     std::to_string(stored_cols) + " values");
@@ -333,7 +373,7 @@ int mq_weight_upload(mq_ctx* ctx, uint32_t gguf_type, uint64_t stored_rows, uint
   w.nb = nb;
   w.rows_padded = (stored_rows + 7) / 8 * 8;
   w.transposed = transposed;
-  w.dev_bytes = w.rows_padded / 8 * nb * static_cast<uint64_t>(mq::tile_bytes(static_cast<int>(gguf_type)));
+  w.dev_bytes = w.rows_padded / 8 * nb * static_cast<uint64_t>(mq::tile_bytes(type));
   uint8_t* raw = nullptr;
   hipError_t e = hipMalloc(&raw, len);
   if (e != hipSuccess) return hip_fail(ctx, e, "hipMalloc(staging)");
@@ -344,7 +384,10 @@ int mq_weight_upload(mq_ctx* ctx, uint32_t gguf_type, uint64_t stored_rows, uint
   }
   if ((e = hipMemcpyAsync(raw, bytes, len, hipMemcpyHostToDevice, ctx->stream)) == hipSuccess &&
       (e = hipMemsetAsync(w.dev, 0, w.dev_bytes, ctx->stream)) == hipSuccess) {
-    mq::launch_repack(static_cast<int>(gguf_type), raw, stored_rows, nb, w.dev, ctx->stream);
+    if (plane_type(gguf_type))
+      mq::launch_repack_planes(type, raw, stored_rows, stored_cols, nb, w.dev, ctx->stream);
+    else
+      mq::launch_repack(type, raw, stored_rows, nb, w.dev, ctx->stream);
     e = hipGetLastError();
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
   }
@@ -498,8 +541,12 @@ int mq_matmul_prequantized_dev(mq_ctx* ctx, uint64_t handle, const int8_t* value
   rc = order_stream(ctx, s);
   if (!rc) rc = acquire_splitk(ctx, s, *w, m, sk);
   if (rc) return rc;
-  mq::launch_gemv_int8(static_cast<int>(w->type), w->dev, w->rows, w->nb, values_dev, scales_dev, sums_dev, m, y_dev,
-                       nullptr, 0, ctx->gemv_splits_override, ctx->gemv_variant, sk, s);
+  if (plane_type(w->type))
+    mq::launch_gemv_planes_int8(static_cast<int>(w->type), w->dev, w->rows, w->nb, k, values_dev, scales_dev,
+                                sums_dev, nullptr, m, y_dev, nullptr, 0, ctx->gemv_splits_override, sk, s);
+  else
+    mq::launch_gemv_int8(static_cast<int>(w->type), w->dev, w->rows, w->nb, values_dev, scales_dev, sums_dev, m,
+                         y_dev, nullptr, 0, ctx->gemv_splits_override, ctx->gemv_variant, sk, s);
   MQ_HIP(ctx, hipGetLastError());
   return MQ_OK;
 }
@@ -533,7 +580,7 @@ int mq_matmul_f16_dev(mq_ctx* ctx, uint64_t handle, const uint16_t* a16_dev, uin
   if (!a16_dev || !y_dev) return fail(ctx, MQ_ERR_ARGUMENT, "mq_matmul_f16_dev: null pointer");
   DeviceGuard guard(ctx->device);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  mq::launch_gemm(static_cast<int>(w->type), w->dev, w->rows, w->nb, a16_dev, m, y_dev, nullptr, 0,
+  mq::launch_gemm(static_cast<int>(w->type), w->dev, w->rows, w->nb, w->cols, a16_dev, m, y_dev, nullptr, 0,
                   ctx->gemm_variant, s);
   MQ_HIP(ctx, hipGetLastError());
   return MQ_OK;
@@ -547,7 +594,10 @@ int mq_dequantize_dev(mq_ctx* ctx, uint64_t handle, int logical, float* out_dev,
   if (!out_dev) return fail(ctx, MQ_ERR_ARGUMENT, "mq_dequantize_dev: null output");
   DeviceGuard guard(ctx->device);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  mq::launch_dequantize(static_cast<int>(w->type), w->dev, w->rows, w->nb, logical, out_dev, s);
+  if (plane_type(w->type))
+    mq::launch_dequantize_planes(static_cast<int>(w->type), w->dev, w->rows, w->cols, w->nb, logical, out_dev, s);
+  else
+    mq::launch_dequantize(static_cast<int>(w->type), w->dev, w->rows, w->nb, logical, out_dev, s);
   MQ_HIP(ctx, hipGetLastError());
   return MQ_OK;
 }
@@ -562,7 +612,11 @@ int mq_dequantize(mq_ctx* ctx, uint64_t handle, int logical, float* out) {
   const size_t bytes = w->rows * w->cols * sizeof(float);
   float* dev = nullptr;
   MQ_HIP(ctx, hipMalloc(&dev, bytes));
-  mq::launch_dequantize(static_cast<int>(w->type), w->dev, w->rows, w->nb, logical, dev, ctx->stream);
+  if (plane_type(w->type))
+    mq::launch_dequantize_planes(static_cast<int>(w->type), w->dev, w->rows, w->cols, w->nb, logical, dev,
+                                 ctx->stream);
+  else
+    mq::launch_dequantize(static_cast<int>(w->type), w->dev, w->rows, w->nb, logical, dev, ctx->stream);
   hipError_t e = hipGetLastError();
   if (e == hipSuccess) e = hipMemcpyAsync(out, dev, bytes, hipMemcpyDeviceToHost, ctx->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);

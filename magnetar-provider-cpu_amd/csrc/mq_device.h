@@ -13,7 +13,23 @@
 //     scales_l[4]), then 8 planes x 8 rows x 16 B, plane p holding block
 //     bytes 8+16p .. 23+16p (run p's 32 indices).
 //
-//   tile(g, b) starts at (g * nb + b) * tile_bytes, nb = K / 256.
+//   Plane formats (Q8_0, Q4_0, IQ4_NL, Q5_K, Q6_K): a "group" is 256
+//     values of a row (a K-quant super-block, or eight 32-value blocks);
+//     the tile is kPlanes planes x 8 rows x 16 B, plane p of row r at
+//     128 p + 16 r, plus for Q6_K one shared 16-byte plane holding the 8
+//     rows' f16 d (row r at byte 2 r):
+//       Q8_0   17 planes: 0 = the 8 blocks' f16 d; 1 + 2i + h = block i's
+//              quants 16h .. 16h + 15.
+//       Q4_0, IQ4_NL  9 planes: 0 = the 8 blocks' f16 d; 1 + i = block i's
+//              16 nibble-pair bytes.
+//       Q5_K   11 planes: the super-block's bytes 16p .. 16p + 15 (0: d,
+//              dmin, scales; 1-2: high bits; 3-10: nibbles).
+//       Q6_K   13 planes: bytes 16p .. 16p + 15 (0-7: low nibbles, 8-11:
+//              high bits, 12: the 16 i8 scales), then the shared d plane.
+//     A row whose K is not a multiple of 256 (32-value formats) ends in a
+//     group padded with zero blocks (d = 0).
+//
+//   tile(g, b) starts at (g * nb + b) * tile_bytes, nb = ceil(K / 256).
 //
 // So a 64-lane load of one plane by 8 rows x 8 blocks touches eight whole
 // 128-byte lines, and a GEMM K-step reads whole lines per 8 rows.
@@ -33,8 +49,41 @@ constexpr int kIq4xsBlockBytes = 136;
 constexpr int kQ4kTileBytes = 1152;
 constexpr int kIq4xsTileBytes = 1088;
 
-__host__ __device__ inline int tile_bytes(int type) {
-  return type == kTypeQ4K ? kQ4kTileBytes : kIq4xsTileBytes;
+constexpr int kTypeQ4_0 = 2;
+constexpr int kTypeQ8_0 = 8;
+constexpr int kTypeQ5K = 13;
+constexpr int kTypeQ6K = 14;
+constexpr int kTypeIq4Nl = 20;
+
+__host__ __device__ constexpr bool is_plane_format(int type) {
+  return type == kTypeQ8_0 || type == kTypeQ4_0 || type == kTypeIq4Nl || type == kTypeQ5K || type == kTypeQ6K;
+}
+
+// Per-row 16-byte planes of a plane format's tile (shared d plane apart).
+__host__ __device__ constexpr int plane_count(int type) {
+  return type == kTypeQ8_0 ? 17 : (type == kTypeQ4_0 || type == kTypeIq4Nl) ? 9 : type == kTypeQ5K ? 11 : 13;
+}
+
+__host__ __device__ constexpr bool plane_shared_d(int type) { return type == kTypeQ6K; }
+
+// Checkpoint block geometry: values and bytes per block.
+__host__ __device__ constexpr int block_values(int type) {
+  return (type == kTypeQ8_0 || type == kTypeQ4_0 || type == kTypeIq4Nl) ? 32 : 256;
+}
+
+__host__ __device__ constexpr int block_bytes_of(int type) {
+  return type == kTypeQ8_0 ? 34
+         : (type == kTypeQ4_0 || type == kTypeIq4Nl) ? 18
+         : type == kTypeQ4K ? kQ4kBlockBytes
+         : type == kTypeQ5K ? 176
+         : type == kTypeQ6K ? 210
+         : kIq4xsBlockBytes;
+}
+
+__host__ __device__ constexpr int tile_bytes(int type) {
+  return type == kTypeQ4K     ? kQ4kTileBytes
+         : type == kTypeIq4Xs ? kIq4xsTileBytes
+                              : 128 * plane_count(type) + (plane_shared_d(type) ? 16 : 0);
 }
 
 // The GGUF kvalues_iq4nl codebook packed 4 bytes per word (little end
@@ -115,6 +164,10 @@ __device__ inline uint4 buffer_ld16(__amdgpu_buffer_rsrc_t r, uint32_t offset) {
   typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
   const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(offset), 0, 0);
   return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ inline uint32_t buffer_ld4(__amdgpu_buffer_rsrc_t r, uint32_t offset) {
+  return static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(offset), 0, 0));
 }
 
 __device__ inline uint2 buffer_ld8(__amdgpu_buffer_rsrc_t r, uint32_t offset) {

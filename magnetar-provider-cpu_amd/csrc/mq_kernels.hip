@@ -695,30 +695,39 @@ __device__ inline void finish_rows(float (&acc)[M], float (&mins)[M], uint64_t r
 // Fused form: quantize the f32 activations straight into LDS with the same
 // per-block arithmetic as quantize_act_kernel (bit-identical values, scales
 // and sums). Every thread runs the same iterations so the 8-lane groups of
-// quantize4 shuffle together.
+// quantize4 shuffle together. Only the first kv values of each row's range
+// exist (kv < kn for a plane format whose K ends inside a group); the rest
+// are staged as zeros with d = 0.
 template <int TYPE, int M>
 struct FusedStage {
   static constexpr int kPre = 4;
   float4 v[kPre];
 
-  __device__ void load(const float* __restrict__ xf, uint64_t K, uint64_t k0, int kn) {
+  __device__ void load(const float* __restrict__ xf, uint64_t K, uint64_t k0, int kn, int kv) {
     const int n4 = M * kn / 4, per_row4 = kn / 4;
 #pragma unroll
     for (int j = 0; j < kPre; ++j) {
       const int i = j * static_cast<int>(blockDim.x) + static_cast<int>(threadIdx.x);
       v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (i < n4) {
-        const int m = M == 1 ? 0 : i / per_row4, c4 = i - m * per_row4;
-        v[j] = *reinterpret_cast<const float4*>(xf + m * K + k0 + 4 * c4);
-      }
+      const int m = M == 1 ? 0 : i / per_row4, c4 = i - m * per_row4;
+      if (i < n4 && 4 * c4 < kv) v[j] = *reinterpret_cast<const float4*>(xf + m * K + k0 + 4 * c4);
     }
   }
 
   __device__ static void put(const Quant4& q, int i, uint8_t* lds, int M_kn) {
     float* rs = reinterpret_cast<float*>(lds + M_kn);
     reinterpret_cast<uint32_t*>(lds)[i] = pack_q4(q);
-    if ((i & 7) == 0) {
-      const int run = i >> 3;  // m * (kn / 32) + run within the range
+    const int run = i >> 3;  // m * (kn / 32) + run within the range
+    if (is_plane_format(TYPE)) {
+      // record (d, half sum 0, half sum 1, 0) per run
+      uint32_t* rec = reinterpret_cast<uint32_t*>(rs) + 4 * run;
+      if ((i & 7) == 0) {
+        rec[0] = __float_as_uint(q.d);
+        rec[1] = static_cast<uint32_t>(q.half_sum);
+      } else if ((i & 7) == 4) {
+        rec[2] = static_cast<uint32_t>(q.half_sum);
+      }
+    } else if ((i & 7) == 0) {
       if (TYPE == kTypeQ4K) {
         rs[2 * run] = q.d;
         rs[2 * run + 1] = q.d * static_cast<float>(q.run_sum);
@@ -728,7 +737,7 @@ struct FusedStage {
     }
   }
 
-  __device__ void store(const float* __restrict__ xf, uint64_t K, uint64_t k0, int kn, uint8_t* lds) const {
+  __device__ void store(const float* __restrict__ xf, uint64_t K, uint64_t k0, int kn, int kv, uint8_t* lds) const {
     const int n4 = M * kn / 4, per_row4 = kn / 4;
 #pragma unroll
     for (int j = 0; j < kPre; ++j) {
@@ -740,7 +749,8 @@ struct FusedStage {
       const int i = i0 + static_cast<int>(threadIdx.x);
       const bool act = i < n4;
       const int m = act ? i / per_row4 : 0, c4 = act ? i - m * per_row4 : 0;
-      const float4 x = act ? *reinterpret_cast<const float4*>(xf + m * K + k0 + 4 * c4) : make_float4(0.f, 0.f, 0.f, 0.f);
+      const float4 x = act && 4 * c4 < kv ? *reinterpret_cast<const float4*>(xf + m * K + k0 + 4 * c4)
+                                          : make_float4(0.f, 0.f, 0.f, 0.f);
       const Quant4 q = quantize4(x);
       if (act) put(q, i, lds, M * kn);
     }
@@ -748,16 +758,16 @@ struct FusedStage {
 };
 
 // Pre-quantized activations: copy values and per-run scales (and Q4_K's
-// d * (s0 + s1)) into LDS.
+// d * (s0 + s1), or a plane format's half sums) into LDS.
 template <int TYPE, int M>
 struct QuantizedStage {
   static constexpr int kPre = 2;
   uint4 v[kPre];
   float d;
-  int hs;
+  int hs, hs1;
 
   __device__ void load(const int8_t* __restrict__ xv, const float* __restrict__ xs, const int32_t* __restrict__ xsum,
-                       uint64_t K, uint64_t k0, int kn) {
+                       uint64_t K, uint64_t k0, int kn, int kv) {
     const int per_row16 = kn / 16, kruns = kn / 32;
     const int runs = static_cast<int>(K / 32), r0 = static_cast<int>(k0 / 32);
     const int t = static_cast<int>(threadIdx.x);
@@ -765,26 +775,28 @@ struct QuantizedStage {
     for (int j = 0; j < kPre; ++j) {
       const int i = j * static_cast<int>(blockDim.x) + t;
       v[j] = make_uint4(0, 0, 0, 0);
-      if (i < M * per_row16) {
-        const int m = M == 1 ? 0 : i / per_row16, c = i - m * per_row16;
-        v[j] = *reinterpret_cast<const uint4*>(xv + m * K + k0 + 16 * c);
-      }
+      const int m = M == 1 ? 0 : i / per_row16, c = i - m * per_row16;
+      if (i < M * per_row16 && 16 * c < kv) v[j] = *reinterpret_cast<const uint4*>(xv + m * K + k0 + 16 * c);
     }
     d = 0.0f;
-    hs = 0;
-    if (t < M * kruns) {
-      const int m = M == 1 ? 0 : t / kruns, u = t - m * kruns;
+    hs = hs1 = 0;
+    const int m = M == 1 ? 0 : t / kruns, u = t - m * kruns;
+    if (t < M * kruns && 32 * u < kv) {
       const int src = m * runs + r0 + u;
       d = xs[src];
-      if (TYPE == kTypeQ4K) {
+      if (TYPE == kTypeQ4K || is_plane_format(TYPE)) {
         const int2 sm = reinterpret_cast<const int2*>(xsum)[src];
-        hs = sm.x + sm.y;
+        hs = TYPE == kTypeQ4K ? sm.x + sm.y : sm.x;
+        hs1 = sm.y;
       }
     }
   }
 
-  __device__ static void put_run(float* rs, int i, float d, int hs) {
-    if (TYPE == kTypeQ4K) {
+  __device__ static void put_run(float* rs, int i, float d, int hs, int hs1) {
+    if (is_plane_format(TYPE)) {
+      reinterpret_cast<uint4*>(rs)[i] =
+          make_uint4(__float_as_uint(d), static_cast<uint32_t>(hs), static_cast<uint32_t>(hs1), 0u);
+    } else if (TYPE == kTypeQ4K) {
       rs[2 * i] = d;
       rs[2 * i + 1] = d * static_cast<float>(hs);
     } else {
@@ -793,7 +805,7 @@ struct QuantizedStage {
   }
 
   __device__ void store(const int8_t* __restrict__ xv, const float* __restrict__ xs, const int32_t* __restrict__ xsum,
-                        uint64_t K, uint64_t k0, int kn, uint8_t* lds) const {
+                        uint64_t K, uint64_t k0, int kn, int kv, uint8_t* lds) const {
     const int per_row16 = kn / 16, kruns = kn / 32;
     const int runs = static_cast<int>(K / 32), r0 = static_cast<int>(k0 / 32);
     const int t = static_cast<int>(threadIdx.x);
@@ -804,19 +816,25 @@ struct QuantizedStage {
     }
     for (int i = kPre * static_cast<int>(blockDim.x) + t; i < M * per_row16; i += blockDim.x) {
       const int m = i / per_row16, c = i - m * per_row16;
-      reinterpret_cast<uint4*>(lds)[i] = *reinterpret_cast<const uint4*>(xv + m * K + k0 + 16 * c);
+      reinterpret_cast<uint4*>(lds)[i] =
+          16 * c < kv ? *reinterpret_cast<const uint4*>(xv + m * K + k0 + 16 * c) : make_uint4(0, 0, 0, 0);
     }
     float* rs = reinterpret_cast<float*>(lds + M * kn);
-    if (t < M * kruns) put_run(rs, t, d, hs);
+    if (t < M * kruns) put_run(rs, t, d, hs, hs1);
     for (int i = static_cast<int>(blockDim.x) + t; i < M * kruns; i += blockDim.x) {
       const int m = i / kruns, u = i - m * kruns;
       const int src = m * runs + r0 + u;
-      int h = 0;
-      if (TYPE == kTypeQ4K) {
-        const int2 sm = reinterpret_cast<const int2*>(xsum)[src];
-        h = sm.x + sm.y;
+      float dd = 0.0f;
+      int h = 0, h1 = 0;
+      if (32 * u < kv) {
+        dd = xs[src];
+        if (TYPE == kTypeQ4K || is_plane_format(TYPE)) {
+          const int2 sm = reinterpret_cast<const int2*>(xsum)[src];
+          h = TYPE == kTypeQ4K ? sm.x + sm.y : sm.x;
+          h1 = sm.y;
+        }
       }
-      put_run(rs, i, xs[src], h);
+      put_run(rs, i, dd, h, h1);
     }
   }
 };
@@ -1127,18 +1145,18 @@ __global__ __launch_bounds__(512) void gemv_lds_int8_kernel(
   FusedStage<TYPE, M> fs;
   QuantizedStage<TYPE, M> qs;
   if (FUSED)
-    fs.load(xf, K, k0, kn);
+    fs.load(xf, K, k0, kn, kn);
   else
-    qs.load(xv, xs, xsum, K, k0, kn);
+    qs.load(xv, xs, xsum, K, k0, kn, kn);
   // 2. the wave's first weight block
   RawRowBlock A;
   const int bA = b0 + s;
   load_row_block<TYPE>(A, rsrc, block_off(bA), r);
   // 3. activations into LDS
   if (FUSED)
-    fs.store(xf, K, k0, kn, lds);
+    fs.store(xf, K, k0, kn, kn, lds);
   else
-    qs.store(xv, xs, xsum, K, k0, kn, lds);
+    qs.store(xv, xs, xsum, K, k0, kn, kn, lds);
   __syncthreads();
 
   float acc[M], mins[M];
@@ -1155,6 +1173,392 @@ __global__ __launch_bounds__(512) void gemv_lds_int8_kernel(
   }
   finish_rows<M>(acc, mins, rows, y, addend, addend_stride, reinterpret_cast<float*>(lds), sk.partials,
                  sk.counters, sk.ks);
+}
+
+// ---------------------------------------------------------------------------
+// Plane formats (Q8_0, Q4_0, IQ4_NL, Q5_K, Q6_K; layout in mq_device.h).
+// One group (256 values) of one row is kPlanes 16-byte planes; run j of the
+// group decodes to 32 values q (as 8 words of 4 bytes), a scale and a min
+// per 16-value half, as the reference's `decode` (src/native/quant.rs:
+// 102-149, 180-195) produces them.
+// ---------------------------------------------------------------------------
+
+__device__ inline uint32_t word_of(const uint4& v, int t) { return t == 0 ? v.x : t == 1 ? v.y : t == 2 ? v.z : v.w; }
+
+// Signed bytes from nibbles 0..15 standing for nibble - 8 (Q4_0).
+__device__ inline uint32_t nibbles_minus_8(uint32_t nib) {
+  const uint32_t x = nib ^ 0x08080808u;
+  return x | ((x & 0x08080808u) * 0x1Eu);  // bytes 0..7 stay, 8..15 gain 0xF0
+}
+
+// Signed bytes from 6-bit values 0..63 standing for value - 32 (Q6_K).
+__device__ inline uint32_t six_bits_minus_32(uint32_t t) {
+  const uint32_t x = t ^ 0x20202020u;
+  return x | ((x & 0x20202020u) * 6u);  // bytes 0..31 stay, 32..63 gain 0xC0
+}
+
+// Run j's values as stored for the integer dots: Q5_K and Q6_K unsigned
+// (0..31, 0..63; the offsets go through the activation sums), the others
+// signed. `P(p)` returns plane p of this row.
+template <int TYPE, class Planes>
+__device__ inline void plane_run_bytes(const Planes& P, int j, uint32_t (&lo)[4], uint32_t (&hi)[4]) {
+  if constexpr (TYPE == kTypeQ8_0) {
+    const uint4 a = P(1 + 2 * j), b = P(2 + 2 * j);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      lo[t] = word_of(a, t);
+      hi[t] = word_of(b, t);
+    }
+  } else if constexpr (TYPE == kTypeQ4_0 || TYPE == kTypeIq4Nl) {
+    const uint4 a = P(1 + j);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const uint32_t w = word_of(a, t);
+      lo[t] = w & 0x0F0F0F0Fu;
+      hi[t] = (w >> 4) & 0x0F0F0F0Fu;
+      if constexpr (TYPE == kTypeIq4Nl) {
+        lo[t] = iq4_lookup4(lo[t]);
+        hi[t] = iq4_lookup4(hi[t]);
+      }
+    }
+  } else if constexpr (TYPE == kTypeQ5K) {
+    const int c = j >> 1, sh = 4 * (j & 1);
+    const uint4 l0 = P(3 + 2 * c), l1 = P(4 + 2 * c), h0 = P(1), h1 = P(2);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      lo[t] = ((word_of(l0, t) >> sh) & 0x0F0F0F0Fu) | (((word_of(h0, t) >> j) & 0x01010101u) << 4);
+      hi[t] = ((word_of(l1, t) >> sh) & 0x0F0F0F0Fu) | (((word_of(h1, t) >> j) & 0x01010101u) << 4);
+    }
+  } else {  // Q6_K
+    const int h = j >> 2, g = j & 3;
+    const int lp = 4 * h + 2 * (g & 1), hp = 8 + 2 * h, ls = 4 * (g >> 1), hs = 2 * g;
+    const uint4 l0 = P(lp), l1 = P(lp + 1), h0 = P(hp), h1 = P(hp + 1);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      lo[t] = ((word_of(l0, t) >> ls) & 0x0F0F0F0Fu) | (((word_of(h0, t) >> hs) & 0x03030303u) << 4);
+      hi[t] = ((word_of(l1, t) >> ls) & 0x0F0F0F0Fu) | (((word_of(h1, t) >> hs) & 0x03030303u) << 4);
+    }
+  }
+}
+
+// The f16 d of 32-value block j from plane 0 (Q8_0, Q4_0, IQ4_NL).
+template <class Planes>
+__device__ inline float block_d(const Planes& P, int j) {
+  return half_bits(word_of(P(0), j >> 1) >> (16 * (j & 1)));
+}
+
+// Q6_K run j's i8 scale of half p.
+template <class Planes>
+__device__ inline int q6k_scale(const Planes& P, int j, int p) {
+  const int i = 8 * (j >> 2) + 2 * (j & 3) + p;
+  return static_cast<int8_t>(byte_of(word_of(P(12), i >> 2), i & 3));
+}
+
+// Run j as the reference decodes it: signed values and, per half, the f32
+// scale and min (scale = d * sub-scale, min = dmin * sub-min).
+template <int TYPE, class Planes>
+__device__ inline void plane_run_signed(const Planes& P, uint32_t d_bits, int j, uint32_t (&q)[8], float (&scale)[2],
+                                        float (&mn)[2]) {
+  uint32_t lo[4], hi[4];
+  plane_run_bytes<TYPE>(P, j, lo, hi);
+  mn[0] = mn[1] = 0.0f;
+  if constexpr (TYPE == kTypeQ4_0) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      lo[t] = nibbles_minus_8(lo[t]);
+      hi[t] = nibbles_minus_8(hi[t]);
+    }
+  } else if constexpr (TYPE == kTypeQ6K) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      lo[t] = six_bits_minus_32(lo[t]);
+      hi[t] = six_bits_minus_32(hi[t]);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    q[t] = lo[t];
+    q[4 + t] = hi[t];
+  }
+  if constexpr (TYPE == kTypeQ5K) {
+    const uint4 hdr = P(0);
+    uint32_t sc, m;
+    q4k_sc_m(q4k_six_bit(hdr), j, sc, m);
+    scale[0] = scale[1] = half_bits(hdr.x) * static_cast<float>(sc);
+    mn[0] = mn[1] = half_bits(hdr.x >> 16) * static_cast<float>(m);
+  } else if constexpr (TYPE == kTypeQ6K) {
+    const float d = half_bits(d_bits);
+    scale[0] = d * static_cast<float>(q6k_scale(P, j, 0));
+    scale[1] = d * static_cast<float>(q6k_scale(P, j, 1));
+  } else {
+    scale[0] = scale[1] = block_d(P, j);
+  }
+}
+
+// Repack: thread per (row, group, plane); plane_count(TYPE) is the shared d
+// plane of Q6_K (2 bytes per row). Blocks past the row's K stay zero.
+template <int TYPE>
+__global__ void repack_planes_kernel(const uint8_t* __restrict__ raw, uint64_t rows, uint64_t K, uint64_t nb,
+                                     uint8_t* __restrict__ tiled) {
+  constexpr int P = plane_count(TYPE), BE = block_values(TYPE), BB = block_bytes_of(TYPE);
+  constexpr int PT = P + (plane_shared_d(TYPE) ? 1 : 0);
+  const uint64_t t = blockIdx.x * static_cast<uint64_t>(blockDim.x) + threadIdx.x;
+  if (t >= rows * nb * PT) return;
+  const int p = static_cast<int>(t % PT);
+  const uint64_t rb = t / PT, b = rb % nb, n = rb / nb;
+  const uint64_t blocks = K / BE, row_bytes = blocks * BB;
+  const uint8_t* row = raw + n * row_bytes;
+  uint8_t* tile = tiled + ((n >> 3) * nb + b) * tile_bytes(TYPE);
+  if (p == P) {  // Q6_K's d: bytes 208..209
+    tile[128 * P + 2 * (n & 7)] = row[b * BB + 208];
+    tile[128 * P + 2 * (n & 7) + 1] = row[b * BB + 209];
+    return;
+  }
+  uint8_t* dst = tile + 128 * p + 16 * (n & 7);
+  for (int i = 0; i < 16; ++i) {
+    uint64_t blk = b, off = 16 * p + i;
+    if (BE == 32) {
+      if (p == 0) {
+        blk = 8 * b + i / 2;
+        off = i % 2;
+      } else if (TYPE == kTypeQ8_0) {
+        blk = 8 * b + (p - 1) / 2;
+        off = 2 + 16 * ((p - 1) % 2) + i;
+      } else {
+        blk = 8 * b + (p - 1);
+        off = 2 + i;
+      }
+    }
+    dst[i] = blk < blocks ? row[blk * BB + off] : 0;
+  }
+}
+
+// Thread per (row, run): value = scale * q - min, product and difference
+// each rounded once (quant.rs:1702-1711).
+template <int TYPE>
+__global__ void dequantize_planes_kernel(const uint8_t* __restrict__ tiled, uint64_t rows, uint64_t K, uint64_t nb,
+                                         int logical, float* __restrict__ out) {
+  constexpr int P = plane_count(TYPE);
+  const uint64_t runs = K / 32;
+  const uint64_t t = blockIdx.x * static_cast<uint64_t>(blockDim.x) + threadIdx.x;
+  if (t >= rows * runs) return;
+  const uint64_t u = t % runs, n = t / runs, b = u / 8;
+  const int j = static_cast<int>(u % 8), r = static_cast<int>(n & 7);
+  const uint8_t* tile = tiled + ((n >> 3) * nb + b) * tile_bytes(TYPE);
+  auto planes = [&](int p) { return ld16(tile + 128 * p + 16 * r); };
+  const uint32_t d_bits =
+      plane_shared_d(TYPE) ? static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(tile + 128 * P + 2 * r)) : 0u;
+  uint32_t q[8];
+  float scale[2], mn[2];
+  plane_run_signed<TYPE>(planes, d_bits, j, q, scale, mn);
+  float v[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    const float p = scale[i >> 4] * static_cast<float>(static_cast<int8_t>(byte_of(q[i >> 2], i & 3)));
+    v[i] = p - mn[i >> 4];
+  }
+  store_run(out, rows, K, n, 32 * u, logical, v);
+}
+
+template <int TYPE>
+struct PlaneBlock {
+  uint4 p[plane_count(TYPE)];
+  uint32_t d_bits;  // Q6_K: this row's f16 d
+};
+
+template <int TYPE>
+__device__ inline void load_planes(PlaneBlock<TYPE>& a, __amdgpu_buffer_rsrc_t rsrc, uint32_t offset, int r) {
+  constexpr int P = plane_count(TYPE);
+  const bool none = offset == kBufferNone;
+#pragma unroll
+  for (int p = 0; p < P; ++p) a.p[p] = buffer_ld16(rsrc, none ? kBufferNone : offset + 128 * p + 16 * r);
+  a.d_bits = 0;
+  if constexpr (plane_shared_d(TYPE)) {
+    const uint32_t w = buffer_ld4(rsrc, none ? kBufferNone : offset + 128 * P + 4 * (r >> 1));
+    a.d_bits = (r & 1) ? (w >> 16) : (w & 0xFFFFu);
+  }
+}
+
+// One run of the int8 GEMV: integer half dots, the format's integer scale
+// and offset terms exact, then d_act (and the block's d per run for the
+// 32-value formats) in f32.
+template <int TYPE, int M>
+__device__ inline void plane_run_int8(const PlaneBlock<TYPE>& a, int j, const uint8_t* lds, int kn, int kruns, int bl,
+                                      float (&accb)[M], float (&minb)[M]) {
+  auto planes = [&](int p) { return a.p[p]; };
+  uint32_t lo[4], hi[4];
+  plane_run_bytes<TYPE>(planes, j, lo, hi);
+  float dj = 0.0f;
+  int sc0 = 0, sc1 = 0, smin = 0;
+  if constexpr (TYPE == kTypeQ5K) {
+    uint32_t sc, m;
+    q4k_sc_m(q4k_six_bit(a.p[0]), j, sc, m);
+    sc0 = static_cast<int>(sc);
+    smin = static_cast<int>(m);
+  } else if constexpr (TYPE == kTypeQ6K) {
+    sc0 = q6k_scale(planes, j, 0);
+    sc1 = q6k_scale(planes, j, 1);
+  } else {
+    dj = block_d(planes, j);
+  }
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    const uint4* xa = reinterpret_cast<const uint4*>(opaque(lds, m * kn + bl * 256 + 32 * j));
+    const uint4 x0 = xa[0], x1 = xa[1];
+    int d0 = sdot4(lo[0], x0.x, 0);
+    d0 = sdot4(lo[1], x0.y, d0);
+    d0 = sdot4(lo[2], x0.z, d0);
+    d0 = sdot4(lo[3], x0.w, d0);
+    int d1 = sdot4(hi[0], x1.x, 0);
+    d1 = sdot4(hi[1], x1.y, d1);
+    d1 = sdot4(hi[2], x1.z, d1);
+    d1 = sdot4(hi[3], x1.w, d1);
+    const uint4 rec = *reinterpret_cast<const uint4*>(opaque(lds, M * kn + 16 * (m * kruns + bl * 8 + j)));
+    const float dx = __uint_as_float(rec.x);
+    const int s0 = static_cast<int>(rec.y), s1 = static_cast<int>(rec.z);
+    if constexpr (TYPE == kTypeQ5K) {
+      accb[m] = fmaf(static_cast<float>(sc0 * (d0 + d1)), dx, accb[m]);
+      minb[m] = fmaf(static_cast<float>(smin * (s0 + s1)), dx, minb[m]);
+    } else if constexpr (TYPE == kTypeQ6K) {
+      accb[m] = fmaf(static_cast<float>(sc0 * (d0 - 32 * s0) + sc1 * (d1 - 32 * s1)), dx, accb[m]);
+    } else if constexpr (TYPE == kTypeQ4_0) {
+      accb[m] = fmaf(dj * dx, static_cast<float>(d0 + d1 - 8 * (s0 + s1)), accb[m]);
+    } else {
+      accb[m] = fmaf(dj * dx, static_cast<float>(d0 + d1), accb[m]);
+    }
+  }
+}
+
+template <int TYPE, int M>
+__device__ inline void plane_block_int8(const PlaneBlock<TYPE>& a, const uint8_t* lds, int kn, int kruns, int bl,
+                                        float (&acc)[M], float (&mins)[M]) {
+  float accb[M], minb[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) accb[m] = minb[m] = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) plane_run_int8<TYPE, M>(a, j, lds, kn, kruns, bl, accb, minb);
+  if constexpr (TYPE == kTypeQ5K) {
+    const float d = half_bits(a.p[0].x), dmin = half_bits(a.p[0].x >> 16);
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      acc[m] = fmaf(d, accb[m], acc[m]);
+      mins[m] = fmaf(dmin, minb[m], mins[m]);
+    }
+  } else if constexpr (TYPE == kTypeQ6K) {
+    const float d = half_bits(a.d_bits);
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[m] = fmaf(d, accb[m], acc[m]);
+  } else {
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[m] += accb[m];
+  }
+}
+
+// Decode GEMV over plane tiles, int8 activations staged in LDS (fused
+// quantization or pre-quantized), row per lane; the same grid, K-split,
+// load order and epilogue as gemv_lds_int8_kernel. K is the logical row
+// length (the last group may be partly padding).
+template <int TYPE, int M, bool FUSED>
+__global__ __launch_bounds__(512) void gemv_planes_int8_kernel(
+    const uint8_t* __restrict__ w, int nb, uint64_t rows, uint64_t K, const int8_t* __restrict__ xv,
+    const float* __restrict__ xs, const int32_t* __restrict__ xsum, const float* __restrict__ xf,
+    float* __restrict__ y, const float* __restrict__ addend, uint64_t addend_stride, SplitK sk) {
+  constexpr int kTile = tile_bytes(TYPE);
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int lane = threadIdx.x & 63;
+  const int s = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int S = blockDim.x >> 6;
+  const int b0 = static_cast<int>(blockIdx.y * nb / sk.ks), b1 = static_cast<int>((blockIdx.y + 1) * nb / sk.ks);
+  const int r = lane & 7;
+  const uint64_t k0 = static_cast<uint64_t>(b0) * 256;
+  const int kn = (b1 - b0) * 256, kruns = kn / 32;
+  const int kv = K - k0 < static_cast<uint64_t>(kn) ? static_cast<int>(K - k0) : kn;
+  const uint64_t groups = (rows + 7) / 8, group_bytes = static_cast<uint64_t>(nb) * kTile;
+  const uint64_t g0 = static_cast<uint64_t>(blockIdx.x) * 8;
+  const uint64_t span = (groups - g0 < 8 ? groups - g0 : 8) * group_bytes;
+  const __amdgpu_buffer_rsrc_t rsrc = buffer_rsrc(w + g0 * group_bytes, static_cast<uint32_t>(span));
+  const uint32_t lane_off = static_cast<uint32_t>((lane >> 3) * group_bytes);
+  auto block_off = [&](int b) { return b < b1 ? lane_off + static_cast<uint32_t>(b) * kTile : kBufferNone; };
+
+  FusedStage<TYPE, M> fs;
+  QuantizedStage<TYPE, M> qs;
+  if (FUSED)
+    fs.load(xf, K, k0, kn, kv);
+  else
+    qs.load(xv, xs, xsum, K, k0, kn, kv);
+  PlaneBlock<TYPE> A;
+  const int bA = b0 + s;
+  load_planes<TYPE>(A, rsrc, block_off(bA), r);
+  if (FUSED)
+    fs.store(xf, K, k0, kn, kv, lds);
+  else
+    qs.store(xv, xs, xsum, K, k0, kn, kv, lds);
+  __syncthreads();
+
+  float acc[M], mins[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) acc[m] = mins[m] = 0.0f;
+  for (int b = bA; b < b1; b += S) {
+    const PlaneBlock<TYPE> cur = A;
+    load_planes<TYPE>(A, rsrc, block_off(b + S), r);
+    __builtin_amdgcn_sched_barrier(0);
+    plane_block_int8<TYPE, M>(cur, lds, kn, kruns, b - b0, acc, mins);
+  }
+  finish_rows<M>(acc, mins, rows, y, addend, addend_stride, reinterpret_cast<float*>(lds), sk.partials,
+                 sk.counters, sk.ks);
+}
+
+// Decode GEMV over plane tiles with f32 activations (the reference's f32
+// column loop, quant.rs:559-597: w = scale * q - min, acc += w * x), row per
+// lane, waves over the groups; the activations are wave-uniform loads.
+template <int TYPE, int M>
+__global__ __launch_bounds__(512) void gemv_planes_f32_kernel(const uint8_t* __restrict__ w, int nb, uint64_t rows,
+                                                              uint64_t K, const float* __restrict__ x,
+                                                              float* __restrict__ y, const float* __restrict__ addend,
+                                                              uint64_t addend_stride) {
+  constexpr int kTile = tile_bytes(TYPE);
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int lane = threadIdx.x & 63;
+  const int s = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int S = blockDim.x >> 6;
+  const int r = lane & 7;
+  const uint64_t groups = (rows + 7) / 8, group_bytes = static_cast<uint64_t>(nb) * kTile;
+  const uint64_t g0 = static_cast<uint64_t>(blockIdx.x) * 8;
+  const uint64_t span = (groups - g0 < 8 ? groups - g0 : 8) * group_bytes;
+  const __amdgpu_buffer_rsrc_t rsrc = buffer_rsrc(w + g0 * group_bytes, static_cast<uint32_t>(span));
+  const uint32_t lane_off = static_cast<uint32_t>((lane >> 3) * group_bytes);
+  float acc[M], mins[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) acc[m] = mins[m] = 0.0f;
+  for (int b = s; b < nb; b += S) {
+    PlaneBlock<TYPE> a;
+    load_planes<TYPE>(a, rsrc, lane_off + static_cast<uint32_t>(b) * kTile, r);
+    auto planes = [&](int p) { return a.p[p]; };
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint64_t k = static_cast<uint64_t>(b) * 256 + 32 * j;
+      if (k >= K) break;
+      uint32_t q[8];
+      float scale[2], mn[2];
+      plane_run_signed<TYPE>(planes, a.d_bits, j, q, scale, mn);
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        const float4* xr = reinterpret_cast<const float4*>(x + m * K + k);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          const float4 xv = xr[t];
+          const float xe[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float wv = scale[t >> 2] * static_cast<float>(static_cast<int8_t>(byte_of(q[t], e)));
+            wv = wv - mn[t >> 2];
+            acc[m] = fmaf(wv, xe[e], acc[m]);
+          }
+        }
+      }
+    }
+  }
+  finish_rows<M>(acc, mins, rows, y, addend, addend_stride, reinterpret_cast<float*>(lds), nullptr, nullptr, 1);
 }
 
 // f32 activations: per run half, sum(q * x) and sum(x) in f32, then
@@ -1283,21 +1687,22 @@ template <int TYPE>
 __global__ __launch_bounds__(256) void gemm_kernel(const uint8_t* __restrict__ w, int nb, uint64_t rows,
                                                    uint64_t rows_padded, const uint16_t* __restrict__ a16,
                                                    uint64_t m_rows, float* __restrict__ y,
-                                                   const float* __restrict__ addend, uint64_t addend_stride) {
+                                                   const float* __restrict__ addend, uint64_t addend_stride,
+                                                   uint64_t kdim) {
   __shared__ __attribute__((aligned(16))) uint16_t As[kBM][kLdsK];
   __shared__ __attribute__((aligned(16))) uint16_t Bs[kBN][kLdsK];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const uint64_t m0 = static_cast<uint64_t>(blockIdx.y) * kBM;
   const uint64_t n0 = static_cast<uint64_t>(blockIdx.x) * kBN;
   const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
-  const uint64_t K = static_cast<uint64_t>(nb) * 256;
+  const uint64_t K = kdim;  // the logical row length (a multiple of 32)
   floatx4 acc[4][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  const int ksteps = nb * 4;
+  const int ksteps = static_cast<int>((K + kBK - 1) / kBK);
   for (int kb = 0; kb < ksteps; ++kb) {
     // A tile: 128 rows x 64 halves, 16 B per chunk, 4 chunks per thread.
 #pragma unroll
@@ -1305,7 +1710,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const uint8_t* __restrict__ w
       int idx = tid + 256 * i;
       int row = idx >> 3, ch = idx & 7;
       uint4 v = make_uint4(0, 0, 0, 0);
-      if (m0 + row < m_rows)
+      if (m0 + row < m_rows && static_cast<uint64_t>(kb) * kBK + ch * 8 < K)
         v = *reinterpret_cast<const uint4*>(a16 + (m0 + row) * K + static_cast<uint64_t>(kb) * kBK + ch * 8);
       *reinterpret_cast<uint4*>(&As[row][ch * 8]) = v;
     }
@@ -1316,7 +1721,27 @@ __global__ __launch_bounds__(256) void gemm_kernel(const uint8_t* __restrict__ w
       const int b = kb >> 2, c = kb & 3;
       uint32_t out[16];
       if (n < rows_padded) {
-        if (TYPE == kTypeQ4K) {
+        if constexpr (is_plane_format(TYPE)) {
+          // run 2c + h: values 0..15 at k = 32h, 16..31 at 32h + 16
+          const uint8_t* tile = w + ((n >> 3) * nb + b) * tile_bytes(TYPE);
+          const int r = static_cast<int>(n & 7);
+          auto planes = [&](int p) { return ld16(tile + 128 * p + 16 * r); };
+          const uint32_t d_bits =
+              plane_shared_d(TYPE)
+                  ? static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(tile + 128 * plane_count(TYPE) + 2 * r))
+                  : 0u;
+          uint32_t q[8];
+          float sc[2], mn[2];
+          plane_run_signed<TYPE>(planes, d_bits, 2 * c + h, q, sc, mn);
+#pragma unroll
+          for (int t = 0; t < 8; ++t) {
+            const float s = sc[t >> 2], m = mn[t >> 2];
+            out[2 * t] = pack_f16x2(fmaf(s, static_cast<float>(static_cast<int8_t>(byte_of(q[t], 0))), -m),
+                                    fmaf(s, static_cast<float>(static_cast<int8_t>(byte_of(q[t], 1))), -m));
+            out[2 * t + 1] = pack_f16x2(fmaf(s, static_cast<float>(static_cast<int8_t>(byte_of(q[t], 2))), -m),
+                                        fmaf(s, static_cast<float>(static_cast<int8_t>(byte_of(q[t], 3))), -m));
+          }
+        } else if constexpr (TYPE == kTypeQ4K) {
           const uint8_t* tile = w + ((n >> 3) * nb + b) * kQ4kTileBytes + (n & 7) * 16;
           const uint4 hdr = ld16(tile);
           const uint4 qq = ld16(tile + 128 * (1 + 2 * c + h));
@@ -1368,7 +1793,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const uint8_t* __restrict__ w
       // Q4_K: run 2c weights 16h..16h+15 at k = 16h, run 2c+1 at k = 32 + 16h.
       // IQ4_XS: run 2c+h weights 0..15 at k = 32h, 16..31 at k = 32h + 16.
       const int k_lo = TYPE == kTypeQ4K ? 16 * h : 32 * h;
-      const int k_hi = TYPE == kTypeQ4K ? 32 + 16 * h : 32 * h + 16;
+      const int k_hi = TYPE == kTypeQ4K ? 32 + 16 * h : 32 * h + 16;  // IQ4_XS and plane formats alike
       uint4* dlo = reinterpret_cast<uint4*>(&Bs[nl][k_lo]);
       uint4* dhi = reinterpret_cast<uint4*>(&Bs[nl][k_hi]);
       dlo[0] = make_uint4(out[0], out[1], out[2], out[3]);
@@ -1855,6 +2280,120 @@ bool launch_gemv_fused(int type, const uint8_t* tiled, uint64_t rows, uint64_t n
   return true;
 }
 
+// ---- plane formats ----------------------------------------------------------
+
+void launch_repack_planes(int type, const uint8_t* raw, uint64_t rows, uint64_t k, uint64_t nb, uint8_t* tiled,
+                          hipStream_t stream) {
+  const uint64_t threads = rows * nb * (plane_count(type) + (plane_shared_d(type) ? 1 : 0));
+  switch (type) {
+#define X(T)                                                                                                 \
+  case T:                                                                                                    \
+    hipLaunchKernelGGL(repack_planes_kernel<T>, dim3(grid_for(threads, 256)), dim3(256), 0, stream, raw, rows, \
+                       k, nb, tiled);                                                                        \
+    break;
+    X(kTypeQ8_0) X(kTypeQ4_0) X(kTypeIq4Nl) X(kTypeQ5K) X(kTypeQ6K)
+#undef X
+    default:
+      break;
+  }
+}
+
+void launch_dequantize_planes(int type, const uint8_t* tiled, uint64_t rows, uint64_t k, uint64_t nb, int logical,
+                              float* out, hipStream_t stream) {
+  const uint64_t threads = rows * (k / 32);
+  switch (type) {
+#define X(T)                                                                                                        \
+  case T:                                                                                                           \
+    hipLaunchKernelGGL(dequantize_planes_kernel<T>, dim3(grid_for(threads, 256)), dim3(256), 0, stream, tiled, rows, \
+                       k, nb, logical, out);                                                                        \
+    break;
+    X(kTypeQ8_0) X(kTypeQ4_0) X(kTypeIq4Nl) X(kTypeQ5K) X(kTypeQ6K)
+#undef X
+    default:
+      break;
+  }
+}
+
+namespace {
+
+// LDS of the plane GEMV: int8 values [m][kn] and a 16-byte record per run,
+// or the cross-wave reduction, whichever is larger.
+size_t gemv_planes_lds_bytes(uint64_t nbk, uint64_t m, int splits) {
+  const size_t act = m * nbk * 256 + m * nbk * 8 * 16;
+  const size_t red = static_cast<size_t>(splits) * m * 2 * 64 * 4;
+  return act > red ? act : red;
+}
+
+int planes_waves(uint64_t nbk, int hint) {
+  int splits = hint;
+  if (splits < 1) {
+    splits = 1;
+    while (splits < 8 && static_cast<uint64_t>(2 * splits) <= nbk) splits *= 2;
+  }
+  return splits > 8 ? 8 : splits;  // launch bound 512
+}
+
+}  // namespace
+
+int gemv_planes_min_ksplit(uint64_t nb, uint64_t m) {
+  int ks = 1;
+  while (gemv_planes_lds_bytes((nb + ks - 1) / ks, m, 8) > 65536 && static_cast<uint64_t>(ks) < nb) ++ks;
+  return ks;
+}
+
+void launch_gemv_planes_int8(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, uint64_t k,
+                             const int8_t* values, const float* scales, const int32_t* sums, const float* x,
+                             uint64_t m, float* y, const float* addend, uint64_t addend_stride, int splits,
+                             const GemvSplitK& sk, hipStream_t stream) {
+  const uint64_t nbk = (nb + sk.ks - 1) / sk.ks;
+  const int waves = planes_waves(nbk, splits);
+  const size_t lds = gemv_planes_lds_bytes(nbk, m, waves);
+  dim3 grid(static_cast<unsigned>((rows + 63) / 64), static_cast<unsigned>(sk.ks)), block(64 * waves);
+  const int inb = static_cast<int>(nb);
+  const SplitK kk{sk.partials, sk.counters, sk.ks};
+  const int key = type * 16 + static_cast<int>(m) - 1;
+  switch (key) {
+#define Y(T, MM)                                                                                                  \
+  case T * 16 + MM - 1:                                                                                           \
+    if (x)                                                                                                        \
+      hipLaunchKernelGGL((gemv_planes_int8_kernel<T, MM, true>), grid, block, lds, stream, tiled, inb, rows, k,    \
+                         values, scales, sums, x, y, addend, addend_stride, kk);                                  \
+    else                                                                                                          \
+      hipLaunchKernelGGL((gemv_planes_int8_kernel<T, MM, false>), grid, block, lds, stream, tiled, inb, rows, k,   \
+                         values, scales, sums, x, y, addend, addend_stride, kk);                                  \
+    break;
+#define X(T) Y(T, 1) Y(T, 2) Y(T, 3) Y(T, 4) Y(T, 5) Y(T, 6) Y(T, 7) Y(T, 8)
+    X(kTypeQ8_0) X(kTypeQ4_0) X(kTypeIq4Nl) X(kTypeQ5K) X(kTypeQ6K)
+#undef X
+#undef Y
+    default:
+      break;
+  }
+}
+
+void launch_gemv_planes_f32(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, uint64_t k, const float* x,
+                            uint64_t m, float* y, const float* addend, uint64_t addend_stride, int splits,
+                            hipStream_t stream) {
+  const int waves = planes_waves(nb, splits);
+  const size_t lds = static_cast<size_t>(waves) * m * 2 * 64 * 4;
+  dim3 grid(static_cast<unsigned>((rows + 63) / 64)), block(64 * waves);
+  const int inb = static_cast<int>(nb);
+  const int key = type * 16 + static_cast<int>(m) - 1;
+  switch (key) {
+#define Y(T, MM)                                                                                                   \
+  case T * 16 + MM - 1:                                                                                            \
+    hipLaunchKernelGGL((gemv_planes_f32_kernel<T, MM>), grid, block, lds, stream, tiled, inb, rows, k, x, y, addend, \
+                       addend_stride);                                                                             \
+    break;
+#define X(T) Y(T, 1) Y(T, 2) Y(T, 3) Y(T, 4) Y(T, 5) Y(T, 6) Y(T, 7) Y(T, 8)
+    X(kTypeQ8_0) X(kTypeQ4_0) X(kTypeIq4Nl) X(kTypeQ5K) X(kTypeQ6K)
+#undef X
+#undef Y
+    default:
+      break;
+  }
+}
+
 // K-splits for the LDS form: only when the row blocks alone leave most of
 // the 256 CUs idle (4096 rows: 64 blocks -> 4 splits; 14336 rows: 224
 // blocks -> none, where the split-K epilogue costs more than the last 32
@@ -1930,8 +2469,22 @@ int gemm_default_variant(uint64_t rows, uint64_t m) {
   return 3;
 }
 
-void launch_gemm(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, const uint16_t* a16, uint64_t m,
-                 float* y, const float* addend, uint64_t addend_stride, int variant, hipStream_t stream) {
+void launch_gemm(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, uint64_t k, const uint16_t* a16,
+                 uint64_t m, float* y, const float* addend, uint64_t addend_stride, int variant,
+                 hipStream_t stream) {
+  const uint64_t rows_padded = (rows + 7) / 8 * 8;
+  dim3 grid(static_cast<unsigned>((rows + kBN - 1) / kBN), static_cast<unsigned>((m + kBM - 1) / kBM));
+  switch (type) {
+#define X(T)                                                                                                     \
+  case T:                                                                                                        \
+    hipLaunchKernelGGL(gemm_kernel<T>, grid, dim3(256), 0, stream, tiled, static_cast<int>(nb), rows, rows_padded, \
+                       a16, m, y, addend, addend_stride, k);                                                     \
+    return;
+    X(kTypeQ8_0) X(kTypeQ4_0) X(kTypeIq4Nl) X(kTypeQ5K) X(kTypeQ6K)
+#undef X
+    default:
+      break;
+  }
   if (variant == 0) variant = gemm_default_variant(rows, m);
   switch (variant) {
     case 2:
@@ -1946,14 +2499,12 @@ void launch_gemm(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, con
     default:
       break;
   }
-  const uint64_t rows_padded = (rows + 7) / 8 * 8;
-  dim3 grid(static_cast<unsigned>((rows + kBN - 1) / kBN), static_cast<unsigned>((m + kBM - 1) / kBM));
   if (type == kTypeQ4K)
     hipLaunchKernelGGL(gemm_kernel<kTypeQ4K>, grid, dim3(256), 0, stream, tiled, static_cast<int>(nb), rows,
-                       rows_padded, a16, m, y, addend, addend_stride);
+                       rows_padded, a16, m, y, addend, addend_stride, k);
   else
     hipLaunchKernelGGL(gemm_kernel<kTypeIq4Xs>, grid, dim3(256), 0, stream, tiled, static_cast<int>(nb), rows,
-                       rows_padded, a16, m, y, addend, addend_stride);
+                       rows_padded, a16, m, y, addend, addend_stride, k);
 }
 
 }  // namespace mq

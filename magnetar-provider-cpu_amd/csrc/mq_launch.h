@@ -65,10 +65,31 @@ void launch_gemv_f32(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb,
 // Prefill GEMM on MFMA: y[m][rows] = a16[m][K] . dequant(W)^T, f32 out.
 // variant 1: B dequantized through LDS (128 x 128 tiles); 2, 3, 4: B in
 // registers with 128 x 256, 128 x 128 and 64 x 256 tiles; 0: choose.
-void launch_gemm(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb,
+// k = the logical row length; plane formats always take variant 1.
+void launch_gemm(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, uint64_t k,
                  const uint16_t* a16, uint64_t m, float* y, const float* addend, uint64_t addend_stride,
                  int variant, hipStream_t stream);
 int gemm_default_variant(uint64_t rows, uint64_t m);
+
+// Plane formats (Q8_0, Q4_0, IQ4_NL, Q5_K, Q6_K; layout in mq_device.h).
+// k is the logical row length (a multiple of the format's block), nb =
+// ceil(k / 256) groups.
+void launch_repack_planes(int type, const uint8_t* raw, uint64_t rows, uint64_t k, uint64_t nb,
+                          uint8_t* tiled, hipStream_t stream);
+void launch_dequantize_planes(int type, const uint8_t* tiled, uint64_t rows, uint64_t k, uint64_t nb,
+                              int logical, float* out, hipStream_t stream);
+// The fewest K-splits whose LDS staging fits 64 KiB for m rows.
+int gemv_planes_min_ksplit(uint64_t nb, uint64_t m);
+// Decode GEMV (m in 1..8), int8 activations: quantized in the kernel from x
+// (x != null) or taken pre-quantized (values, scales, sums).
+void launch_gemv_planes_int8(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, uint64_t k,
+                             const int8_t* values, const float* scales, const int32_t* sums, const float* x,
+                             uint64_t m, float* y, const float* addend, uint64_t addend_stride, int splits,
+                             const GemvSplitK& sk, hipStream_t stream);
+// Decode GEMV (m in 1..8), f32 activations.
+void launch_gemv_planes_f32(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, uint64_t k,
+                            const float* x, uint64_t m, float* y, const float* addend, uint64_t addend_stride,
+                            int splits, hipStream_t stream);
 
 // Grid-shape helper for the GEMV (waves per work-group).
 int gemv_default_splits(uint64_t rows, uint64_t nb, uint64_t m, int variant);

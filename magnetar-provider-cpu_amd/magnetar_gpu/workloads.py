@@ -14,7 +14,7 @@ import functools
 
 import numpy as np
 
-from . import IQ4_XS, Q4_K, gaussian, quantize
+from . import BLOCK_BYTES, BLOCK_VALUES, IQ4_XS, Q4_K, Q5_K, Q6_K, gaussian, quantize
 
 # name -> (gguf type, stored rows N, stored cols K, workload seed, weight index)
 WEIGHTS = {
@@ -53,3 +53,25 @@ def activations(seed, m, k):
 def weight_bytes_per_call(name):
     fmt, n, k, _, _ = WEIGHTS[name]
     return n * k // 256 * (144 if fmt == Q4_K else 136)
+
+
+def scale_offsets(fmt):
+    """Byte offsets of a block's f16 scale fields."""
+    if fmt in (Q4_K, Q5_K):
+        return (0, 2)
+    return (208,) if fmt == Q6_K else (0,)
+
+
+def random_blocks(fmt, rows, cols, seed):
+    """Checkpoint-shaped random blocks for timing the formats without an
+    encoder: uniform random bytes with every f16 scale field a small
+    positive value (exponent 3..7, as the reference's own test matrices).
+    uint8 [rows, row bytes]."""
+    bb, bv = BLOCK_BYTES[fmt], BLOCK_VALUES[fmt]
+    rng = np.random.default_rng(seed)
+    blocks = rng.integers(0, 256, size=(rows * cols // bv, bb), dtype=np.uint8)
+    for at in scale_offsets(fmt):
+        bits = (rng.integers(3, 8, size=blocks.shape[0]) << 10) | rng.integers(0, 1024, size=blocks.shape[0])
+        blocks[:, at] = bits & 0xFF
+        blocks[:, at + 1] = bits >> 8
+    return blocks.reshape(rows, cols // bv * bb)

@@ -293,7 +293,7 @@ def test_device_entry_points_agree_with_host_entry_point(ctx):
 def test_boundary_errors_and_declines(ctx):
     w = packed(Q4_K, 4, 256, 41)
     with pytest.raises(mg.Declined):
-        ctx.upload(8, 4, 256, np.zeros(4 * 34, np.uint8))  # Q8_0 has no GPU path
+        ctx.upload(10, 4, 256, np.zeros(4 * 84, np.uint8))  # Q2_K has no GPU path
     with pytest.raises(mg.Declined):
         ctx.upload(Q4_K, 4, 256, w, transposed=False)
     with pytest.raises(mg.GpuError) as e:
