@@ -11,7 +11,8 @@ the device time.
 
 Also reported: the GEMV kernel alone against the 8 TB/s HBM roofline, the
 other decode shapes, one Llama-3-8B-shaped decoder layer decode step
-(device-resident, weights + KV cache bytes per step), the M=512 prefill
+(device-resident, weights + KV cache bytes per step), the same GEMV and
+GEMM for Q8_0, Q6_K, Q5_K, Q4_0 and IQ4_NL weights, the M=512 prefill
 GEMM (x[512, 4096] . W[14336, 4096]^T) in TFLOP/s against the 2.5 PFLOP/s
 dense f16 MFMA peak, and the reference's CPU path (the oracle's AVX2
 restatement) timed on this host's cores.
@@ -128,7 +129,7 @@ def main():
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=8.0, help="bound on CPU-baseline timing")
-    ap.add_argument("--parts", default="gemv,shapes,iq4xs,layer,gemm,cpu",
+    ap.add_argument("--parts", default="gemv,shapes,iq4xs,layer,formats,gemm,cpu",
                     help="comma list of parts to run (the headline line needs gemv)")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="also run a plain device copy of this size (counter calibration under rocprofv3)")
@@ -239,6 +240,8 @@ def main():
         iq4xs_part(ctx, torch, workloads, args, per_graph, use_graph, extra)
     if "layer" in parts:
         layer_part(ctx, torch, per_graph, use_graph, extra)
+    if "formats" in parts:
+        formats_part(ctx, torch, per_graph, use_graph, extra)
     gemm = gemm_part(ctx, torch, workloads, use_graph, args) if "gemm" in parts else None
     cpu = cpu_part(fmt, wbytes, n, k, x_host, y_gpu, weight_bytes, args) if "cpu" in parts else None
 
@@ -304,6 +307,47 @@ def layer_part(ctx, torch, per_graph, use_graph, extra):
     log(f"decoder layer decode step: {t * 1e6:.1f} us, {hbm} HBM bytes (Q4_K weights {data.weight_bytes()} + "
         f"f32 K/V {kv_bytes}), {hbm / t / 1e9:.1f} GB/s")
     layer.release()
+
+
+def formats_part(ctx, torch, per_graph, use_graph, extra):
+    # ---- the plane formats: decode GEMV x[1, 4096] . W[14336, 4096]^T and the
+    # M = 512 prefill GEMM on the same weight (random blocks, small f16 scales)
+    import magnetar_gpu as mg
+    from magnetar_gpu import workloads
+
+    n, k = 14336, 4096
+    x = torch.from_numpy(mg.gaussian(4500, 1.0, k).reshape(1, k)).cuda()
+    y = torch.empty((1, n), dtype=torch.float32, device="cuda")
+    xm = torch.from_numpy(mg.gaussian(4501, 1.0, 512 * k).reshape(512, k)).cuda()
+    ym = torch.empty((512, n), dtype=torch.float32, device="cuda")
+    for fmt in (mg.Q8_0, mg.Q6_K, mg.Q5_K, mg.Q4_0, mg.IQ4_NL):
+        name = mg.FORMAT_NAMES[fmt]
+        w = workloads.random_blocks(fmt, n, k, 4000 + fmt)
+        copies = [ctx.upload(fmt, n, k, w) for _ in range(max(2, -(-600_000_000 // w.size)))]
+
+        def gv(i, stream, copies=copies):
+            ctx.matmul_dev(copies[i % len(copies)], x.data_ptr(), 1, k, y.data_ptr(), int8=True, stream=stream)
+
+        r = GraphRunner(torch, gv, per_graph, use_graph)
+        r.time(per_graph)
+        t = r.time(5 * per_graph) / (5 * per_graph)
+        extra[f"{name}_gemv_kernel_us"] = round(t * 1e6, 3)
+        extra[f"{name}_gemv_GBps"] = round(w.size / t / 1e9, 1)
+        extra[f"{name}_gemv_frac_hbm"] = round(w.size / t / 1e9 / HBM_PEAK_GBS, 4)
+
+        def gm(i, stream, copies=copies):
+            ctx.matmul_dev(copies[i % len(copies)], xm.data_ptr(), 512, k, ym.data_ptr(), int8=True, stream=stream)
+
+        rg = GraphRunner(torch, gm, 5, use_graph)
+        rg.time(5)
+        tg = rg.time(20) / 20
+        tflops = 2 * 512 * n * k / tg / 1e12
+        extra[f"{name}_gemm512_us"] = round(tg * 1e6, 2)
+        extra[f"{name}_gemm512_TFLOPs"] = round(tflops, 1)
+        log(f"{name}: gemv {t * 1e6:.2f} us, {w.size / t / 1e9:.1f} GB/s ({w.size} B); "
+            f"M=512 gemm {tg * 1e6:.1f} us, {tflops:.1f} TFLOP/s")
+        for h in copies:
+            h.release()
 
 
 def gemm_part(ctx, torch, workloads, use_graph, args):
