@@ -45,8 +45,10 @@ void mg_executor_destroy(mg_executor *ex);
 const char *mg_executor_last_error(mg_executor *ex);
 
 /* `write_packed_weight_tensor` (src/native/mod.rs:638-653): *stored = 1
- * (PackedWeightWrite::Stored) or 0 (Declined: unsupported format,
- * untransposed weight, or packed weights disabled). */
+ * (PackedWeightWrite::Stored) or 0 (Declined: a format without a GPU path,
+ * packed weights disabled, or device bytes the memory ledger cannot
+ * admit). Untransposed weights and tables are stored: matmuls read them
+ * by the reference's orientation rule, embeddings gather their rows. */
 int mg_write_packed_weight_tensor(mg_executor *ex, const char *id, uint32_t gguf_type,
                                   uint64_t stored_rows, uint64_t stored_cols,
                                   int transposed, const uint8_t *bytes, size_t len,
@@ -116,6 +118,13 @@ const char *mg_kernel_advertisement_json(uint32_t index);
 /* Packed weights materialized to f32 so far (the profile counter,
  * src/native/mod.rs:79-81). */
 uint64_t mg_materialization_count(mg_executor *ex);
+
+/* Bytes the memory ledger holds: admitted f32 tensors and kernel outputs
+ * (`write_tensor_admitted`, src/lib.rs:1713-1738; output admission,
+ * src/lib.rs:2132-2285) plus every packed weight's device footprint, which
+ * is admitted before its upload replaces a weight of the same id (an
+ * upload the ledger cannot hold is declined). */
+uint64_t mg_memory_used(mg_executor *ex);
 
 #ifdef __cplusplus
 }

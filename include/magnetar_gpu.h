@@ -46,6 +46,7 @@ extern "C" {
 
 /* matmul flags */
 #define MQ_INT8_ACTIVATIONS 1u /* MAGNETAR_CPU_INT8_ACTIVATIONS (default on) */
+#define MQ_TRANSPOSE_B 2u      /* the Kernel's transpose_b attribute */
 
 typedef struct mq_ctx mq_ctx;
 
@@ -67,10 +68,11 @@ const char *mq_last_error(mq_ctx *ctx);
  * `len` = stored_rows * stored_cols / block_values * block_bytes checkpoint
  * bytes (Q8_0 32 / 34, Q4_0 and IQ4_NL 32 / 18, Q4_K 256 / 144, Q5_K
  * 256 / 176, Q6_K 256 / 210, IQ4_XS 256 / 136); stored_cols must be whole
- * blocks. Returns MQ_DECLINED for a type without a GPU path (Q2_K, Q3_K,
- * the IQ2 / IQ3 grid formats) or for
- * transposed == 0 (stored rows are the input rows: the axpy layout), so
- * the caller keeps the f32 path. Replaces
+ * blocks. transposed != 0: the stored rows are the logical [k, n] weight's
+ * output columns; 0: an untransposed weight or table whose stored rows are
+ * its logical rows. Returns MQ_DECLINED for a type without a GPU path
+ * (Q2_K, Q3_K, the IQ2 / IQ3 grid formats), so the caller keeps the f32
+ * path. Replaces
  * `write_packed_weight_tensor` -> `PackedWeightWrite::{Stored,Declined}`
  * (src/native/mod.rs:638-653) and `PackedWeight::new` (external,
  * magnetar-provider-api; used at src/native/tests.rs:66). */
@@ -89,12 +91,17 @@ int mq_weight_info(mq_ctx *ctx, uint64_t handle, uint32_t *gguf_type,
                    uint64_t *stored_rows, uint64_t *stored_cols, int *transposed,
                    uint64_t *device_bytes);
 
-/* y[m][stored_rows] = x[m][k] . W^T, host pointers, synchronous (returns
- * after y is copied back). k must equal stored_cols (else MQ_ERR_SHAPE).
- * flags & MQ_INT8_ACTIVATIONS selects int8 activations (the reference
- * default) else f32 activations. Replaces `NativeState::packed_matmul`
- * (src/native/mod.rs:110-152) with `quant::matmul_columns`
- * (src/native/quant.rs:430-446). */
+/* y[m][n] = x[m][k] . W, host pointers, synchronous (returns after y is
+ * copied back). The orientation follows the reference's rule
+ * (src/native/mod.rs:217-227): when `transposed` (upload) differs from
+ * flags & MQ_TRANSPOSE_B the stored rows are the n output columns and k
+ * must equal stored_cols (`NativeState::packed_matmul`, mod.rs:110-152 with
+ * `quant::matmul_columns`, quant.rs:430-446; flags & MQ_INT8_ACTIVATIONS
+ * selects int8 activations, the reference default, else f32); otherwise
+ * the stored rows are the k input rows, n = stored_cols, and the product
+ * is the input-major one with f32 activations (`packed_axpy`, mod.rs:154-194
+ * with `quant::axpy_columns`, quant.rs:1652-1688). A k mismatch is
+ * MQ_ERR_SHAPE with the reference's text. */
 int mq_matmul(mq_ctx *ctx, uint64_t handle, const float *x, uint64_t m,
               uint64_t k, uint32_t flags, float *y);
 
@@ -129,7 +136,8 @@ int mq_quantize_activations_dev(mq_ctx *ctx, const float *x_dev, uint64_t m,
 /* The decode GEMV on already-quantized activations (m <= 8): the column
  * kernels' int8 path `columns_q4k_avx2` / `columns_iq4xs_avx2`
  * (src/native/quant.rs:666-744, 1386-1433) without the quantization step,
- * so one quantized activation can feed several weights. */
+ * so one quantized activation can feed several weights. The stored rows
+ * are the outputs, whatever the weight's `transposed`. */
 int mq_matmul_prequantized_dev(mq_ctx *ctx, uint64_t handle,
                                const int8_t *values_dev, const float *scales_dev,
                                const int32_t *sums_dev, uint64_t m, uint64_t k,
@@ -162,6 +170,22 @@ int mq_dequantize(mq_ctx *ctx, uint64_t handle, int logical, float *out);
 /* mq_dequantize into device memory, enqueued on `stream`. */
 int mq_dequantize_dev(mq_ctx *ctx, uint64_t handle, int logical, float *out_dev,
                       void *stream);
+
+/* The `embedding` Kernel on a packed table (src/native/mod.rs:389-417,
+ * 432-449): out[count][dim] = the table's logical rows ids[0..count) (the
+ * stored rows when the table was uploaded untransposed, else each token's
+ * value in every stored row), times `scale` unless scale is NaN (the
+ * Kernel's optional `scale` attribute). ids are f32 token ids in host
+ * memory, validated first: a negative, fractional or out-of-vocabulary id
+ * is MQ_ERR_SHAPE with the reference's text ("token id X is not below the
+ * vocabulary size V"). Host output, synchronous. */
+int mq_embedding(mq_ctx *ctx, uint64_t handle, const float *ids, uint64_t count,
+                 float scale, float *out);
+
+/* mq_embedding into device memory, enqueued on `stream` (the ids are
+ * staged synchronously before the kernel is queued). */
+int mq_embedding_dev(mq_ctx *ctx, uint64_t handle, const float *ids, uint64_t count,
+                     float scale, float *out_dev, void *stream);
 
 /* ---- Decoder-layer operators ------------------------------------------------
  * Device memory, enqueued on `stream` (a hipStream_t; NULL is the null

@@ -3,6 +3,8 @@
 #include "executor.hpp"
 
 #include <algorithm>
+#include <cmath>
+#include <cstdlib>
 #include <cstring>
 
 namespace magnetar {
@@ -43,13 +45,13 @@ std::vector<uint64_t> PackedWeight::logical_shape() const {
 // f32 in/out, contiguous, Host memory class, rank 2, TimeoutOnly.
 std::vector<KernelAdvertisement> gpu_kernel_advertisements() {
   std::vector<KernelAdvertisement> out;
-  for (const char* name : {"matmul", "matmul-bias", "matmul-residual"}) {
+  for (const char* name : {"matmul", "matmul-bias", "matmul-residual", "embedding"}) {
     KernelAdvertisement a;
     a.provider = kGpuProviderName;
     a.name = name;
     a.version = "1.0.0";
     a.operator_id = std::string("magnetar:") + name + "@1";
-    a.family = "GpuMatrix";
+    a.family = std::string(name) == "embedding" ? "GpuGather" : "GpuMatrix";
     a.conformance_profile = kConformanceProfile;
     a.input_dtypes = {"f32"};
     a.output_dtypes = {"f32"};
@@ -96,13 +98,24 @@ std::optional<GpuPackedWeights::Entry> GpuPackedWeights::find(const std::string&
 
 bool GpuPackedWeights::contains(const std::string& id) { return find(id).has_value(); }
 
-PackedWeightWrite GpuPackedWeights::store(const std::string& id, const PackedWeight& w, std::string* why) {
+PackedWeightWrite GpuPackedWeights::store(const std::string& id, const PackedWeight& w, std::string* why,
+                                          const std::function<bool(uint64_t)>& admit) {
   uint64_t handle = 0;
   int rc = mq_weight_upload(ctx_, w.format, w.stored_rows, w.stored_cols, w.transposed ? 1 : 0, w.bytes.data(),
                             w.bytes.size(), &handle);
   if (rc != MQ_OK) {
     if (why) *why = mq_last_error(ctx_);
     return PackedWeightWrite::Declined;
+  }
+  if (admit) {
+    uint32_t type = 0;
+    uint64_t rows = 0, cols = 0, bytes = 0;
+    int tr = 0;
+    if (mq_weight_info(ctx_, handle, &type, &rows, &cols, &tr, &bytes) != MQ_OK || !admit(bytes)) {
+      mq_weight_release(ctx_, handle);
+      if (why) *why = "memory admission denied for the packed weight's " + std::to_string(bytes) + " device bytes";
+      return PackedWeightWrite::Declined;
+    }
   }
   std::lock_guard<std::mutex> lock(mu_);
   auto it = packed_.find(id);
@@ -143,6 +156,13 @@ std::optional<HostTensor> GpuPackedWeights::materialize(const std::string& id) {
 // forms when input 1 is a packed weight.
 std::optional<Result<HostTensor>> GpuPackedWeights::run(const GpuExecutor& executor,
                                                         const KernelInvocation& inv) {
+  if (inv.kernel == "embedding") {
+    // the table is input 0; an f32 table is the wrapped executor's
+    if (inv.inputs.size() < 2) return std::nullopt;
+    auto t = find(inv.inputs[0]);
+    if (!t) return std::nullopt;
+    return embedding(executor, inv, *t);
+  }
   if (inv.kernel != "matmul" && inv.kernel != "matmul-bias" && inv.kernel != "matmul-residual") return std::nullopt;
   if (inv.inputs.size() < 2) return std::nullopt;
   auto w = find(inv.inputs[1]);
@@ -168,7 +188,7 @@ Result<HostTensor> GpuPackedWeights::matmul(const GpuExecutor& executor, const K
   uint64_t m = 0, k = 0;
   if (!a.rows_cols(m, k))
     return R::failure(KernelError::failed("matmul expects a rank-2 activation tensor, got shape " + shape_text(a.shape)));
-  uint32_t flags = int8_ ? MQ_INT8_ACTIVATIONS : 0;
+  uint32_t flags = (int8_ ? MQ_INT8_ACTIVATIONS : 0) | (transpose_b ? MQ_TRANSPOSE_B : 0);
   if (transpose_a) {
     // The reference expands the weight and runs the dense f32 matmul: f32
     // activations, the transposed activation read by stride swap.
@@ -179,16 +199,20 @@ Result<HostTensor> GpuPackedWeights::matmul(const GpuExecutor& executor, const K
       for (uint64_t c = 0; c < k; ++c) t.data[c * m + r] = a.data[r * k + c];
     std::swap(m, k);
     a = std::move(t);
-    flags = 0;
-  } else if (w.transposed == transpose_b) {
-    return R::failure({KernelErrorKind::AttributeUnsupported,
-                       "packed weight " + inv.inputs[1] + " is read input-major (transpose_b " +
-                           (transpose_b ? "true" : "false") + "): the GPU path multiplies output-major weights only"});
+    flags &= ~MQ_INT8_ACTIVATIONS;
   }
-  if (k != w.cols || k % 32 != 0)
+  // the reference's orientation rule (src/native/mod.rs:217-227): stored
+  // rows are the outputs when transposed != transpose_b, else the inputs
+  // (`packed_axpy`, f32 activations)
+  const bool output_major = w.transposed != transpose_b;
+  if (!output_major) flags &= ~MQ_INT8_ACTIVATIONS;
+  if (output_major && (k != w.cols || k % 32 != 0))
     return R::failure(KernelError::failed("packed matmul: activations have " + std::to_string(k) +
                                           " columns, the weight's stored rows " + std::to_string(w.cols)));
-  const uint64_t n = w.rows;
+  if (!output_major && k != w.rows)
+    return R::failure(KernelError::failed("packed matmul: activations have " + std::to_string(k) +
+                                          " columns, the weight " + std::to_string(w.rows) + " stored rows"));
+  const uint64_t n = output_major ? w.rows : w.cols;
   HostTensor out;
   out.shape = {m, n};
   out.data.resize(m * n);
@@ -214,6 +238,31 @@ Result<HostTensor> GpuPackedWeights::matmul(const GpuExecutor& executor, const K
   int rc = addend ? mq_matmul_add(ctx_, w.handle, a.data.data(), m, k, flags, addend, addend_rows, out.data.data())
                   : mq_matmul(ctx_, w.handle, a.data.data(), m, k, flags, out.data.data());
   if (rc != MQ_OK) return R::failure(KernelError::failed(mq_last_error(ctx_)));
+  return R::success(std::move(out));
+}
+
+// `NativeState::embedding` (src/native/mod.rs:389-417) and the `scale`
+// attribute (432-449): the token rows of a packed table, validated and
+// gathered on the GPU.
+Result<HostTensor> GpuPackedWeights::embedding(const GpuExecutor& executor, const KernelInvocation& inv,
+                                               const Entry& table) {
+  using R = Result<HostTensor>;
+  auto ids = executor.read_tensor(inv.inputs[1]);
+  if (!ids) return R::failure(KernelError::failed("no materialized data for input resource " + inv.inputs[1]));
+  float scale = std::nanf("");
+  auto it = inv.attributes.find("scale");
+  if (it != inv.attributes.end()) {
+    char* end = nullptr;
+    scale = std::strtof(it->second.c_str(), &end);
+    if (end == it->second.c_str())
+      return R::failure({KernelErrorKind::AttributeUnsupported, "embedding scale " + it->second + " is not a number"});
+  }
+  const uint64_t dim = table.transposed ? table.rows : table.cols;
+  HostTensor out;
+  out.shape = {static_cast<uint64_t>(ids->data.size()), dim};
+  out.data.resize(ids->data.size() * dim);
+  if (mq_embedding(ctx_, table.handle, ids->data.data(), ids->data.size(), scale, out.data.data()) != MQ_OK)
+    return R::failure(KernelError::failed(mq_last_error(ctx_)));
   return R::success(std::move(out));
 }
 
@@ -254,7 +303,12 @@ PackedWeightWrite GpuExecutor::write_packed_weight_tensor(const std::string& id,
     if (why) *why = "packed weights are disabled";
     return PackedWeightWrite::Declined;
   }
-  PackedWeightWrite r = packed_->store(id, w, why);
+  // the device bytes are admitted to the ledger before the upload replaces
+  // a weight of the same id
+  PackedWeightWrite r = packed_->store(id, w, why, [&](uint64_t bytes) {
+    std::lock_guard<std::mutex> lock(mu_);
+    return memory_.admit(id, bytes);
+  });
   if (r == PackedWeightWrite::Stored) {
     std::lock_guard<std::mutex> lock(mu_);
     storage_.erase(id);
@@ -265,8 +319,9 @@ PackedWeightWrite GpuExecutor::write_packed_weight_tensor(const std::string& id,
 // `write_tensor`: an f32 write forgets a packed weight of the same id
 // (src/native/mod.rs:629-636).
 void GpuExecutor::write_tensor(const std::string& id, HostTensor tensor) {
-  if (packed_) packed_->forget(id);
+  const bool was_packed = packed_ && packed_->forget(id);
   std::lock_guard<std::mutex> lock(mu_);
+  if (was_packed) memory_.release(id);  // the device bytes it held
   storage_[id] = std::move(tensor);
 }
 

@@ -17,6 +17,7 @@
 
 #include <atomic>
 #include <cstdint>
+#include <functional>
 #include <map>
 #include <memory>
 #include <mutex>
@@ -139,7 +140,11 @@ class GpuPackedWeights {
   std::optional<HostTensor> materialize(const std::string& id);
   std::optional<std::vector<uint64_t>> shape(const std::string& id);
 
-  PackedWeightWrite store(const std::string& id, const PackedWeight& weight, std::string* why);
+  // Uploads the weight; `admit` (may be empty) is asked for its device
+  // bytes before the upload replaces a weight of the same id: false
+  // releases the upload and declines, leaving any previous weight.
+  PackedWeightWrite store(const std::string& id, const PackedWeight& weight, std::string* why,
+                          const std::function<bool(uint64_t)>& admit = {});
   bool forget(const std::string& id);
   bool contains(const std::string& id);
   uint64_t materializations() const { return materialized_; }
@@ -153,6 +158,7 @@ class GpuPackedWeights {
   };
   std::optional<Entry> find(const std::string& id);
   Result<HostTensor> matmul(const GpuExecutor& executor, const KernelInvocation& invocation, const Entry& weight);
+  Result<HostTensor> embedding(const GpuExecutor& executor, const KernelInvocation& invocation, const Entry& table);
 
   mq_ctx* ctx_;
   bool int8_;

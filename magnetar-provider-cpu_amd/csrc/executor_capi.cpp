@@ -220,4 +220,6 @@ const char* mg_kernel_advertisement_json(uint32_t index) {
 
 uint64_t mg_materialization_count(mg_executor* e) { return e ? e->ex->materializations() : 0; }
 
+uint64_t mg_memory_used(mg_executor* e) { return e ? e->ex->memory().used() : 0; }
+
 }  // extern "C"

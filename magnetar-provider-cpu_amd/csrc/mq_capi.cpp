@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <map>
@@ -58,6 +59,9 @@ struct mq_ctx {
   int gemv_splits_override = 0;
   int gemv_variant = 0;
   int gemm_variant = 0;
+  // Token ids of the embedding lookup (device copy).
+  uint32_t* ids = nullptr;
+  size_t ids_cap = 0;
   // Attention split-key partials (stream-ordered like the workspace).
   void* attn = nullptr;
   size_t attn_bytes = 0;
@@ -183,7 +187,24 @@ const Weight* find_weight(mq_ctx* ctx, uint64_t handle) {
   return it == ctx->weights.end() ? nullptr : &it->second;
 }
 
-int check_k(mq_ctx* ctx, const Weight& w, uint64_t k) {
+// The reference's orientation rule (src/native/mod.rs:217-227): the stored
+// rows are the output columns when the weight is stored transposed and not
+// read transposed, or stored untransposed (a tied table) and read
+// transposed; otherwise they are the input rows (the axpy product).
+bool output_major(const Weight& w, uint32_t flags) {
+  return (w.transposed != 0) != ((flags & MQ_TRANSPOSE_B) != 0);
+}
+
+uint64_t out_cols(const Weight& w, uint32_t flags) { return output_major(w, flags) ? w.rows : w.cols; }
+
+int check_k(mq_ctx* ctx, const Weight& w, uint64_t k, uint32_t flags = 0) {
+  if (!output_major(w, flags)) {
+    if (k != w.rows)
+      return fail(ctx, MQ_ERR_SHAPE,
+                  "packed matmul: activations have " + std::to_string(k) + " columns, the weight " +
+                      std::to_string(w.rows) + " stored rows");
+    return MQ_OK;
+  }
   if (k != w.cols || k % 32 != 0)
     return fail(ctx, MQ_ERR_SHAPE,
                 "packed matmul: activations have " + std::to_string(k) + " columns, the weight's stored rows " +
@@ -257,18 +278,27 @@ int gemv_locked(mq_ctx* ctx, const Weight& w, const float* x, uint64_t m, uint64
 // addend_rows: 0 (no addend), 1 (one row broadcast) or m.
 int matmul_locked(mq_ctx* ctx, const Weight& w, const float* x, uint64_t m, uint64_t k, uint32_t flags, float* y,
                   hipStream_t stream, const float* addend = nullptr, uint64_t addend_rows = 0) {
-  int rc = check_k(ctx, w, k);
+  if (flags & ~(MQ_INT8_ACTIVATIONS | MQ_TRANSPOSE_B)) return fail(ctx, MQ_ERR_ARGUMENT, "unknown matmul flag bits");
+  int rc = check_k(ctx, w, k, flags);
   if (rc) return rc;
-  if (flags & ~MQ_INT8_ACTIVATIONS) return fail(ctx, MQ_ERR_ARGUMENT, "unknown matmul flag bits");
   if (m == 0) return MQ_OK;
   if (!x || !y) return fail(ctx, MQ_ERR_ARGUMENT, "null activation or output pointer");
   if (addend && addend_rows != 1 && addend_rows != m)
     return fail(ctx, MQ_ERR_SHAPE, "addend must hold 1 or " + std::to_string(m) + " rows, not " +
                                        std::to_string(addend_rows));
-  const uint64_t addend_stride = addend && addend_rows == m && m > 1 ? w.rows : 0;
+  const uint64_t n = out_cols(w, flags);
+  const uint64_t addend_stride = addend && addend_rows == m && m > 1 ? n : 0;
   if (!addend) addend_rows = 0;
   const bool int8 = (flags & MQ_INT8_ACTIVATIONS) != 0;
-  if (m <= kGemvChunkRows || k < kGemmMinK) {
+  if (!output_major(w, flags)) {
+    // input-major (axpy): f32 activations whatever the int8 setting, as
+    // the reference's `packed_axpy` (src/native/mod.rs:154-194)
+    const int ks = mq::axpy_ksplit(k, n);
+    rc = acquire_workspace(ctx, stream, align256(static_cast<size_t>(ks) * 4 * n * sizeof(float)));
+    if (rc) return rc;
+    mq::launch_axpy(static_cast<int>(w.type), w.dev, w.nb, k, n, x, m, y, addend, addend_stride,
+                    static_cast<float*>(ctx->ws), ks, stream);
+  } else if (m <= kGemvChunkRows || k < kGemmMinK) {
     for (uint64_t r0 = 0; r0 < m; r0 += kGemvMaxRows) {
       const uint64_t mc = m - r0 < kGemvMaxRows ? m - r0 : kGemvMaxRows;
       const float* ad = addend ? addend + (addend_stride ? r0 * w.rows : 0) : nullptr;
@@ -332,6 +362,7 @@ void mq_destroy(mq_ctx* ctx) {
   if (ctx->io) (void)hipFree(ctx->io);
   if (ctx->sk) (void)hipFree(ctx->sk);
   if (ctx->attn) (void)hipFree(ctx->attn);
+  if (ctx->ids) (void)hipFree(ctx->ids);
   for (auto& kv : ctx->rope_tables) (void)hipFree(kv.second);
   (void)hipEventDestroy(ctx->ws_event);
   (void)hipStreamDestroy(ctx->stream);
@@ -350,8 +381,6 @@ int mq_weight_upload(mq_ctx* ctx, uint32_t gguf_type, uint64_t stored_rows, uint
   *handle = 0;
   if (!known_type(gguf_type))
     return fail(ctx, MQ_DECLINED, "packed weight format " + std::to_string(gguf_type) + " has no GPU path");
-  if (!transposed)
-    return fail(ctx, MQ_DECLINED, "packed weight stores input rows (untransposed): no GPU path");
   const int type = static_cast<int>(gguf_type);
   const uint64_t be = static_cast<uint64_t>(mq::block_values(type)), bb = static_cast<uint64_t>(mq::block_bytes_of(type));
   if (stored_rows == 0 || stored_cols == 0 || stored_cols % be != 0)
@@ -445,15 +474,17 @@ namespace {
 // context's stream, copy y back. Caller holds ctx->mu.
 int matmul_host_locked(mq_ctx* ctx, const Weight& w, const float* x, uint64_t m, uint64_t k, uint32_t flags,
                        const float* addend, uint64_t addend_rows, float* y) {
-  int rc = check_k(ctx, w, k);
+  if (flags & ~(MQ_INT8_ACTIVATIONS | MQ_TRANSPOSE_B)) return fail(ctx, MQ_ERR_ARGUMENT, "unknown matmul flag bits");
+  int rc = check_k(ctx, w, k, flags);
   if (rc) return rc;
+  const uint64_t n = out_cols(w, flags);
   if (m == 0) return MQ_OK;
   if (!x || !y) return fail(ctx, MQ_ERR_ARGUMENT, "mq_matmul: null host pointer");
   if (addend && addend_rows != 1 && addend_rows != m)
     return fail(ctx, MQ_ERR_SHAPE, "addend must hold 1 or " + std::to_string(m) + " rows, not " +
                                        std::to_string(addend_rows));
-  const uint64_t add_count = addend ? addend_rows * w.rows : 0;
-  const size_t xb = align256(m * k * sizeof(float)), yb = align256(m * w.rows * sizeof(float));
+  const uint64_t add_count = addend ? addend_rows * n : 0;
+  const size_t xb = align256(m * k * sizeof(float)), yb = align256(m * n * sizeof(float));
   const size_t ab = align256(add_count * sizeof(float));
   if (xb + yb + ab > ctx->io_bytes) {
     MQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
@@ -471,7 +502,7 @@ int matmul_host_locked(mq_ctx* ctx, const Weight& w, const float* x, uint64_t m,
   if (ad) MQ_HIP(ctx, hipMemcpyAsync(ad, addend, add_count * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
   rc = matmul_locked(ctx, w, xd, m, k, flags, yd, ctx->stream, ad, addend_rows);
   if (rc) return rc;
-  MQ_HIP(ctx, hipMemcpyAsync(y, yd, m * w.rows * sizeof(float), hipMemcpyDeviceToHost, ctx->stream));
+  MQ_HIP(ctx, hipMemcpyAsync(y, yd, m * n * sizeof(float), hipMemcpyDeviceToHost, ctx->stream));
   MQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
   return MQ_OK;
 }
@@ -529,7 +560,7 @@ int mq_matmul_prequantized_dev(mq_ctx* ctx, uint64_t handle, const int8_t* value
   std::lock_guard<std::mutex> lock(ctx->mu);
   const Weight* w = find_weight(ctx, handle);
   if (!w) return fail(ctx, MQ_ERR_ARGUMENT, "unknown weight handle " + std::to_string(handle));
-  int rc = check_k(ctx, *w, k);
+  int rc = check_k(ctx, *w, k, w->transposed ? 0u : MQ_TRANSPOSE_B);  // stored rows are the outputs
   if (rc) return rc;
   if (m > kGemvMaxRows) return fail(ctx, MQ_ERR_SHAPE, "prequantized matmul takes at most 8 activation rows");
   if (m == 0) return MQ_OK;
@@ -574,7 +605,7 @@ int mq_matmul_f16_dev(mq_ctx* ctx, uint64_t handle, const uint16_t* a16_dev, uin
   std::lock_guard<std::mutex> lock(ctx->mu);
   const Weight* w = find_weight(ctx, handle);
   if (!w) return fail(ctx, MQ_ERR_ARGUMENT, "unknown weight handle " + std::to_string(handle));
-  int rc = check_k(ctx, *w, k);
+  int rc = check_k(ctx, *w, k, w->transposed ? 0u : MQ_TRANSPOSE_B);  // stored rows are the outputs
   if (rc) return rc;
   if (m == 0) return MQ_OK;
   if (!a16_dev || !y_dev) return fail(ctx, MQ_ERR_ARGUMENT, "mq_matmul_f16_dev: null pointer");
@@ -625,6 +656,96 @@ int mq_dequantize(mq_ctx* ctx, uint64_t handle, int logical, float* out) {
   return MQ_OK;
 }
 
+
+// ---- embedding lookup ------------------------------------------------------------
+
+namespace {
+
+// Rust's `Display` of an f32 as the reference prints a token id: integral
+// values without a fraction, NaN and inf by name.
+std::string f32_text(float v) {
+  if (std::isnan(v)) return "NaN";
+  if (std::isinf(v)) return v > 0 ? "inf" : "-inf";
+  if (v == std::floor(v) && std::fabs(v) < 1e15f) return std::to_string(static_cast<long long>(v));
+  char buf[64];
+  for (int prec = 1; prec <= 9; ++prec) {  // the shortest text that reads back as v
+    std::snprintf(buf, sizeof buf, "%.*g", prec, static_cast<double>(v));
+    if (std::strtof(buf, nullptr) == v) break;
+  }
+  return buf;
+}
+
+// Validates the ids as the reference does (src/native/mod.rs:399-404) and
+// copies them to the device as u32. Caller holds ctx->mu.
+int stage_ids(mq_ctx* ctx, const Weight& w, const float* ids, uint64_t count, hipStream_t stream) {
+  const uint64_t vocab = w.transposed ? w.cols : w.rows;
+  std::vector<uint32_t> host(count);
+  for (uint64_t i = 0; i < count; ++i) {
+    const float raw = ids[i];
+    if (!(raw >= 0.0f) || raw != std::floor(raw) || static_cast<double>(raw) >= static_cast<double>(vocab))
+      return fail(ctx, MQ_ERR_SHAPE,
+                  "token id " + f32_text(raw) + " is not below the vocabulary size " + std::to_string(vocab));
+    host[i] = static_cast<uint32_t>(raw);
+  }
+  if (count > ctx->ids_cap) {
+    MQ_HIP(ctx, hipStreamSynchronize(stream));
+    if (ctx->ids) MQ_HIP(ctx, hipFree(ctx->ids));
+    ctx->ids = nullptr;
+    ctx->ids_cap = 0;
+    const size_t cap = count < 4096 ? 4096 : count;
+    MQ_HIP(ctx, hipMalloc(&ctx->ids, cap * sizeof(uint32_t)));
+    ctx->ids_cap = cap;
+  }
+  MQ_HIP(ctx, hipMemcpyAsync(ctx->ids, host.data(), count * sizeof(uint32_t), hipMemcpyHostToDevice, stream));
+  MQ_HIP(ctx, hipStreamSynchronize(stream));  // `host` is released on return
+  return MQ_OK;
+}
+
+}  // namespace
+
+int mq_embedding_dev(mq_ctx* ctx, uint64_t handle, const float* ids, uint64_t count, float scale, float* out_dev,
+                     void* stream) {
+  if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_embedding_dev: null context");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  const Weight* w = find_weight(ctx, handle);
+  if (!w) return fail(ctx, MQ_ERR_ARGUMENT, "unknown weight handle " + std::to_string(handle));
+  if (count == 0) return MQ_OK;
+  if (!ids || !out_dev) return fail(ctx, MQ_ERR_ARGUMENT, "mq_embedding_dev: null pointer");
+  DeviceGuard guard(ctx->device);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int rc = order_stream(ctx, s);
+  if (!rc) rc = stage_ids(ctx, *w, ids, count, s);
+  if (rc) return rc;
+  const uint64_t dim = w->transposed ? w->rows : w->cols;
+  mq::launch_embedding(static_cast<int>(w->type), w->dev, w->nb, w->transposed, ctx->ids, count, dim, scale,
+                       std::isnan(scale) ? 0 : 1, out_dev, s);
+  MQ_HIP(ctx, hipGetLastError());
+  return MQ_OK;
+}
+
+int mq_embedding(mq_ctx* ctx, uint64_t handle, const float* ids, uint64_t count, float scale, float* out) {
+  if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_embedding: null context");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  const Weight* w = find_weight(ctx, handle);
+  if (!w) return fail(ctx, MQ_ERR_ARGUMENT, "unknown weight handle " + std::to_string(handle));
+  if (count == 0) return MQ_OK;
+  if (!ids || !out) return fail(ctx, MQ_ERR_ARGUMENT, "mq_embedding: null pointer");
+  DeviceGuard guard(ctx->device);
+  int rc = order_stream(ctx, ctx->stream);
+  if (!rc) rc = stage_ids(ctx, *w, ids, count, ctx->stream);
+  if (rc) return rc;
+  const uint64_t dim = w->transposed ? w->rows : w->cols;
+  const size_t bytes = count * dim * sizeof(float);
+  rc = acquire_workspace(ctx, ctx->stream, bytes);
+  if (rc) return rc;
+  auto* dev = static_cast<float*>(ctx->ws);
+  mq::launch_embedding(static_cast<int>(w->type), w->dev, w->nb, w->transposed, ctx->ids, count, dim, scale,
+                       std::isnan(scale) ? 0 : 1, dev, ctx->stream);
+  MQ_HIP(ctx, hipGetLastError());
+  MQ_HIP(ctx, hipMemcpyAsync(out, dev, bytes, hipMemcpyDeviceToHost, ctx->stream));
+  MQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return MQ_OK;
+}
 
 // ---- decoder-layer operators ----------------------------------------------------
 

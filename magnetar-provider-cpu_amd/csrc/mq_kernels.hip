@@ -1561,6 +1561,152 @@ __global__ __launch_bounds__(512) void gemv_planes_f32_kernel(const uint8_t* __r
   finish_rows<M>(acc, mins, rows, y, addend, addend_stride, reinterpret_cast<float*>(lds), nullptr, nullptr, 1);
 }
 
+// ---------------------------------------------------------------------------
+// Run u of stored row `row` as f32 values, any format: value = scale * q -
+// min with the product and difference each rounded once, bit for bit the
+// reference's `RunReader::read` + `dequantize_row` arithmetic
+// (src/native/quant.rs:308-318, 1702-1711).
+// ---------------------------------------------------------------------------
+template <int TYPE>
+__device__ inline void row_run_values(const uint8_t* __restrict__ tiled, uint64_t nb, uint64_t row, uint64_t u,
+                                      float (&v)[32]) {
+  const uint64_t b = u >> 3;
+  const int j = static_cast<int>(u & 7), r = static_cast<int>(row & 7);
+  const uint8_t* tile = tiled + ((row >> 3) * nb + b) * tile_bytes(TYPE);
+  if constexpr (TYPE == kTypeQ4K) {
+    const uint8_t* t = tile + 16 * r;
+    const uint4 hdr = ld16(t);
+    const int c = j >> 1, shift = 4 * (j & 1);
+    const uint4 q0 = ld16(t + 128 * (1 + 2 * c)), q1 = ld16(t + 128 * (2 + 2 * c));
+    uint32_t sc, m;
+    q4k_sc_m(q4k_six_bit(hdr), j, sc, m);
+    const float scale = half_bits(hdr.x) * static_cast<float>(sc);
+    const float mn = half_bits(hdr.x >> 16) * static_cast<float>(m);
+    const uint32_t words[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      const float p = scale * static_cast<float>((byte_of(words[i >> 2], i & 3) >> shift) & 0xFu);
+      v[i] = p - mn;
+    }
+  } else if constexpr (TYPE == kTypeIq4Xs) {
+    const uint2 hdr = ld8(tile + 8 * r);
+    const uint4 qq = ld16(tile + 64 + 128 * j + 16 * r);
+    const float scale = half_bits(hdr.x) * static_cast<float>(iq4xs_ls(hdr, j));
+    const uint32_t words[4] = {qq.x, qq.y, qq.z, qq.w};
+#pragma unroll
+    for (int t4 = 0; t4 < 4; ++t4) {
+      const uint32_t lo = iq4_lookup4(words[t4] & 0x0F0F0F0Fu), hi = iq4_lookup4((words[t4] >> 4) & 0x0F0F0F0Fu);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[4 * t4 + e] = scale * static_cast<float>(static_cast<int8_t>(byte_of(lo, e)));
+        v[16 + 4 * t4 + e] = scale * static_cast<float>(static_cast<int8_t>(byte_of(hi, e)));
+      }
+    }
+  } else {
+    constexpr int P = plane_count(TYPE);
+    auto planes = [&](int p) { return ld16(tile + 128 * p + 16 * r); };
+    const uint32_t d_bits =
+        plane_shared_d(TYPE) ? static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(tile + 128 * P + 2 * r)) : 0u;
+    uint32_t q[8];
+    float scale[2], mn[2];
+    plane_run_signed<TYPE>(planes, d_bits, j, q, scale, mn);
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      const float p = scale[i >> 4] * static_cast<float>(static_cast<int8_t>(byte_of(q[i >> 2], i & 3)));
+      v[i] = p - mn[i >> 4];
+    }
+  }
+}
+
+// Embedding of an untransposed packed table (src/native/mod.rs:389-417):
+// thread per (token, run), the token's stored row decoded run by run, times
+// `scale` when `scaled` (the Kernel's `scale` attribute).
+template <int TYPE>
+__global__ void embed_rows_kernel(const uint8_t* __restrict__ tiled, uint64_t nb, const uint32_t* __restrict__ ids,
+                                  uint64_t count, uint64_t dim, float scale, int scaled, float* __restrict__ out) {
+  const uint64_t runs = dim / 32;
+  const uint64_t t = blockIdx.x * static_cast<uint64_t>(blockDim.x) + threadIdx.x;
+  if (t >= count * runs) return;
+  const uint64_t tok = t / runs, u = t % runs;
+  float v[32];
+  row_run_values<TYPE>(tiled, nb, ids[tok], u, v);
+  float4* o = reinterpret_cast<float4*>(out + tok * dim + 32 * u);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float4 q = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+    if (scaled) q = make_float4(q.x * scale, q.y * scale, q.z * scale, q.w * scale);
+    o[i] = q;
+  }
+}
+
+// Embedding of a transposed table (stored [dim][vocab]): the token's value
+// in every stored row (`quant::element`, src/native/quant.rs:1690-1698).
+template <int TYPE>
+__global__ void embed_columns_kernel(const uint8_t* __restrict__ tiled, uint64_t nb, const uint32_t* __restrict__ ids,
+                                     uint64_t count, uint64_t dim, float scale, int scaled, float* __restrict__ out) {
+  const uint64_t t = blockIdx.x * static_cast<uint64_t>(blockDim.x) + threadIdx.x;
+  if (t >= count * dim) return;
+  const uint64_t tok = t / dim, j = t % dim;
+  const uint32_t id = ids[tok];
+  float v[32];
+  row_run_values<TYPE>(tiled, nb, j, id >> 5, v);
+  float x = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) x = (static_cast<int>(id & 31) == i) ? v[i] : x;
+  out[tok * dim + j] = scaled ? x * scale : x;
+}
+
+// Input-major (axpy) product (src/native/quant.rs:1652-1688): the stored
+// rows are the K input rows, each holding N output columns. Thread per (run
+// of 32 columns, half); work-group column y = a K-split; each row j adds
+// x[r][j] * value for every row r whose x[r][j] is not zero (the reference
+// skips zero activations), f32 multiply then add. Partials [ks][MM][N].
+template <int TYPE, int MM>
+__global__ __launch_bounds__(256) void axpy_kernel(const uint8_t* __restrict__ tiled, uint64_t nb, uint64_t K,
+                                                   uint64_t N, const float* __restrict__ x, int rows, uint64_t kchunk,
+                                                   float* __restrict__ part) {
+  const uint64_t t = blockIdx.x * static_cast<uint64_t>(blockDim.x) + threadIdx.x;
+  const uint64_t u = t >> 1;
+  const int h = static_cast<int>(t & 1);
+  if (u >= N / 32) return;
+  const uint64_t ks = blockIdx.y, j0 = ks * kchunk, j1 = j0 + kchunk < K ? j0 + kchunk : K;
+  float acc[MM][16];
+#pragma unroll
+  for (int m = 0; m < MM; ++m)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[m][i] = 0.0f;
+  for (uint64_t j = j0; j < j1; ++j) {
+    float v[32];
+    row_run_values<TYPE>(tiled, nb, j, u, v);
+#pragma unroll
+    for (int m = 0; m < MM; ++m) {
+      const float xv = m < rows ? x[m * K + j] : 0.0f;
+      if (xv != 0.0f) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[m][i] += xv * (h ? v[16 + i] : v[i]);
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < MM; ++m) {
+    float4* o = reinterpret_cast<float4*>(part + (ks * MM + m) * N + 32 * u + 16 * h);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = make_float4(acc[m][4 * i], acc[m][4 * i + 1], acc[m][4 * i + 2], acc[m][4 * i + 3]);
+  }
+}
+
+// y[r][n] = sum over the K-splits in split order [+ addend].
+__global__ void axpy_finish_kernel(const float* __restrict__ part, int ks, int mm, int rows, uint64_t N,
+                                   float* __restrict__ y, const float* __restrict__ addend, uint64_t addend_stride) {
+  const uint64_t t = blockIdx.x * static_cast<uint64_t>(blockDim.x) + threadIdx.x;
+  if (t >= static_cast<uint64_t>(rows) * N) return;
+  const uint64_t r = t / N, n = t % N;
+  float s = part[r * N + n];
+  for (int i = 1; i < ks; ++i) s += part[(static_cast<uint64_t>(i) * mm + r) * N + n];
+  if (addend) s = s + addend[r * addend_stride + n];
+  y[r * N + n] = s;
+}
+
 // f32 activations: per run half, sum(q * x) and sum(x) in f32, then
 // acc += scale * sum(q x) - min * sum(x).
 __device__ inline float4 ldf4(const float* p) { return *reinterpret_cast<const float4*>(p); }
@@ -2278,6 +2424,63 @@ bool launch_gemv_fused(int type, const uint8_t* tiled, uint64_t rows, uint64_t n
   launch_gemv_lds<true>(type, tiled, rows, nb, nullptr, nullptr, nullptr, x, m, y, addend, addend_stride,
                         lds_splits, sk, lds, stream);
   return true;
+}
+
+// ---- embedding and input-major products (any format) --------------------------
+
+#define MQ_ALL_TYPES(X) X(kTypeQ4K) X(kTypeIq4Xs) X(kTypeQ8_0) X(kTypeQ4_0) X(kTypeIq4Nl) X(kTypeQ5K) X(kTypeQ6K)
+
+void launch_embedding(int type, const uint8_t* tiled, uint64_t nb, int transposed, const uint32_t* ids,
+                      uint64_t count, uint64_t dim, float scale, int scaled, float* out, hipStream_t stream) {
+  const uint64_t threads = transposed ? count * dim : count * (dim / 32);
+  switch (type) {
+#define X(T)                                                                                                       \
+  case T:                                                                                                          \
+    if (transposed)                                                                                                \
+      hipLaunchKernelGGL(embed_columns_kernel<T>, dim3(grid_for(threads, 256)), dim3(256), 0, stream, tiled, nb,   \
+                         ids, count, dim, scale, scaled, out);                                                     \
+    else                                                                                                           \
+      hipLaunchKernelGGL(embed_rows_kernel<T>, dim3(grid_for(threads, 256)), dim3(256), 0, stream, tiled, nb, ids, \
+                         count, dim, scale, scaled, out);                                                          \
+    break;
+    MQ_ALL_TYPES(X)
+#undef X
+    default:
+      break;
+  }
+}
+
+int axpy_ksplit(uint64_t k, uint64_t n) {
+  // about 64K threads in flight: (n / 16) per split
+  const uint64_t per = n / 16 ? n / 16 : 1;
+  uint64_t ks = (65536 + per - 1) / per;
+  if (ks > k) ks = k;
+  if (ks > 256) ks = 256;
+  return static_cast<int>(ks < 1 ? 1 : ks);
+}
+
+void launch_axpy(int type, const uint8_t* tiled, uint64_t nb, uint64_t k, uint64_t n, const float* x, uint64_t m,
+                 float* y, const float* addend, uint64_t addend_stride, float* part, int ks, hipStream_t stream) {
+  constexpr int MM = 4;
+  const uint64_t kchunk = (k + ks - 1) / ks;
+  dim3 grid(grid_for(n / 16, 256), static_cast<unsigned>(ks));
+  for (uint64_t r0 = 0; r0 < m; r0 += MM) {
+    const int rows = static_cast<int>(m - r0 < MM ? m - r0 : MM);
+    switch (type) {
+#define X(T)                                                                                                        \
+  case T:                                                                                                           \
+    hipLaunchKernelGGL((axpy_kernel<T, MM>), grid, dim3(256), 0, stream, tiled, nb, k, n, x + r0 * k, rows, kchunk, \
+                       part);                                                                                       \
+    break;
+      MQ_ALL_TYPES(X)
+#undef X
+      default:
+        break;
+    }
+    hipLaunchKernelGGL(axpy_finish_kernel, dim3(grid_for(rows * n, 256)), dim3(256), 0, stream, part, ks, MM, rows, n,
+                       y + r0 * n, addend ? addend + (addend_stride ? r0 * addend_stride : 0) : nullptr,
+                       addend_stride);
+  }
 }
 
 // ---- plane formats ----------------------------------------------------------

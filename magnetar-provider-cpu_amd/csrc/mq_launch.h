@@ -91,6 +91,20 @@ void launch_gemv_planes_f32(int type, const uint8_t* tiled, uint64_t rows, uint6
                             const float* x, uint64_t m, float* y, const float* addend, uint64_t addend_stride,
                             int splits, hipStream_t stream);
 
+// Embedding lookup of `count` token ids (validated, on the device) in a
+// packed table of any format: stored rows are the tokens (transposed == 0,
+// out[t] = row ids[t]) or the `dim` stored rows hold every token's value
+// (transposed != 0). out[count][dim] times `scale` when `scaled`.
+void launch_embedding(int type, const uint8_t* tiled, uint64_t nb, int transposed, const uint32_t* ids,
+                      uint64_t count, uint64_t dim, float scale, int scaled, float* out, hipStream_t stream);
+
+// Input-major product y[m][n] = x[m][k] . W, W's k stored rows the input
+// rows (any format, f32 activations), K-split `ks` ways through `part`
+// (ks * 4 * n floats); the splits are added in order [+ addend].
+int axpy_ksplit(uint64_t k, uint64_t n);
+void launch_axpy(int type, const uint8_t* tiled, uint64_t nb, uint64_t k, uint64_t n, const float* x, uint64_t m,
+                 float* y, const float* addend, uint64_t addend_stride, float* part, int ks, hipStream_t stream);
+
 // Grid-shape helper for the GEMV (waves per work-group).
 int gemv_default_splits(uint64_t rows, uint64_t nb, uint64_t m, int variant);
 

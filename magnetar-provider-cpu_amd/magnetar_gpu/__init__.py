@@ -38,6 +38,7 @@ ERR_HIP = 4
 ERR_OOM = 5
 ERR_ARGUMENT = 6
 INT8_ACTIVATIONS = 1
+TRANSPOSE_B = 2
 
 _u8p = ctypes.POINTER(ctypes.c_uint8)
 _f32p = ctypes.POINTER(ctypes.c_float)
@@ -90,6 +91,8 @@ def gpu_lib():
         L.mq_matmul_f16_dev.argtypes = [_vp, _u64, _vp, _u64, _u64, _vp, _vp]
         L.mq_dequantize.argtypes = [_vp, _u64, ctypes.c_int, _f32p]
         L.mq_dequantize_dev.argtypes = [_vp, _u64, ctypes.c_int, _vp, _vp]
+        L.mq_embedding.argtypes = [_vp, _u64, _f32p, _u64, ctypes.c_float, _f32p]
+        L.mq_embedding_dev.argtypes = [_vp, _u64, _f32p, _u64, ctypes.c_float, _vp, _vp]
         L.mq_matmul_add_dev.argtypes = [_vp, _u64, _vp, _u64, _u64, ctypes.c_uint32, _vp, _u64, _vp, _vp]
         f32 = ctypes.c_float
         L.mq_rmsnorm_dev.argtypes = [_vp, _vp, _u64, _u64, _vp, _u64, f32, _vp, _vp]
@@ -217,20 +220,39 @@ class Context:
         return {"type": t.value, "stored_rows": r.value, "stored_cols": c.value,
                 "transposed": tr.value, "device_bytes": nbytes.value}
 
-    def matmul(self, weight, x, int8=True):
-        """y = x . W^T on host arrays (synchronous)."""
+    def matmul(self, weight, x, int8=True, transpose_b=False):
+        """x . W on host arrays (synchronous), W the logical weight read as
+        the reference reads it: the stored rows are the outputs when
+        weight.transposed != transpose_b, else the input rows (axpy)."""
         x = np.ascontiguousarray(x, dtype=np.float32)
         if x.ndim != 2:
             raise ValueError("x must be [m, k]")
         m, k = x.shape
-        y = np.empty((m, weight.stored_rows), np.float32)
-        self._check(gpu_lib().mq_matmul(self.ptr, weight.handle, _p(x, ctypes.c_float), m, k,
-                                        INT8_ACTIVATIONS if int8 else 0, _p(y, ctypes.c_float)))
+        n = weight.stored_rows if bool(weight.transposed) != bool(transpose_b) else weight.stored_cols
+        y = np.empty((m, n), np.float32)
+        flags = (INT8_ACTIVATIONS if int8 else 0) | (TRANSPOSE_B if transpose_b else 0)
+        self._check(gpu_lib().mq_matmul(self.ptr, weight.handle, _p(x, ctypes.c_float), m, k, flags,
+                                        _p(y, ctypes.c_float)))
         return y
 
-    def matmul_dev(self, weight, x_ptr, m, k, y_ptr, int8=True, stream=None):
-        self._check(gpu_lib().mq_matmul_dev(self.ptr, weight.handle, x_ptr, m, k,
-                                            INT8_ACTIVATIONS if int8 else 0, y_ptr, stream))
+    def matmul_dev(self, weight, x_ptr, m, k, y_ptr, int8=True, stream=None, transpose_b=False):
+        flags = (INT8_ACTIVATIONS if int8 else 0) | (TRANSPOSE_B if transpose_b else 0)
+        self._check(gpu_lib().mq_matmul_dev(self.ptr, weight.handle, x_ptr, m, k, flags, y_ptr, stream))
+
+    def embedding(self, weight, ids, scale=None):
+        """The `embedding` Kernel on a packed table: [len(ids), dim]."""
+        ids = np.ascontiguousarray(ids, dtype=np.float32).reshape(-1)
+        dim = weight.logical_shape[1]
+        out = np.empty((ids.size, dim), np.float32)
+        self._check(gpu_lib().mq_embedding(self.ptr, weight.handle, _p(ids, ctypes.c_float), ids.size,
+                                           float("nan") if scale is None else float(scale),
+                                           _p(out, ctypes.c_float)))
+        return out
+
+    def embedding_dev(self, weight, ids, out_ptr, scale=None, stream=None):
+        ids = np.ascontiguousarray(ids, dtype=np.float32).reshape(-1)
+        self._check(gpu_lib().mq_embedding_dev(self.ptr, weight.handle, _p(ids, ctypes.c_float), ids.size,
+                                               float("nan") if scale is None else float(scale), out_ptr, stream))
 
     def quantize_activations_dev(self, x_ptr, m, k, values_ptr, scales_ptr, sums_ptr, stream=None):
         self._check(gpu_lib().mq_quantize_activations_dev(self.ptr, x_ptr, m, k, values_ptr, scales_ptr,

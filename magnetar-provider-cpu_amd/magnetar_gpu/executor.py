@@ -60,6 +60,8 @@ def lib():
         L.mg_kernel_advertisement_json.restype = ctypes.c_char_p
         L.mg_materialization_count.argtypes = [vp]
         L.mg_materialization_count.restype = u64
+        L.mg_memory_used.argtypes = [vp]
+        L.mg_memory_used.restype = u64
         _lib = L
     return _lib
 
@@ -198,3 +200,6 @@ class GpuExecutor:
 
     def materializations(self):
         return int(lib().mg_materialization_count(self.ptr))
+
+    def memory_used(self):
+        return int(lib().mg_memory_used(self.ptr))

@@ -3,6 +3,14 @@ import sys
 
 import pytest
 
+# torch first: its bundled HIP runtime must be the process's one before
+# libmagnetar_gpu.so (linked against the same soname) is loaded, or torch
+# later finds no device
+try:
+    import torch  # noqa: F401
+except ImportError:
+    pass
+
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 PKG = os.path.join(ROOT, "magnetar-provider-cpu_amd")
 for p in (ROOT, PKG, os.path.dirname(os.path.abspath(__file__))):

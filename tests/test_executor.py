@@ -7,7 +7,8 @@ import pytest
 
 import magnetar_gpu as mg
 import oracle
-from helpers import IQ4_XS, Q4_K, activations, assert_close_reference, assert_row_tolerance, packed
+from helpers import (IQ4_XS, PLANE_FORMATS, Q4_K, Q8_0, activations, assert_close_reference, assert_row_tolerance,
+                     packed)
 from magnetar_gpu import executor as ex
 
 
@@ -70,9 +71,11 @@ def test_executor_stores_packed_weights(executor):
         assert not declining.write_packed_weight_tensor("w", Q4_K, 4, 256, w)
     finally:
         declining.close()
-    # formats without a GPU path and input-major weights are declined too
-    assert not executor.write_packed_weight_tensor("q8", 8, 2, 32, np.zeros(2 * 34, np.uint8))
-    assert not executor.write_packed_weight_tensor("t", Q4_K, 4, 256, w, transposed=False)
+    # a format without a GPU path (Q2_K) is declined; an untransposed
+    # weight is stored with its logical shape [stored_rows, stored_cols]
+    assert not executor.write_packed_weight_tensor("q2", 10, 2, 256, np.zeros(2 * 84, np.uint8))
+    assert executor.write_packed_weight_tensor("t", Q4_K, 4, 256, w, transposed=False)
+    assert executor.resident_shape("t") == [4, 256]
 
 
 @gpu
@@ -87,9 +90,10 @@ def test_packed_weights_yield_to_f32_writes_and_admission(executor):
     executor.write_tensor_admitted("w", replacement)
     assert not executor.is_packed("w")
     np.testing.assert_array_equal(executor.read_tensor("w"), replacement)
-    small = ex.GpuExecutor(0, memory_capacity=1024)
+    small = ex.GpuExecutor(0, memory_capacity=1500)  # the weight's 1152 device bytes, not 2048 f32 ones
     try:
         assert small.write_packed_weight_tensor("w", Q4_K, 2, 256, w)
+        assert small.memory_used() == 1152
         with pytest.raises(ex.ExecutorError) as e:
             small.write_tensor_admitted("w", replacement)
         assert e.value.code == ex.MEMORY_DENIED
@@ -191,10 +195,10 @@ def test_kernel_errors_and_single_completion(executor):
 
 @gpu
 def test_output_admission_denial_does_not_store(executor):
-    small = ex.GpuExecutor(0, memory_capacity=16)
+    small = ex.GpuExecutor(0, memory_capacity=1160)  # the weight's 1152 device bytes, not the 32-byte output
     try:
         w = packed(Q4_K, 8, 256, 1)
-        small.write_packed_weight_tensor("w", Q4_K, 8, 256, w)
+        assert small.write_packed_weight_tensor("w", Q4_K, 8, 256, w)
         small.write_tensor("a", activations(1, 256, 1))
         r = small.complete_kernel(small.submit_kernel("matmul", "big", ["a", "w"], "y"))
         assert r.error == ex.KERNEL_EXECUTION_FAILED and "admission denied" in r.reason
@@ -202,3 +206,78 @@ def test_output_admission_denial_does_not_store(executor):
         assert ("KernelMemoryFeasibilityFailed", "matmul") in small.observations()
     finally:
         small.close()
+
+
+@gpu
+def test_packed_weight_device_bytes_are_admitted(executor):
+    """A packed upload the memory ledger cannot hold is declined and leaves
+    the previous weight of the id resident; releases return the bytes."""
+    small = ex.GpuExecutor(0, memory_capacity=3000)
+    try:
+        w1 = packed(Q4_K, 8, 256, 2)
+        assert small.write_packed_weight_tensor("w", Q4_K, 8, 256, w1)
+        assert small.memory_used() == 1152
+        big = packed(Q4_K, 24, 256, 3)  # 3 row groups: 3456 device bytes
+        assert not small.write_packed_weight_tensor("w", Q4_K, 24, 256, big)
+        assert small.is_packed("w") and small.resident_shape("w") == [256, 8]
+        assert small.release_tensor("w")
+        assert small.memory_used() == 0
+    finally:
+        small.close()
+
+
+@gpu
+@pytest.mark.parametrize("fmt", [Q8_0, Q4_K])
+def test_embedding_kernel_on_packed_tables(executor, fmt):
+    """`packed_tables_serve_lookups_and_tied_heads` (src/native/tests.rs:178-191)
+    through Kernels: an untransposed packed table [50, 64] serves `embedding`
+    (bit-exact rows, the `scale` attribute) and, read transposed, a tied
+    output head; a transposed table [dim, vocab] gathers each token's column."""
+    cols = 64 if fmt == Q8_0 else 256
+    table = packed(fmt, 50, cols, 31)
+    dense = oracle.dequantize(fmt, table, 50, cols)  # logical [vocab, dim]
+    assert executor.write_packed_weight_tensor("tab", fmt, 50, cols, table, transposed=False)
+    executor.write_tensor("ids", np.array([7, 0, 49, 7], np.float32))
+    r = executor.complete_kernel(executor.submit_kernel("embedding", "e", ["tab", "ids"], "rows"))
+    assert r.succeeded, r.reason
+    np.testing.assert_array_equal(executor.read_tensor("rows"), dense[[7, 0, 49, 7]])
+    r = executor.complete_kernel(executor.submit_kernel("embedding", "e2", ["tab", "ids"], "rows", {"scale": "0.5"}))
+    assert r.succeeded, r.reason
+    np.testing.assert_array_equal(executor.read_tensor("rows"), dense[[7, 0, 49, 7]] * np.float32(0.5))
+    executor.write_tensor("bad", np.array([50], np.float32))
+    r = executor.complete_kernel(executor.submit_kernel("embedding", "e3", ["tab", "bad"], "rows"))
+    assert r.error == ex.KERNEL_EXECUTION_FAILED
+    assert r.reason == "token id 50 is not below the vocabulary size 50"
+    # tied head: the untransposed table read transposed multiplies output-major
+    a = activations(2, cols, 3)
+    executor.write_tensor("h", a)
+    r = executor.complete_kernel(executor.submit_kernel("matmul", "head", ["h", "tab"], "logits",
+                                                        {"transpose_b": "true"}))
+    assert r.succeeded, r.reason
+    exp = oracle.matmul_dense(oracle.int8_rounded(a), dense, False, True)
+    assert_close_reference(executor.read_tensor("logits"), exp, "tied head")
+    # a transposed table: stored [dim][vocab]
+    tt = packed(fmt, 40, cols, 33)
+    dense_t = oracle.dequantize(fmt, tt, 40, cols)  # stored rows = dim
+    assert executor.write_packed_weight_tensor("tt", fmt, 40, cols, tt, transposed=True)
+    executor.write_tensor("ids2", np.array([3, 63], np.float32))
+    r = executor.complete_kernel(executor.submit_kernel("embedding", "e4", ["tt", "ids2"], "cols"))
+    assert r.succeeded, r.reason
+    np.testing.assert_array_equal(executor.read_tensor("cols"), dense_t[:, [3, 63]].T)
+
+
+@gpu
+@pytest.mark.parametrize("fmt", PLANE_FORMATS + [Q4_K, IQ4_XS])
+def test_input_major_weights_multiply_packed(executor, fmt):
+    """`input_major_weights_multiply_packed` (src/native/tests.rs:193-209):
+    an untransposed [64, 256] weight read without transpose_b multiplies
+    through the axpy product, f32 activations, every format."""
+    w = packed(fmt, 64, 256, 61)
+    dense = oracle.dequantize(fmt, w, 64, 256)  # logical [k, n]
+    assert executor.write_packed_weight_tensor("w", fmt, 64, 256, w, transposed=False)
+    for m in (1, 4, 9):
+        a = activations(m, 64, 62)
+        executor.write_tensor("a", a)
+        r = executor.complete_kernel(executor.submit_kernel("matmul", f"ax{m}", ["a", "w"], "y"))
+        assert r.succeeded, r.reason
+        assert_close_reference(executor.read_tensor("y"), oracle.matmul_dense(a, dense), f"m {m}")

@@ -294,8 +294,6 @@ def test_boundary_errors_and_declines(ctx):
     w = packed(Q4_K, 4, 256, 41)
     with pytest.raises(mg.Declined):
         ctx.upload(10, 4, 256, np.zeros(4 * 84, np.uint8))  # Q2_K has no GPU path
-    with pytest.raises(mg.Declined):
-        ctx.upload(Q4_K, 4, 256, w, transposed=False)
     with pytest.raises(mg.GpuError) as e:
         ctx.upload(Q4_K, 4, 256, w[:, :100])
     assert e.value.code == mg.ERR_SHAPE
