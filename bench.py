@@ -284,29 +284,32 @@ def iq4xs_part(ctx, torch, workloads, args, per_graph, use_graph, extra):
 
 def layer_part(ctx, torch, per_graph, use_graph, extra):
     # ---- one Llama-3-8B-shaped decoder layer decode step (seed 4) ----------------
+    # fused: 6 launches (mq_decode_matmul_dev); unfused: each operator's own
+    # entry point, 12 launches
     from magnetar_gpu import decoder
 
     data = decoder.LayerData(seed=4)
-    layer = decoder.DecoderLayer(ctx, torch, data)
     position = data.prefilled  # the token after the 4095 cached ones
-
-    def step(i, stream):
-        layer.step(position, stream=stream)
-
-    per = max(10, per_graph // 10)
-    r = GraphRunner(torch, step, per, use_graph)
-    r.time(per)
-    calls = 10 * per
-    t = r.time(calls) / calls
     kv_bytes = 2 * (position + 1) * decoder.KV_HEADS * decoder.HEAD_DIM * 4
     hbm = data.weight_bytes() + kv_bytes
-    extra["layer_decode_step_us"] = round(t * 1e6, 2)
+    for fused, key in ((True, "layer_decode_step"), (False, "layer_decode_step_unfused")):
+        layer = decoder.DecoderLayer(ctx, torch, data, fused=fused)
+
+        def step(i, stream, layer=layer):
+            layer.step(position, stream=stream)
+
+        per = max(10, per_graph // 10)
+        r = GraphRunner(torch, step, per, use_graph)
+        r.time(per)
+        calls = 10 * per
+        t = r.time(calls) / calls
+        extra[f"{key}_us"] = round(t * 1e6, 2)
+        extra[f"{key}_GBps"] = round(hbm / t / 1e9, 1)
+        extra[f"{key}_frac_hbm"] = round(hbm / t / 1e9 / HBM_PEAK_GBS, 4)
+        log(f"decoder layer decode step ({'fused, 6' if fused else 'unfused, 12'} launches): {t * 1e6:.1f} us, "
+            f"{hbm} HBM bytes (Q4_K weights {data.weight_bytes()} + f32 K/V {kv_bytes}), {hbm / t / 1e9:.1f} GB/s")
+        layer.release()
     extra["layer_decode_step_bytes"] = hbm
-    extra["layer_decode_step_GBps"] = round(hbm / t / 1e9, 1)
-    extra["layer_decode_step_frac_hbm"] = round(hbm / t / 1e9 / HBM_PEAK_GBS, 4)
-    log(f"decoder layer decode step: {t * 1e6:.1f} us, {hbm} HBM bytes (Q4_K weights {data.weight_bytes()} + "
-        f"f32 K/V {kv_bytes}), {hbm / t / 1e9:.1f} GB/s")
-    layer.release()
 
 
 def formats_part(ctx, torch, per_graph, use_graph, extra):

@@ -243,6 +243,45 @@ int mq_silu_mul_dev(mq_ctx *ctx, const float *gate_dev, const float *up_dev, uin
 int mq_add_dev(mq_ctx *ctx, const float *a_dev, uint64_t n, const float *b_dev, uint64_t b_n,
                float *out_dev, void *stream);
 
+/* ---- Decode-step fusions ------------------------------------------------------
+ * No counterpart in the reference: one launch for a chain of its operators
+ * in a one-token decode step, for callers that keep the step on the device.
+ * Each part computes what the separate entry points compute (the same
+ * operators, rounded the same way; the rmsnorm's sum of squares is added
+ * in another tree order). */
+
+#define MQ_EPILOGUE_NONE 0u
+#define MQ_EPILOGUE_ROPE_KV 1u    /* rope rows, route rows to Q / K-row / V-row outputs */
+#define MQ_EPILOGUE_SILU_PAIRS 2u /* silu(gate) * up of interleaved gate / up rows */
+
+typedef struct {
+  /* non-NULL: x is first rmsnorm'd with this [k] weight and norm_epsilon
+   * (mq_rmsnorm_dev with w_rows 1) */
+  const float *norm_weight;
+  float norm_epsilon;
+  uint32_t epilogue;
+  /* MQ_EPILOGUE_ROPE_KV: output rows [0, rope_rows) are rotated in
+   * interleaved pairs, heads of rope_dim, at position rope_offset with
+   * rope_base / rope_scale (mq_rope_dev, MQ_ROPE_INTERLEAVED); then rows
+   * [seg_begin[i], seg_begin[i + 1]) are written to seg_out[i] (seg_begin[0]
+   * = 0, the last segment ends at stored_rows): e.g. Q, the K cache's row,
+   * the V cache's row (mq_kv_write_dev). y_dev is unused. */
+  uint64_t rope_rows, rope_dim, rope_offset;
+  float rope_base, rope_scale;
+  uint64_t seg_begin[3];
+  float *seg_out[3];
+} mq_decode_fusion;
+
+/* One activation row, int8 activations: y = [rmsnorm](x) . W^T with the
+ * epilogue. MQ_EPILOGUE_SILU_PAIRS takes a weight whose stored rows
+ * interleave gate and up rows in blocks of 32 (block 2i: gate rows 32i..,
+ * block 2i + 1: up rows 32i..; stored_rows a multiple of 64) and writes
+ * y[j] = silu(gate_j) * up_j, stored_rows / 2 values (mq_silu_mul_dev).
+ * Q4_K and IQ4_XS weights; others, or a row too long for the kernel's LDS
+ * staging, return MQ_DECLINED. */
+int mq_decode_matmul_dev(mq_ctx *ctx, uint64_t handle, const float *x_dev, uint64_t k,
+                         const mq_decode_fusion *fusion, float *y_dev, void *stream);
+
 /* Library version string. */
 const char *mq_version(void);
 

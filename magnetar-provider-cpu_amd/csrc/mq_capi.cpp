@@ -320,6 +320,71 @@ int matmul_locked(mq_ctx* ctx, const Weight& w, const float* x, uint64_t m, uint
   return MQ_OK;
 }
 
+// The frequency table base^(-2p / dimension), p < dimension / 2, cached per
+// (base, dimension) on the device. Caller holds ctx->mu.
+int rope_table(mq_ctx* ctx, float base, uint64_t dimension, const float** out) {
+  uint32_t base_bits;
+  std::memcpy(&base_bits, &base, sizeof base_bits);
+  const auto key = std::make_pair(base_bits, dimension);
+  auto it = ctx->rope_tables.find(key);
+  if (it == ctx->rope_tables.end()) {
+    // the reference's table: base.powf(-2.0 * (pair as f32) / dimension as f32), in f32
+    std::vector<float> table(dimension / 2);
+    for (uint64_t p = 0; p < dimension / 2; ++p)
+      table[p] = std::pow(base, -2.0f * static_cast<float>(p) / static_cast<float>(dimension));
+    float* dev = nullptr;
+    MQ_HIP(ctx, hipMalloc(&dev, table.size() * sizeof(float)));
+    hipError_t e = hipMemcpy(dev, table.data(), table.size() * sizeof(float), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+      (void)hipFree(dev);
+      return hip_fail(ctx, e, "hipMemcpy(rope table)");
+    }
+    it = ctx->rope_tables.emplace(key, dev).first;
+  }
+  *out = it->second;
+  return MQ_OK;
+}
+
+// Rust's `Display` of an f32 as the reference prints a token id: integral
+// values without a fraction, NaN and inf by name.
+std::string f32_text(float v) {
+  if (std::isnan(v)) return "NaN";
+  if (std::isinf(v)) return v > 0 ? "inf" : "-inf";
+  if (v == std::floor(v) && std::fabs(v) < 1e15f) return std::to_string(static_cast<long long>(v));
+  char buf[64];
+  for (int prec = 1; prec <= 9; ++prec) {  // the shortest text that reads back as v
+    std::snprintf(buf, sizeof buf, "%.*g", prec, static_cast<double>(v));
+    if (std::strtof(buf, nullptr) == v) break;
+  }
+  return buf;
+}
+
+// Validates the ids as the reference does (src/native/mod.rs:399-404) and
+// copies them to the device as u32. Caller holds ctx->mu.
+int stage_ids(mq_ctx* ctx, const Weight& w, const float* ids, uint64_t count, hipStream_t stream) {
+  const uint64_t vocab = w.transposed ? w.cols : w.rows;
+  std::vector<uint32_t> host(count);
+  for (uint64_t i = 0; i < count; ++i) {
+    const float raw = ids[i];
+    if (!(raw >= 0.0f) || raw != std::floor(raw) || static_cast<double>(raw) >= static_cast<double>(vocab))
+      return fail(ctx, MQ_ERR_SHAPE,
+                  "token id " + f32_text(raw) + " is not below the vocabulary size " + std::to_string(vocab));
+    host[i] = static_cast<uint32_t>(raw);
+  }
+  if (count > ctx->ids_cap) {
+    MQ_HIP(ctx, hipStreamSynchronize(stream));
+    if (ctx->ids) MQ_HIP(ctx, hipFree(ctx->ids));
+    ctx->ids = nullptr;
+    ctx->ids_cap = 0;
+    const size_t cap = count < 4096 ? 4096 : count;
+    MQ_HIP(ctx, hipMalloc(&ctx->ids, cap * sizeof(uint32_t)));
+    ctx->ids_cap = cap;
+  }
+  MQ_HIP(ctx, hipMemcpyAsync(ctx->ids, host.data(), count * sizeof(uint32_t), hipMemcpyHostToDevice, stream));
+  MQ_HIP(ctx, hipStreamSynchronize(stream));  // `host` is released on return
+  return MQ_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -657,51 +722,71 @@ int mq_dequantize(mq_ctx* ctx, uint64_t handle, int logical, float* out) {
 }
 
 
-// ---- embedding lookup ------------------------------------------------------------
+// ---- decode-step fusions ----------------------------------------------------------
 
-namespace {
-
-// Rust's `Display` of an f32 as the reference prints a token id: integral
-// values without a fraction, NaN and inf by name.
-std::string f32_text(float v) {
-  if (std::isnan(v)) return "NaN";
-  if (std::isinf(v)) return v > 0 ? "inf" : "-inf";
-  if (v == std::floor(v) && std::fabs(v) < 1e15f) return std::to_string(static_cast<long long>(v));
-  char buf[64];
-  for (int prec = 1; prec <= 9; ++prec) {  // the shortest text that reads back as v
-    std::snprintf(buf, sizeof buf, "%.*g", prec, static_cast<double>(v));
-    if (std::strtof(buf, nullptr) == v) break;
+int mq_decode_matmul_dev(mq_ctx* ctx, uint64_t handle, const float* x_dev, uint64_t k, const mq_decode_fusion* f,
+                         float* y_dev, void* stream) {
+  if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_decode_matmul_dev: null context");
+  if (!f || !x_dev) return fail(ctx, MQ_ERR_ARGUMENT, "mq_decode_matmul_dev: null argument");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  const Weight* w = find_weight(ctx, handle);
+  if (!w) return fail(ctx, MQ_ERR_ARGUMENT, "unknown weight handle " + std::to_string(handle));
+  const uint32_t orient = w->transposed ? 0u : MQ_TRANSPOSE_B;  // stored rows are the outputs
+  int rc = check_k(ctx, *w, k, orient);
+  if (rc) return rc;
+  if (plane_type(w->type))
+    return fail(ctx, MQ_DECLINED, "decode-step fusions cover Q4_K and IQ4_XS weights");
+  if (f->norm_weight && !(f->norm_epsilon > 0.0f))
+    return fail(ctx, MQ_ERR_SHAPE, "rmsnorm epsilon must be positive");
+  mq::GemvFusion fu;
+  fu.norm_w = f->norm_weight;
+  fu.norm_eps = f->norm_epsilon;
+  DeviceGuard guard(ctx->device);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (f->epilogue == MQ_EPILOGUE_ROPE_KV) {
+    if (f->rope_dim == 0 || f->rope_dim % 2 || f->rope_rows % f->rope_dim || f->rope_rows > w->rows)
+      return fail(ctx, MQ_ERR_SHAPE, "rope rows must be whole heads of an even dimension within the output");
+    if (!std::isfinite(f->rope_base) || f->rope_base <= 0.0f || !std::isfinite(f->rope_scale) ||
+        f->rope_scale <= 0.0f)
+      return fail(ctx, MQ_ERR_SHAPE, "RoPE base and scale must be finite and positive");
+    if (f->seg_begin[0] != 0 || f->seg_begin[1] < f->seg_begin[0] || f->seg_begin[2] < f->seg_begin[1] ||
+        f->seg_begin[2] > w->rows)
+      return fail(ctx, MQ_ERR_SHAPE, "output segments must start at 0 and be ordered within the output");
+    const uint64_t ends[3] = {f->seg_begin[1], f->seg_begin[2], w->rows};
+    for (int i = 0; i < 3; ++i) {
+      if (ends[i] > f->seg_begin[i] && !f->seg_out[i])
+        return fail(ctx, MQ_ERR_ARGUMENT, "null output for a non-empty segment");
+      fu.seg_begin[i] = static_cast<uint32_t>(f->seg_begin[i]);
+      fu.seg_out[i] = f->seg_out[i];
+    }
+    const float* freq = nullptr;
+    rc = rope_table(ctx, f->rope_base, f->rope_dim, &freq);
+    if (rc) return rc;
+    fu.freq = freq;
+    fu.position = static_cast<float>(f->rope_offset) * f->rope_scale;
+    fu.rope_rows = static_cast<uint32_t>(f->rope_rows);
+    fu.rope_dim = static_cast<uint32_t>(f->rope_dim);
+  } else if (f->epilogue == MQ_EPILOGUE_SILU_PAIRS) {
+    if (w->rows % 64) return fail(ctx, MQ_ERR_SHAPE, "gate/up pairs need a multiple of 64 stored rows");
+    if (!y_dev) return fail(ctx, MQ_ERR_ARGUMENT, "mq_decode_matmul_dev: null output");
+  } else if (f->epilogue == MQ_EPILOGUE_NONE) {
+    if (!y_dev) return fail(ctx, MQ_ERR_ARGUMENT, "mq_decode_matmul_dev: null output");
+    if (!f->norm_weight) return matmul_locked(ctx, *w, x_dev, 1, k, MQ_INT8_ACTIVATIONS | orient, y_dev, s);
+  } else {
+    return fail(ctx, MQ_ERR_ARGUMENT, "unknown decode epilogue " + std::to_string(f->epilogue));
   }
-  return buf;
-}
-
-// Validates the ids as the reference does (src/native/mod.rs:399-404) and
-// copies them to the device as u32. Caller holds ctx->mu.
-int stage_ids(mq_ctx* ctx, const Weight& w, const float* ids, uint64_t count, hipStream_t stream) {
-  const uint64_t vocab = w.transposed ? w.cols : w.rows;
-  std::vector<uint32_t> host(count);
-  for (uint64_t i = 0; i < count; ++i) {
-    const float raw = ids[i];
-    if (!(raw >= 0.0f) || raw != std::floor(raw) || static_cast<double>(raw) >= static_cast<double>(vocab))
-      return fail(ctx, MQ_ERR_SHAPE,
-                  "token id " + f32_text(raw) + " is not below the vocabulary size " + std::to_string(vocab));
-    host[i] = static_cast<uint32_t>(raw);
-  }
-  if (count > ctx->ids_cap) {
-    MQ_HIP(ctx, hipStreamSynchronize(stream));
-    if (ctx->ids) MQ_HIP(ctx, hipFree(ctx->ids));
-    ctx->ids = nullptr;
-    ctx->ids_cap = 0;
-    const size_t cap = count < 4096 ? 4096 : count;
-    MQ_HIP(ctx, hipMalloc(&ctx->ids, cap * sizeof(uint32_t)));
-    ctx->ids_cap = cap;
-  }
-  MQ_HIP(ctx, hipMemcpyAsync(ctx->ids, host.data(), count * sizeof(uint32_t), hipMemcpyHostToDevice, stream));
-  MQ_HIP(ctx, hipStreamSynchronize(stream));  // `host` is released on return
+  mq::GemvSplitK sk;
+  rc = order_stream(ctx, s);
+  if (!rc) rc = acquire_splitk(ctx, s, *w, 1, sk);
+  if (rc) return rc;
+  if (!mq::launch_gemv_decode_fused(static_cast<int>(w->type), w->dev, w->rows, w->nb, x_dev, y_dev,
+                                    f->norm_weight != nullptr, static_cast<int>(f->epilogue), fu, sk, s))
+    return fail(ctx, MQ_DECLINED, "the row does not fit the fused decode GEMV's LDS staging");
+  MQ_HIP(ctx, hipGetLastError());
   return MQ_OK;
 }
 
-}  // namespace
+// ---- embedding lookup ------------------------------------------------------------
 
 int mq_embedding_dev(mq_ctx* ctx, uint64_t handle, const float* ids, uint64_t count, float scale, float* out_dev,
                      void* stream) {
@@ -787,25 +872,10 @@ int mq_rope_dev(mq_ctx* ctx, const float* x_dev, uint64_t rows, uint64_t cols, f
   if (!x_dev || !out_dev) return fail(ctx, MQ_ERR_ARGUMENT, "mq_rope_dev: null pointer");
   std::lock_guard<std::mutex> lock(ctx->mu);
   DeviceGuard guard(ctx->device);
-  uint32_t base_bits;
-  std::memcpy(&base_bits, &base, sizeof base_bits);
-  const auto key = std::make_pair(base_bits, dimension);
-  auto it = ctx->rope_tables.find(key);
-  if (it == ctx->rope_tables.end()) {
-    // the reference's table: base.powf(-2.0 * (pair as f32) / dimension as f32), in f32
-    std::vector<float> table(dimension / 2);
-    for (uint64_t p = 0; p < dimension / 2; ++p)
-      table[p] = std::pow(base, -2.0f * static_cast<float>(p) / static_cast<float>(dimension));
-    float* dev = nullptr;
-    MQ_HIP(ctx, hipMalloc(&dev, table.size() * sizeof(float)));
-    hipError_t e = hipMemcpy(dev, table.data(), table.size() * sizeof(float), hipMemcpyHostToDevice);
-    if (e != hipSuccess) {
-      (void)hipFree(dev);
-      return hip_fail(ctx, e, "hipMemcpy(rope table)");
-    }
-    it = ctx->rope_tables.emplace(key, dev).first;
-  }
-  mq::launch_rope(x_dev, rows, cols, head_count, dimension, scale, position_offset, pairing, it->second, out_dev,
+  const float* freq = nullptr;
+  int rc = rope_table(ctx, base, dimension, &freq);
+  if (rc) return rc;
+  mq::launch_rope(x_dev, rows, cols, head_count, dimension, scale, position_offset, pairing, freq, out_dev,
                   static_cast<hipStream_t>(stream));
   MQ_HIP(ctx, hipGetLastError());
   return MQ_OK;

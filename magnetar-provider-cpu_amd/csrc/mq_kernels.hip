@@ -600,10 +600,87 @@ __global__ __launch_bounds__(512) void gemv_rows_iq4xs_int8_kernel(
 // which stalls every other work-group on the XCD.
 constexpr int kWaitVmcnt0 = 0x0F70;  // s_waitcnt vmcnt(0) expcnt(7) lgkmcnt(15): stores only
 
-template <int M>
+// Decode-step fusions of the LDS-form GEMV (m = 1), fixed per launch:
+//  NORM: the activation row is rmsnorm'd in the staging, x * scale * w with
+//   scale = 1 / sqrt(mean(x^2) + eps) (src/lib.rs:348-402), before the int8
+//   quantization;
+//  kEpiRope: rows below rope_rows are rotated in interleaved pairs (rows
+//   2i, 2i + 1 of a head of rope_dim) at `position` (src/lib.rs:616-687),
+//   and rows are routed to three outputs by row range (Q, then the K and V
+//   caches' rows: the kv-write, src/lib.rs:740-768);
+//  kEpiSiluPairs: the stored rows interleave gate and up by blocks of 32
+//   (block 2i = gate rows 32i.., block 2i + 1 = up rows 32i..), and the
+//   output is silu(gate) * up (src/lib.rs:2592-2596, 993-1004).
+constexpr int kEpiPlain = 0, kEpiRope = 1, kEpiSiluPairs = 2;
+
+using Fusion = GemvFusion;
+
+__device__ inline float wave_sum64(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// 1 / sqrt(mean(x^2) + eps) of the activation row, over the work-group
+// (the whole row, whatever the work-group's K range).
+__device__ inline float row_norm_scale(const float* __restrict__ x, uint64_t K, float eps) {
+  __shared__ float part[8];
+  float ss = 0.0f;
+  for (uint64_t i = threadIdx.x; i < K / 4; i += blockDim.x) {
+    const float4 a = reinterpret_cast<const float4*>(x)[i];
+    ss += a.x * a.x;
+    ss += a.y * a.y;
+    ss += a.z * a.z;
+    ss += a.w * a.w;
+  }
+  ss = wave_sum64(ss);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  float total = 0.0f;
+  for (int i = 0; i < static_cast<int>(blockDim.x >> 6); ++i) total += part[i];
+  return 1.0f / sqrtf(total / static_cast<float>(K) + eps);
+}
+
+// Stores one lane's row results (every lane of the wave calls it: the
+// epilogues exchange values across lanes).
+template <int M, int EPI>
+__device__ inline void store_out(const float (&v)[M], uint64_t row, bool valid, int lane, uint64_t rows, float* y,
+                                 const Fusion& fu) {
+  if constexpr (EPI == kEpiPlain) {
+    if (valid) {
+#pragma unroll
+      for (int m = 0; m < M; ++m) y[m * rows + row] = v[m];
+    }
+  } else if constexpr (EPI == kEpiRope) {
+    static_assert(M == 1, "decode-step epilogues take one activation row");
+    const float other = __shfl_xor(v[0], 1);
+    float o = v[0];
+    if (row < fu.rope_rows) {
+      const uint32_t p = static_cast<uint32_t>(row % fu.rope_dim) / 2;
+      const float angle = fu.position * fu.freq[p];
+      const float sn = sinf(angle), cs = cosf(angle);
+      // pair (a, b) = (even row, odd row): a c - b s, a s + b c
+      o = (lane & 1) == 0 ? v[0] * cs - other * sn : other * sn + v[0] * cs;
+    }
+    if (valid) {
+      const int seg = row >= fu.seg_begin[2] ? 2 : row >= fu.seg_begin[1] ? 1 : 0;
+      fu.seg_out[seg][row - fu.seg_begin[seg]] = o;
+    }
+  } else {
+    static_assert(M == 1, "decode-step epilogues take one activation row");
+    const float u = __shfl_down(v[0], 32);
+    if (lane < 32 && valid) {
+      const float g = v[0];
+      const float sg = g * (1.0f / (1.0f + expf(-g)));
+      y[(row - lane) / 2 + lane] = sg * u;
+    }
+  }
+}
+
+template <int M, int EPI>
 __device__ inline void splitk_finish(float (&acc)[M], float (&mins)[M], uint64_t rows, float* y,
                                      const float* addend, uint64_t addend_stride, float* partials,
-                                     uint32_t* counters, int KS) {
+                                     uint32_t* counters, int KS, const Fusion& fu) {
   const int lane = threadIdx.x & 63;
   const uint64_t rb = blockIdx.x, ks = blockIdx.y;
   const uint64_t rows64 = static_cast<uint64_t>(gridDim.x) * 64;
@@ -621,6 +698,8 @@ __device__ inline void splitk_finish(float (&acc)[M], float (&mins)[M], uint64_t
   if (lane == 0) ticket = __hip_atomic_fetch_add(&counters[rb], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   ticket = __shfl(ticket, 0);
   if (ticket != static_cast<uint32_t>(KS - 1)) return;
+  const bool valid = row < rows;
+  float v[M];
 #pragma unroll
   for (int m = 0; m < M; ++m) {
     float a = 0.0f, mn = 0.0f;
@@ -630,20 +709,19 @@ __device__ inline void splitk_finish(float (&acc)[M], float (&mins)[M], uint64_t
       mn += __hip_atomic_load(&partials[((i * M + m) * 2 + 1) * rows64 + row], __ATOMIC_RELAXED,
                               __HIP_MEMORY_SCOPE_AGENT);
     }
-    if (row < rows) {
-      float v = a - mn;
-      if (addend) v = v + addend[m * addend_stride + row];
-      y[m * rows + row] = v;
-    }
+    v[m] = a - mn;
+    if (addend && valid) v[m] = v[m] + addend[m * addend_stride + row];
   }
+  store_out<M, EPI>(v, row, valid, lane, rows, y, fu);
   if (lane == 0) __hip_atomic_store(&counters[rb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Cross-wave (within a work-group) reduction through the kernel's dynamic
 // LDS, then either the store of y (KS == 1) or the split-K epilogue.
-template <int M>
+template <int M, int EPI = kEpiPlain>
 __device__ inline void finish_rows(float (&acc)[M], float (&mins)[M], uint64_t rows, float* y, const float* addend,
-                                   uint64_t addend_stride, float* red, float* partials, uint32_t* counters, int KS) {
+                                   uint64_t addend_stride, float* red, float* partials, uint32_t* counters, int KS,
+                                   const Fusion& fu = Fusion{}) {
   const int lane = threadIdx.x & 63, s = threadIdx.x >> 6, S = blockDim.x >> 6;
   if (S > 1) {
     __syncthreads();  // every wave is done reading activations
@@ -666,17 +744,18 @@ __device__ inline void finish_rows(float (&acc)[M], float (&mins)[M], uint64_t r
     }
   }
   if (KS > 1) {
-    splitk_finish<M>(acc, mins, rows, y, addend, addend_stride, partials, counters, KS);
+    splitk_finish<M, EPI>(acc, mins, rows, y, addend, addend_stride, partials, counters, KS, fu);
     return;
   }
   const uint64_t row = static_cast<uint64_t>(blockIdx.x) * 64 + lane;
-  if (row >= rows) return;
+  const bool valid = row < rows;
+  float v[M];
 #pragma unroll
   for (int m = 0; m < M; ++m) {
-    float v = acc[m] - mins[m];
-    if (addend) v = v + addend[m * addend_stride + row];
-    y[m * rows + row] = v;
+    v[m] = acc[m] - mins[m];
+    if (addend && valid) v[m] = v[m] + addend[m * addend_stride + row];
   }
+  store_out<M, EPI>(v, row, valid, lane, rows, y, fu);
 }
 
 // ---------------------------------------------------------------------------
@@ -698,12 +777,14 @@ __device__ inline void finish_rows(float (&acc)[M], float (&mins)[M], uint64_t r
 // quantize4 shuffle together. Only the first kv values of each row's range
 // exist (kv < kn for a plane format whose K ends inside a group); the rest
 // are staged as zeros with d = 0.
-template <int TYPE, int M>
+template <int TYPE, int M, bool NORM = false>
 struct FusedStage {
   static constexpr int kPre = 4;
   float4 v[kPre];
+  float4 g[NORM ? kPre : 1];  // NORM: the rmsnorm weight at the same positions (M == 1)
 
-  __device__ void load(const float* __restrict__ xf, uint64_t K, uint64_t k0, int kn, int kv) {
+  __device__ void load(const float* __restrict__ xf, uint64_t K, uint64_t k0, int kn, int kv,
+                       const float* __restrict__ nw = nullptr) {
     const int n4 = M * kn / 4, per_row4 = kn / 4;
 #pragma unroll
     for (int j = 0; j < kPre; ++j) {
@@ -711,7 +792,16 @@ struct FusedStage {
       v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
       const int m = M == 1 ? 0 : i / per_row4, c4 = i - m * per_row4;
       if (i < n4 && 4 * c4 < kv) v[j] = *reinterpret_cast<const float4*>(xf + m * K + k0 + 4 * c4);
+      if constexpr (NORM) {
+        g[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (i < n4 && 4 * c4 < kv) g[j] = *reinterpret_cast<const float4*>(nw + k0 + 4 * c4);
+      }
     }
+  }
+
+  // x * scale * w, each product rounded (the rmsnorm's order)
+  __device__ static float4 normed(float4 x, float scale, float4 w) {
+    return make_float4(x.x * scale * w.x, x.y * scale * w.y, x.z * scale * w.z, x.w * scale * w.w);
   }
 
   __device__ static void put(const Quant4& q, int i, uint8_t* lds, int M_kn) {
@@ -737,20 +827,27 @@ struct FusedStage {
     }
   }
 
-  __device__ void store(const float* __restrict__ xf, uint64_t K, uint64_t k0, int kn, int kv, uint8_t* lds) const {
+  __device__ void store(const float* __restrict__ xf, uint64_t K, uint64_t k0, int kn, int kv, uint8_t* lds,
+                        float nscale = 1.0f, const float* __restrict__ nw = nullptr) const {
     const int n4 = M * kn / 4, per_row4 = kn / 4;
 #pragma unroll
     for (int j = 0; j < kPre; ++j) {
       const int i = j * static_cast<int>(blockDim.x) + static_cast<int>(threadIdx.x);
-      const Quant4 q = quantize4(v[j]);
+      float4 x = v[j];
+      if constexpr (NORM) x = normed(x, nscale, g[j]);
+      const Quant4 q = quantize4(x);
       if (i < n4) put(q, i, lds, M * kn);
     }
     for (int i0 = kPre * static_cast<int>(blockDim.x); i0 < n4; i0 += blockDim.x) {
       const int i = i0 + static_cast<int>(threadIdx.x);
       const bool act = i < n4;
       const int m = act ? i / per_row4 : 0, c4 = act ? i - m * per_row4 : 0;
-      const float4 x = act && 4 * c4 < kv ? *reinterpret_cast<const float4*>(xf + m * K + k0 + 4 * c4)
-                                          : make_float4(0.f, 0.f, 0.f, 0.f);
+      const bool in = act && 4 * c4 < kv;
+      float4 x = in ? *reinterpret_cast<const float4*>(xf + m * K + k0 + 4 * c4) : make_float4(0.f, 0.f, 0.f, 0.f);
+      if constexpr (NORM) {
+        const float4 w = in ? *reinterpret_cast<const float4*>(nw + k0 + 4 * c4) : make_float4(0.f, 0.f, 0.f, 0.f);
+        x = normed(x, nscale, w);
+      }
       const Quant4 q = quantize4(x);
       if (act) put(q, i, lds, M * kn);
     }
@@ -1115,11 +1212,12 @@ __device__ inline void row_block(const RawRowBlock& a, const uint8_t* lds, int k
   }
 }
 
-template <int TYPE, int M, bool FUSED>
+template <int TYPE, int M, bool FUSED, bool NORM = false, int EPI = kEpiPlain>
 __global__ __launch_bounds__(512) void gemv_lds_int8_kernel(
     const uint8_t* __restrict__ w, int nb, uint64_t rows, const int8_t* __restrict__ xv,
     const float* __restrict__ xs, const int32_t* __restrict__ xsum, const float* __restrict__ xf,
-    float* __restrict__ y, const float* __restrict__ addend, uint64_t addend_stride, SplitK sk) {
+    float* __restrict__ y, const float* __restrict__ addend, uint64_t addend_stride, SplitK sk, Fusion fu) {
+  static_assert(!NORM || (FUSED && M == 1), "the rmsnorm staging takes one f32 activation row");
   constexpr bool PIPE = M == 1;
   constexpr int kTile = TYPE == kTypeQ4K ? kQ4kTileBytes : kIq4xsTileBytes;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -1142,19 +1240,21 @@ __global__ __launch_bounds__(512) void gemv_lds_int8_kernel(
   auto block_off = [&](int b) { return b < b1 ? lane_off + static_cast<uint32_t>(b) * kTile : kBufferNone; };
 
   // 1. activation loads
-  FusedStage<TYPE, M> fs;
+  FusedStage<TYPE, M, NORM> fs;
   QuantizedStage<TYPE, M> qs;
   if (FUSED)
-    fs.load(xf, K, k0, kn, kn);
+    fs.load(xf, K, k0, kn, kn, fu.norm_w);
   else
     qs.load(xv, xs, xsum, K, k0, kn, kn);
   // 2. the wave's first weight block
   RawRowBlock A;
   const int bA = b0 + s;
   load_row_block<TYPE>(A, rsrc, block_off(bA), r);
-  // 3. activations into LDS
+  // 3. activations into LDS (rmsnorm'd first under NORM)
+  float nscale = 1.0f;
+  if constexpr (NORM) nscale = row_norm_scale(xf, K, fu.norm_eps);
   if (FUSED)
-    fs.store(xf, K, k0, kn, kn, lds);
+    fs.store(xf, K, k0, kn, kn, lds, nscale, fu.norm_w);
   else
     qs.store(xv, xs, xsum, K, k0, kn, kn, lds);
   __syncthreads();
@@ -1171,8 +1271,8 @@ __global__ __launch_bounds__(512) void gemv_lds_int8_kernel(
     if (!PIPE) __builtin_amdgcn_sched_barrier(0);
     row_block<TYPE, M, PIPE>(cur, lds, kn, kruns, b - b0, b + S - b0, b + S < b1, next, acc, mins);
   }
-  finish_rows<M>(acc, mins, rows, y, addend, addend_stride, reinterpret_cast<float*>(lds), sk.partials,
-                 sk.counters, sk.ks);
+  finish_rows<M, EPI>(acc, mins, rows, y, addend, addend_stride, reinterpret_cast<float*>(lds), sk.partials,
+                      sk.counters, sk.ks, fu);
 }
 
 // ---------------------------------------------------------------------------
@@ -2302,7 +2402,7 @@ void launch_gemv_lds(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb,
 #define X(MM)                                                                                                  \
   case MM:                                                                                                     \
     hipLaunchKernelGGL((gemv_lds_int8_kernel<kTypeQ4K, MM, FUSED>), grid, block, lds, stream, tiled, inb, rows, \
-                       values, scales, sums, x, y, addend, addend_stride, k);                                  \
+                       values, scales, sums, x, y, addend, addend_stride, k, Fusion{});                        \
     break;
       MQ_GEMV_CASES(X)
 #undef X
@@ -2314,7 +2414,7 @@ void launch_gemv_lds(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb,
 #define X(MM)                                                                                                    \
   case MM:                                                                                                       \
     hipLaunchKernelGGL((gemv_lds_int8_kernel<kTypeIq4Xs, MM, FUSED>), grid, block, lds, stream, tiled, inb, rows, \
-                       values, scales, nullptr, x, y, addend, addend_stride, k);                                 \
+                       values, scales, nullptr, x, y, addend, addend_stride, k, Fusion{});                       \
     break;
       MQ_GEMV_CASES(X)
 #undef X
@@ -2424,6 +2524,32 @@ bool launch_gemv_fused(int type, const uint8_t* tiled, uint64_t rows, uint64_t n
   launch_gemv_lds<true>(type, tiled, rows, nb, nullptr, nullptr, nullptr, x, m, y, addend, addend_stride,
                         lds_splits, sk, lds, stream);
   return true;
+}
+
+bool launch_gemv_decode_fused(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, const float* x, float* y,
+                              bool norm, int epilogue, const GemvFusion& fu, const GemvSplitK& sk,
+                              hipStream_t stream) {
+  int splits = 0;
+  size_t lds = 0;
+  if (!lds_form_shape(type, rows, nb, 1, 0, sk.ks, splits, lds)) return false;
+  dim3 grid(static_cast<unsigned>((rows + 63) / 64), static_cast<unsigned>(sk.ks)), block(64 * splits);
+  const int inb = static_cast<int>(nb);
+  const SplitK k{sk.partials, sk.counters, sk.ks};
+  const int key = (type == kTypeQ4K ? 0 : 8) + (norm ? 4 : 0) + epilogue;
+  switch (key) {
+#define X(T, KEY, N, E)                                                                                              \
+  case KEY:                                                                                                          \
+    hipLaunchKernelGGL((gemv_lds_int8_kernel<T, 1, true, N, E>), grid, block, lds, stream, tiled, inb, rows, nullptr, \
+                       nullptr, nullptr, x, y, nullptr, 0, k, fu);                                                    \
+    return true;
+    X(kTypeQ4K, 1, false, kEpiRope) X(kTypeQ4K, 2, false, kEpiSiluPairs) X(kTypeQ4K, 4, true, kEpiPlain)
+    X(kTypeQ4K, 5, true, kEpiRope) X(kTypeQ4K, 6, true, kEpiSiluPairs)
+    X(kTypeIq4Xs, 9, false, kEpiRope) X(kTypeIq4Xs, 10, false, kEpiSiluPairs) X(kTypeIq4Xs, 12, true, kEpiPlain)
+    X(kTypeIq4Xs, 13, true, kEpiRope) X(kTypeIq4Xs, 14, true, kEpiSiluPairs)
+#undef X
+    default:
+      return false;
+  }
 }
 
 // ---- embedding and input-major products (any format) --------------------------

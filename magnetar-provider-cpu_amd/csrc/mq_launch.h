@@ -57,6 +57,28 @@ bool launch_gemv_fused(int type, const uint8_t* tiled, uint64_t rows, uint64_t n
                        uint64_t m, float* y, const float* addend, uint64_t addend_stride, int splits,
                        const GemvSplitK& sk, hipStream_t stream);
 
+// Decode-step fusions of the fused-quantization GEMV (m = 1; Q4_K and
+// IQ4_XS). norm: rmsnorm the activation row with norm_w, norm_eps before
+// quantizing it. epilogue 1 (rope): rows below rope_rows rotated in
+// interleaved pairs of heads of rope_dim at `position` with frequencies
+// freq[rope_dim / 2], and row r written to seg_out[i][r - seg_begin[i]] for
+// the segment i holding it (seg_begin[0] = 0, y unused); epilogue 2 (silu
+// pairs): stored rows interleave gate / up in blocks of 32 (rows % 64 == 0)
+// and y[j] = silu(gate_j) * up_j. Returns false (nothing launched) when the
+// shape does not fit the LDS form.
+struct GemvFusion {
+  const float* norm_w = nullptr;
+  float norm_eps = 0.0f;
+  const float* freq = nullptr;
+  float position = 0.0f;
+  uint32_t rope_rows = 0, rope_dim = 2;
+  uint32_t seg_begin[3] = {0, 0, 0};
+  float* seg_out[3] = {nullptr, nullptr, nullptr};
+};
+bool launch_gemv_decode_fused(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, const float* x, float* y,
+                              bool norm, int epilogue, const GemvFusion& fusion, const GemvSplitK& sk,
+                              hipStream_t stream);
+
 // Decode GEMV, m in 1..8, f32 activations.
 void launch_gemv_f32(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb,
                      const float* x, uint64_t m, float* y, const float* addend, uint64_t addend_stride,

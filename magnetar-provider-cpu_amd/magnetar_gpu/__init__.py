@@ -39,6 +39,17 @@ ERR_OOM = 5
 ERR_ARGUMENT = 6
 INT8_ACTIVATIONS = 1
 TRANSPOSE_B = 2
+EPILOGUE_NONE = 0
+EPILOGUE_ROPE_KV = 1
+EPILOGUE_SILU_PAIRS = 2
+
+
+class DecodeFusion(ctypes.Structure):
+    """mq_decode_fusion (include/magnetar_gpu.h)."""
+    _fields_ = [("norm_weight", ctypes.c_void_p), ("norm_epsilon", ctypes.c_float), ("epilogue", ctypes.c_uint32),
+                ("rope_rows", ctypes.c_uint64), ("rope_dim", ctypes.c_uint64), ("rope_offset", ctypes.c_uint64),
+                ("rope_base", ctypes.c_float), ("rope_scale", ctypes.c_float),
+                ("seg_begin", ctypes.c_uint64 * 3), ("seg_out", ctypes.c_void_p * 3)]
 
 _u8p = ctypes.POINTER(ctypes.c_uint8)
 _f32p = ctypes.POINTER(ctypes.c_float)
@@ -92,6 +103,7 @@ def gpu_lib():
         L.mq_dequantize.argtypes = [_vp, _u64, ctypes.c_int, _f32p]
         L.mq_dequantize_dev.argtypes = [_vp, _u64, ctypes.c_int, _vp, _vp]
         L.mq_embedding.argtypes = [_vp, _u64, _f32p, _u64, ctypes.c_float, _f32p]
+        L.mq_decode_matmul_dev.argtypes = [_vp, _u64, _vp, _u64, ctypes.POINTER(DecodeFusion), _vp, _vp]
         L.mq_embedding_dev.argtypes = [_vp, _u64, _f32p, _u64, ctypes.c_float, _vp, _vp]
         L.mq_matmul_add_dev.argtypes = [_vp, _u64, _vp, _u64, _u64, ctypes.c_uint32, _vp, _u64, _vp, _vp]
         f32 = ctypes.c_float
@@ -238,6 +250,24 @@ class Context:
     def matmul_dev(self, weight, x_ptr, m, k, y_ptr, int8=True, stream=None, transpose_b=False):
         flags = (INT8_ACTIVATIONS if int8 else 0) | (TRANSPOSE_B if transpose_b else 0)
         self._check(gpu_lib().mq_matmul_dev(self.ptr, weight.handle, x_ptr, m, k, flags, y_ptr, stream))
+
+    def decode_matmul_dev(self, weight, x_ptr, k, y_ptr=None, norm_weight_ptr=None, norm_epsilon=0.0,
+                          epilogue=EPILOGUE_NONE, rope_rows=0, rope_dim=2, rope_offset=0, rope_base=1.0,
+                          rope_scale=1.0, segments=(), stream=None):
+        """One decode row through mq_decode_matmul_dev. segments: up to three
+        (first row, device pointer) pairs for EPILOGUE_ROPE_KV."""
+        f = DecodeFusion()
+        f.norm_weight = norm_weight_ptr
+        f.norm_epsilon = norm_epsilon
+        f.epilogue = epilogue
+        f.rope_rows, f.rope_dim, f.rope_offset = rope_rows, rope_dim, rope_offset
+        f.rope_base, f.rope_scale = rope_base, rope_scale
+        segs = list(segments) + [(weight.stored_rows, None)] * (3 - len(segments))
+        for i, (begin, ptr) in enumerate(segs):
+            f.seg_begin[i] = begin
+            f.seg_out[i] = ptr
+        self._check(gpu_lib().mq_decode_matmul_dev(self.ptr, weight.handle, x_ptr, k, ctypes.byref(f), y_ptr,
+                                                   stream))
 
     def embedding(self, weight, ids, scale=None):
         """The `embedding` Kernel on a packed table: [len(ids), dim]."""

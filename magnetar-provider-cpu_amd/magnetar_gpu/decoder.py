@@ -23,7 +23,7 @@ FFN 14336, rmsnorm eps 1e-5, rope theta 5e5.
 
 import numpy as np
 
-from . import Q4_K, gaussian, quantize
+from . import EPILOGUE_ROPE_KV, EPILOGUE_SILU_PAIRS, Q4_K, gaussian, quantize
 
 HIDDEN = 4096
 HEADS = 32
@@ -72,13 +72,27 @@ class LayerData:
         return sum(int(w.size) for w in self.weights.values())
 
 
+def interleave_gate_up(gate, up, block=32):
+    """Stored rows of gate and up interleaved in blocks of `block` rows (the
+    layout mq_decode_matmul_dev's silu-pairs epilogue reads)."""
+    n, rb = gate.shape
+    return np.stack([gate.reshape(n // block, block, rb), up.reshape(n // block, block, rb)], axis=1).reshape(2 * n, rb)
+
+
 class DecoderLayer:
     """The layer on one device: uploads the packed weights and the KV
     cache, allocates every intermediate once, and runs `step` (all device
-    work enqueued on one stream; nothing allocated per step)."""
+    work enqueued on one stream; nothing allocated per step).
 
-    def __init__(self, ctx, torch, data, int8=True):
-        self.ctx, self.torch, self.int8 = ctx, torch, int8
+    fused=True runs the step in 6 launches through mq_decode_matmul_dev:
+    rmsnorm + QKV GEMV + rope + kv-write; attention partials; combine;
+    O GEMV + residual; rmsnorm + gate/up GEMV + silu-mul; down GEMV +
+    residual. fused=False runs each operator's own entry point (12)."""
+
+    def __init__(self, ctx, torch, data, int8=True, fused=False):
+        self.ctx, self.torch, self.int8, self.fused = ctx, torch, int8, fused
+        if fused and not int8:
+            raise ValueError("the fused decode step quantizes its activations to int8")
         dev = "cuda"
         # Q, K and V share their input, as do gate and up: each trio/pair is
         # uploaded as one matrix of stacked rows (a row's bytes do not
@@ -86,7 +100,10 @@ class DecoderLayer:
         w = data.weights
         self.w = {name: ctx.upload(Q4_K, *PROJECTIONS[name], w[name]) for name in ("o", "down")}
         self.w["qkv"] = ctx.upload(Q4_K, QKV_ROWS, HIDDEN, np.concatenate([w["q"], w["k"], w["v"]]))
-        self.w["gate_up"] = ctx.upload(Q4_K, 2 * FFN, HIDDEN, np.concatenate([w["gate"], w["up"]]))
+        if fused:
+            self.w["gate_up"] = ctx.upload(Q4_K, 2 * FFN, HIDDEN, interleave_gate_up(w["gate"], w["up"]))
+        else:
+            self.w["gate_up"] = ctx.upload(Q4_K, 2 * FFN, HIDDEN, np.concatenate([w["gate"], w["up"]]))
         t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
         self.g_attn, self.g_ffn = t(data.g_attn), t(data.g_ffn)
         self.k_cache, self.v_cache = t(data.k_cache), t(data.v_cache)
@@ -102,6 +119,8 @@ class DecoderLayer:
         written there; attention reads rows 0..position)."""
         if not 0 <= position < self.capacity:
             raise ValueError(f"position {position} outside the {self.capacity}-row KV cache")
+        if self.fused:
+            return self._step_fused(position, stream)
         c, p = self.ctx, lambda t: t.data_ptr()  # noqa: E731
         c.rmsnorm_dev(p(self.x), 1, HIDDEN, p(self.g_attn), 1, EPS, p(self.xn), stream=stream)
         c.matmul_dev(self.w["qkv"], p(self.xn), 1, HIDDEN, p(self.qkv), int8=self.int8, stream=stream)
@@ -122,6 +141,24 @@ class DecoderLayer:
         c.silu_mul_dev(p(self.gu), p(self.gu) + FFN * 4, FFN, p(self.f), stream=stream)
         c.matmul_add_dev(self.w["down"], p(self.f), 1, FFN, p(self.h), 1, p(self.out), int8=self.int8,
                          stream=stream)
+        return self.out
+
+    def _step_fused(self, position, stream):
+        c, p = self.ctx, lambda t: t.data_ptr()  # noqa: E731
+        width = KV_HEADS * HEAD_DIM
+        q = p(self.qkv)
+        c.decode_matmul_dev(self.w["qkv"], p(self.x), HIDDEN, norm_weight_ptr=p(self.g_attn), norm_epsilon=EPS,
+                            epilogue=EPILOGUE_ROPE_KV, rope_rows=HIDDEN + width, rope_dim=HEAD_DIM,
+                            rope_offset=position, rope_base=THETA, rope_scale=1.0,
+                            segments=[(0, q), (HIDDEN, p(self.k_cache) + position * width * 4),
+                                      (HIDDEN + width, p(self.v_cache) + position * width * 4)], stream=stream)
+        c.attention_dev(q, 1, p(self.k_cache), p(self.v_cache), self.capacity, position + 1, HEADS,
+                        HEAD_DIM, KV_HEADS, p(self.a), causal=True, stream=stream)
+        c.matmul_add_dev(self.w["o"], p(self.a), 1, HEADS * HEAD_DIM, p(self.x), 1, p(self.h), int8=True,
+                         stream=stream)
+        c.decode_matmul_dev(self.w["gate_up"], p(self.h), HIDDEN, p(self.f), norm_weight_ptr=p(self.g_ffn),
+                            norm_epsilon=EPS, epilogue=EPILOGUE_SILU_PAIRS, stream=stream)
+        c.matmul_add_dev(self.w["down"], p(self.f), 1, FFN, p(self.h), 1, p(self.out), int8=True, stream=stream)
         return self.out
 
     def release(self):

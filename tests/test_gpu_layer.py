@@ -164,3 +164,124 @@ def test_decoder_layer_decode_step_matches_the_oracle(ctx):
     np.testing.assert_array_equal(kc[:4095], data.k_cache[:4095])
     close(kc[4095], ekc[4095], 1e-3, "new K row")
     close(vc[4095], evc[4095], 1e-3, "new V row")
+
+
+# ---- decode-step fusions (mq_decode_matmul_dev) -----------------------------------
+
+def test_decoder_layer_fused_step_matches_the_oracle(ctx):
+    """The same step in 6 launches (rmsnorm, rope and kv-write fused into
+    the QKV GEMV; rmsnorm and silu-mul into the gate/up GEMV) against the
+    oracle, at the packed matmul's 1e-3 bar."""
+    data = decoder.LayerData(seed=4)
+    layer = decoder.DecoderLayer(ctx, torch, data, fused=True)
+    try:
+        out = host(layer.step(4095))
+        kc, vc = host(layer.k_cache), host(layer.v_cache)
+    finally:
+        layer.release()
+    exp, ekc, evc = decoder.reference_step(data, 4095, oracle)
+    close(out, exp, 1e-3, "fused decoder layer output")
+    np.testing.assert_array_equal(kc[:4095], data.k_cache[:4095])
+    close(kc[4095], ekc[4095], 1e-3, "new K row")
+    close(vc[4095], evc[4095], 1e-3, "new V row")
+
+
+def _q4k(seed, n, k):
+    return mg.quantize(mg.Q4_K, mg.gaussian(seed, 0.02, n * k).reshape(n, k))
+
+
+def test_rope_kv_epilogue_equals_the_unfused_chain(ctx):
+    """GEMV + rope + kv-write in one launch equals matmul_dev, rope_dev and
+    kv_write_dev bit for bit (same kernel results, same rotation)."""
+    n, k, dim, pos = 768, 1024, 64, 37
+    w = _q4k(5, n, k)
+    h = ctx.upload(mg.Q4_K, n, k, w)
+    x = dev(rng(3).standard_normal((1, k)))
+    try:
+        y = torch.empty((1, n), dtype=torch.float32, device="cuda")
+        ctx.matmul_dev(h, x.data_ptr(), 1, k, y.data_ptr())
+        ref = torch.empty_like(y)
+        ctx.rope_dev(y.data_ptr(), 1, 512, 10000.0, 1.0, dim, pos, 512 // dim, ref.data_ptr())
+        exp = host(y).copy()
+        exp[:, :512] = host(ref)[:, :512]
+        q = torch.zeros((1, 384), dtype=torch.float32, device="cuda")
+        kc = torch.zeros((4, 128), dtype=torch.float32, device="cuda")
+        vc = torch.zeros((4, 256), dtype=torch.float32, device="cuda")
+        ctx.decode_matmul_dev(h, x.data_ptr(), k, epilogue=mg.EPILOGUE_ROPE_KV, rope_rows=512, rope_dim=dim,
+                              rope_offset=pos, rope_base=10000.0,
+                              segments=[(0, q.data_ptr()), (384, kc.data_ptr() + 2 * 128 * 4),
+                                        (512, vc.data_ptr() + 1 * 256 * 4)])
+        got = np.concatenate([host(q)[0], host(kc)[2], host(vc)[1]])
+        np.testing.assert_array_equal(got, exp[0])
+        assert not host(kc)[[0, 1, 3]].any() and not host(vc)[[0, 2, 3]].any()
+    finally:
+        h.release()
+
+
+def test_silu_pairs_epilogue_equals_silu_mul(ctx):
+    """Interleaved gate/up GEMV with silu-mul in the epilogue equals the
+    plain GEMV followed by silu_mul_dev, bit for bit."""
+    f, k = 640, 1024
+    g, u = _q4k(6, f, k), _q4k(7, f, k)
+    wi = decoder.interleave_gate_up(g, u)
+    h = ctx.upload(mg.Q4_K, 2 * f, k, wi)
+    x = dev(rng(4).standard_normal((1, k)))
+    try:
+        y = torch.empty((1, 2 * f), dtype=torch.float32, device="cuda")
+        ctx.matmul_dev(h, x.data_ptr(), 1, k, y.data_ptr())
+        yy = host(y)[0].reshape(-1, 2, 32)
+        gd, ud = dev(yy[:, 0].reshape(-1)), dev(yy[:, 1].reshape(-1))
+        exp = torch.empty(f, dtype=torch.float32, device="cuda")
+        ctx.silu_mul_dev(gd.data_ptr(), ud.data_ptr(), f, exp.data_ptr())
+        out = torch.empty(f, dtype=torch.float32, device="cuda")
+        ctx.decode_matmul_dev(h, x.data_ptr(), k, out.data_ptr(), epilogue=mg.EPILOGUE_SILU_PAIRS)
+        np.testing.assert_array_equal(host(out), host(exp))
+    finally:
+        h.release()
+
+
+def test_norm_staging_matches_rmsnorm_then_matmul(ctx):
+    """rmsnorm folded into the GEMV's staging: within the matmul bar of the
+    rmsnorm_dev + matmul_dev chain (the sum of squares adds in another
+    order, so an int8 rounding may differ), and of the oracle."""
+    n, k = 4096, 4096
+    w = _q4k(8, n, k)
+    h = ctx.upload(mg.Q4_K, n, k, w)
+    xh = (rng(5).standard_normal((1, k)) * 3).astype(np.float32)
+    gh = (1 + 0.1 * rng(6).standard_normal(k)).astype(np.float32)
+    x, gw = dev(xh), dev(gh)
+    try:
+        xn = torch.empty_like(x)
+        ctx.rmsnorm_dev(x.data_ptr(), 1, k, gw.data_ptr(), 1, 1e-5, xn.data_ptr())
+        y1 = torch.empty((1, n), dtype=torch.float32, device="cuda")
+        ctx.matmul_dev(h, xn.data_ptr(), 1, k, y1.data_ptr())
+        y2 = torch.empty_like(y1)
+        ctx.decode_matmul_dev(h, x.data_ptr(), k, y2.data_ptr(), norm_weight_ptr=gw.data_ptr(), norm_epsilon=1e-5)
+        close(host(y2), host(y1), 1e-3, "fused vs chained")
+        exp = oracle.columns_scalar(mg.Q4_K, w, n, k, oracle.rmsnorm(xh, gh, 1e-5), True)
+        close(host(y2), exp, 1e-3, "fused vs oracle")
+    finally:
+        h.release()
+
+
+def test_decode_fusion_rejects_and_declines(ctx):
+    w8 = mg.quantize(mg.Q4_K, mg.gaussian(1, 0.02, 96 * 256).reshape(96, 256))
+    h = ctx.upload(mg.Q4_K, 96, 256, w8)
+    z = torch.zeros(1 << 12, dtype=torch.float32, device="cuda")
+    try:
+        with pytest.raises(mg.GpuError):  # gate/up pairs need a multiple of 64 rows
+            ctx.decode_matmul_dev(h, z.data_ptr(), 256, z.data_ptr(), epilogue=mg.EPILOGUE_SILU_PAIRS)
+        with pytest.raises(mg.GpuError):  # rope rows must be whole heads
+            ctx.decode_matmul_dev(h, z.data_ptr(), 256, epilogue=mg.EPILOGUE_ROPE_KV, rope_rows=50, rope_dim=64,
+                                  segments=[(0, z.data_ptr())])
+        with pytest.raises(mg.GpuError):  # k mismatch
+            ctx.decode_matmul_dev(h, z.data_ptr(), 512, z.data_ptr())
+    finally:
+        h.release()
+    from magnetar_gpu import workloads
+    hq = ctx.upload(mg.Q8_0, 64, 256, workloads.random_blocks(mg.Q8_0, 64, 256, 3))
+    try:
+        with pytest.raises(mg.Declined):
+            ctx.decode_matmul_dev(hq, z.data_ptr(), 256, z.data_ptr(), epilogue=mg.EPILOGUE_SILU_PAIRS)
+    finally:
+        hq.release()
