@@ -5,6 +5,8 @@
 // Built with -ffp-contract=off: no multiply-add is fused unless written as
 // fmaf, so the dequantizer reproduces the reference's separately rounded
 // product and difference.
+#include <type_traits>
+
 #include "mq_device.h"
 #include "mq_launch.h"
 
@@ -2200,6 +2202,122 @@ __device__ inline void dequant_b(const RawB<TYPE, NF>& r, int kq, half8 (&bop)[2
   }
 }
 
+// Plane formats on the register-B GEMM: one lane's bytes of one group (256
+// values of its weight row) for the values 8 kq .. 8 kq + 7 of every run
+// (its K slot of the 32-wide MFMA K), loaded one group ahead.
+//  Q8_0: q[j] = run j's 8 quants; hdr = plane 0 (the 8 d).
+//  Q4_0 / IQ4_NL: q[j] = run j's 8 nibble-pair bytes (low nibbles hold
+//   values 0..15, high 16..31); hdr = plane 0.
+//  Q5_K: q[c] = chunk c's 8 nibble bytes (runs 2c, 2c + 1); hb[0] = the 8
+//   high-bit bytes; hdr = d, dmin, scales.
+//  Q6_K: q[2h + g % 2] = low-nibble bytes of half h; hb[h] = its high-bit
+//   bytes; hdr = the 16 i8 scales; dsh = d.
+template <int TYPE, int NF>
+struct RawPB {
+  uint4 hdr[NF];
+  uint2 q[8][NF];
+  uint2 hb[2][NF];
+  uint32_t dsh[NF];
+};
+
+template <int TYPE, int NF>
+__device__ inline void load_raw_pb(RawPB<TYPE, NF>& r, const uint8_t* const (&tile0)[NF], const int (&row)[NF],
+                                   const bool (&live)[NF], uint64_t b, int kq) {
+  constexpr int P = plane_count(TYPE);
+#pragma unroll
+  for (int f = 0; f < NF; ++f) {
+    if (!live[f]) {
+      r.hdr[f] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) r.q[j][f] = make_uint2(0, 0);
+      r.hb[0][f] = r.hb[1][f] = make_uint2(0, 0);
+      r.dsh[f] = 0;
+      continue;
+    }
+    const uint8_t* t = tile0[f] + b * tile_bytes(TYPE);
+    const int R = row[f], off = 16 * R + 8 * (kq & 1), hp = kq >> 1;
+    if constexpr (TYPE == kTypeQ8_0) {
+      r.hdr[f] = ld16(t + 16 * R);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) r.q[j][f] = ld8(t + 128 * (1 + 2 * j + hp) + off);
+    } else if constexpr (TYPE == kTypeQ4_0 || TYPE == kTypeIq4Nl) {
+      r.hdr[f] = ld16(t + 16 * R);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) r.q[j][f] = ld8(t + 128 * (1 + j) + off);
+    } else if constexpr (TYPE == kTypeQ5K) {
+      r.hdr[f] = ld16(t + 16 * R);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) r.q[c][f] = ld8(t + 128 * (3 + 2 * c + hp) + off);
+      r.hb[0][f] = ld8(t + 128 * (1 + hp) + off);
+    } else {
+      r.hdr[f] = ld16(t + 128 * 12 + 16 * R);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        r.q[2 * h][f] = ld8(t + 128 * (4 * h + hp) + off);
+        r.q[2 * h + 1][f] = ld8(t + 128 * (4 * h + 2 + hp) + off);
+        r.hb[h][f] = ld8(t + 128 * (8 + 2 * h + hp) + off);
+      }
+      r.dsh[f] = *reinterpret_cast<const uint16_t*>(t + 128 * P + 2 * R);
+    }
+  }
+}
+
+// K-step C (runs 2C, 2C + 1) of the plane formats as MFMA B operands:
+// value = scale * q - min, rounded once to f16.
+template <int TYPE, int NF, int C>
+__device__ inline void dequant_pb(const RawPB<TYPE, NF>& r, int kq, half8 (&bop)[2][NF]) {
+#pragma unroll
+  for (int f = 0; f < NF; ++f) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int j = 2 * C + h;
+      uint32_t v[2];
+      float sc, mn = 0.0f;
+      if constexpr (TYPE == kTypeQ8_0) {
+        v[0] = r.q[j][f].x;
+        v[1] = r.q[j][f].y;
+        sc = half_bits(word_of(r.hdr[f], j >> 1) >> (16 * (j & 1)));
+      } else if constexpr (TYPE == kTypeQ4_0 || TYPE == kTypeIq4Nl) {
+        const int sh = 4 * (kq >> 1);
+        const uint32_t n0 = (r.q[j][f].x >> sh) & 0x0F0F0F0Fu, n1 = (r.q[j][f].y >> sh) & 0x0F0F0F0Fu;
+        if constexpr (TYPE == kTypeQ4_0) {
+          v[0] = nibbles_minus_8(n0);
+          v[1] = nibbles_minus_8(n1);
+        } else {
+          v[0] = iq4_lookup4(n0);
+          v[1] = iq4_lookup4(n1);
+        }
+        sc = half_bits(word_of(r.hdr[f], j >> 1) >> (16 * (j & 1)));
+      } else if constexpr (TYPE == kTypeQ5K) {
+        const uint2 w = r.q[C][f], hb = r.hb[0][f];
+        v[0] = ((w.x >> (4 * h)) & 0x0F0F0F0Fu) | (((hb.x >> j) & 0x01010101u) << 4);
+        v[1] = ((w.y >> (4 * h)) & 0x0F0F0F0Fu) | (((hb.y >> j) & 0x01010101u) << 4);
+        uint32_t s6, m6;
+        q4k_sc_m(q4k_six_bit(r.hdr[f]), j, s6, m6);
+        sc = half_bits(r.hdr[f].x) * static_cast<float>(s6);
+        mn = half_bits(r.hdr[f].x >> 16) * static_cast<float>(m6);
+      } else {
+        const int hh = j >> 2, g = j & 3;
+        const uint2 w = r.q[2 * hh + (g & 1)][f], hb = r.hb[hh][f];
+        const int ls = 4 * (g >> 1), hs = 2 * g;
+        v[0] = six_bits_minus_32(((w.x >> ls) & 0x0F0F0F0Fu) | (((hb.x >> hs) & 0x03030303u) << 4));
+        v[1] = six_bits_minus_32(((w.y >> ls) & 0x0F0F0F0Fu) | (((hb.y >> hs) & 0x03030303u) << 4));
+        const int si = 8 * hh + 2 * g + (kq >> 1);
+        sc = half_bits(r.dsh[f]) * static_cast<float>(static_cast<int8_t>(byte_of(word_of(r.hdr[f], si >> 2), si & 3)));
+      }
+      uint32_t p[4];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        p[2 * t] = pack_f16x2(fmaf(sc, static_cast<float>(static_cast<int8_t>(byte_of(v[t], 0))), -mn),
+                              fmaf(sc, static_cast<float>(static_cast<int8_t>(byte_of(v[t], 1))), -mn));
+        p[2 * t + 1] = pack_f16x2(fmaf(sc, static_cast<float>(static_cast<int8_t>(byte_of(v[t], 2))), -mn),
+                                  fmaf(sc, static_cast<float>(static_cast<int8_t>(byte_of(v[t], 3))), -mn));
+      }
+      bop[h][f] = *reinterpret_cast<half8*>(p);
+    }
+  }
+}
+
 template <int TYPE, int MF, int NF>
 __global__ __launch_bounds__(256) void gemm_rb_kernel(const uint8_t* __restrict__ w, int nb, uint64_t rows,
                                                       uint64_t rows_padded, const uint16_t* __restrict__ a16,
@@ -2223,9 +2341,11 @@ __global__ __launch_bounds__(256) void gemm_rb_kernel(const uint8_t* __restrict_
     for (int f = 0; f < NF; ++f) acc[i][f] = floatx4{0.f, 0.f, 0.f, 0.f};
 
   // this lane's weight row per fragment: header address in super-block 0,
-  // and (IQ4_XS) the start of its quant planes
+  // and (IQ4_XS) the start of its quant planes; plane formats: the tile
+  // and the row within it
   const uint8_t* tile0[NF];
   const uint8_t* planes0[NF];
+  int prow[NF];
   bool wlive[NF];
 #pragma unroll
   for (int f = 0; f < NF; ++f) {
@@ -2233,7 +2353,8 @@ __global__ __launch_bounds__(256) void gemm_rb_kernel(const uint8_t* __restrict_
     wlive[f] = n < rows_padded;
     const uint64_t nn = wlive[f] ? n : 0;
     const uint8_t* t = w + (nn >> 3) * nb * tile_bytes(TYPE);
-    tile0[f] = t + (nn & 7) * (TYPE == kTypeQ4K ? 16 : 8);
+    prow[f] = static_cast<int>(nn & 7);
+    tile0[f] = is_plane_format(TYPE) ? t : t + (nn & 7) * (TYPE == kTypeQ4K ? 16 : 8);
     planes0[f] = t + 64 + (nn & 7) * 16 + 8 * (kq & 1);
   }
 
@@ -2254,9 +2375,17 @@ __global__ __launch_bounds__(256) void gemm_rb_kernel(const uint8_t* __restrict_
     }
   };
 
-  RawB<TYPE, NF> cur, nxt;
-  load_raw_b<TYPE, NF>(nxt, tile0, wlive, 0, kq);
-  if (TYPE == kTypeIq4Xs) load_raw_b_iq4<NF>(reinterpret_cast<RawB<kTypeIq4Xs, NF>&>(nxt), planes0, wlive, 0);
+  using Raw = std::conditional_t<is_plane_format(TYPE), RawPB<TYPE, NF>, RawB<TYPE, NF>>;
+  auto load_b = [&](Raw& r, uint64_t b) {
+    if constexpr (is_plane_format(TYPE)) {
+      load_raw_pb<TYPE, NF>(r, tile0, prow, wlive, b, kq);
+    } else {
+      load_raw_b<TYPE, NF>(r, tile0, wlive, b, kq);
+      if constexpr (TYPE == kTypeIq4Xs) load_raw_b_iq4<NF>(r, planes0, wlive, b);
+    }
+  };
+  Raw cur, nxt;
+  load_b(nxt, 0);
   uint4 areg[A_CHUNKS];
   load_a(0, areg);
   store_a(0, areg);
@@ -2282,21 +2411,27 @@ __global__ __launch_bounds__(256) void gemm_rb_kernel(const uint8_t* __restrict_
 
   for (int b = 0; b < nb; ++b) {
     cur = nxt;
-    if (b + 1 < nb) {
-      load_raw_b<TYPE, NF>(nxt, tile0, wlive, static_cast<uint64_t>(b + 1), kq);
-      if (TYPE == kTypeIq4Xs)
-        load_raw_b_iq4<NF>(reinterpret_cast<RawB<kTypeIq4Xs, NF>&>(nxt), planes0, wlive,
-                           static_cast<uint64_t>(b + 1));
-    }
+    if (b + 1 < nb) load_b(nxt, static_cast<uint64_t>(b + 1));
     half8 bop[2][NF];
-    dequant_b<TYPE, NF, 0>(cur, kq, bop);
-    kstep(4 * b + 0, bop);
-    dequant_b<TYPE, NF, 1>(cur, kq, bop);
-    kstep(4 * b + 1, bop);
-    dequant_b<TYPE, NF, 2>(cur, kq, bop);
-    kstep(4 * b + 2, bop);
-    dequant_b<TYPE, NF, 3>(cur, kq, bop);
-    kstep(4 * b + 3, bop);
+    if constexpr (is_plane_format(TYPE)) {
+      dequant_pb<TYPE, NF, 0>(cur, kq, bop);
+      kstep(4 * b + 0, bop);
+      dequant_pb<TYPE, NF, 1>(cur, kq, bop);
+      kstep(4 * b + 1, bop);
+      dequant_pb<TYPE, NF, 2>(cur, kq, bop);
+      kstep(4 * b + 2, bop);
+      dequant_pb<TYPE, NF, 3>(cur, kq, bop);
+      kstep(4 * b + 3, bop);
+    } else {
+      dequant_b<TYPE, NF, 0>(cur, kq, bop);
+      kstep(4 * b + 0, bop);
+      dequant_b<TYPE, NF, 1>(cur, kq, bop);
+      kstep(4 * b + 1, bop);
+      dequant_b<TYPE, NF, 2>(cur, kq, bop);
+      kstep(4 * b + 2, bop);
+      dequant_b<TYPE, NF, 3>(cur, kq, bop);
+      kstep(4 * b + 3, bop);
+    }
   }
 
 #pragma unroll
@@ -2776,12 +2911,17 @@ void launch_gemm_rb(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, 
   const uint64_t rows_padded = (rows + 7) / 8 * 8;
   const uint64_t bn = 4 * NF * 16, bm = MF * 16;
   dim3 grid(static_cast<unsigned>((rows + bn - 1) / bn), static_cast<unsigned>((m + bm - 1) / bm));
-  if (type == kTypeQ4K)
-    hipLaunchKernelGGL((gemm_rb_kernel<kTypeQ4K, MF, NF>), grid, dim3(256), 0, stream, tiled, static_cast<int>(nb),
-                       rows, rows_padded, a16, m, y, addend, addend_stride);
-  else
-    hipLaunchKernelGGL((gemm_rb_kernel<kTypeIq4Xs, MF, NF>), grid, dim3(256), 0, stream, tiled,
-                       static_cast<int>(nb), rows, rows_padded, a16, m, y, addend, addend_stride);
+  switch (type) {
+#define X(T)                                                                                                     \
+  case T:                                                                                                        \
+    hipLaunchKernelGGL((gemm_rb_kernel<T, MF, NF>), grid, dim3(256), 0, stream, tiled, static_cast<int>(nb), rows, \
+                       rows_padded, a16, m, y, addend, addend_stride);                                          \
+    break;
+    MQ_ALL_TYPES(X)
+#undef X
+    default:
+      break;
+  }
 }
 
 uint64_t tiles(uint64_t rows, uint64_t m, uint64_t bn, uint64_t bm) {
@@ -2803,16 +2943,20 @@ void launch_gemm(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, uin
                  hipStream_t stream) {
   const uint64_t rows_padded = (rows + 7) / 8 * 8;
   dim3 grid(static_cast<unsigned>((rows + kBN - 1) / kBN), static_cast<unsigned>((m + kBM - 1) / kBM));
-  switch (type) {
-#define X(T)                                                                                                     \
-  case T:                                                                                                        \
+  // plane formats whose rows end inside a group take the LDS-B form
+  if (is_plane_format(type) && k % 256 != 0) variant = 1;
+  if (variant == 1 && is_plane_format(type)) {
+    switch (type) {
+#define X(T)                                                                                                       \
+  case T:                                                                                                          \
     hipLaunchKernelGGL(gemm_kernel<T>, grid, dim3(256), 0, stream, tiled, static_cast<int>(nb), rows, rows_padded, \
-                       a16, m, y, addend, addend_stride, k);                                                     \
+                       a16, m, y, addend, addend_stride, k);                                                       \
     return;
-    X(kTypeQ8_0) X(kTypeQ4_0) X(kTypeIq4Nl) X(kTypeQ5K) X(kTypeQ6K)
+      X(kTypeQ8_0) X(kTypeQ4_0) X(kTypeIq4Nl) X(kTypeQ5K) X(kTypeQ6K)
 #undef X
-    default:
-      break;
+      default:
+        return;
+    }
   }
   if (variant == 0) variant = gemm_default_variant(rows, m);
   switch (variant) {
