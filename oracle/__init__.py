@@ -6,8 +6,8 @@ product library (``magnetar-provider-cpu_amd``) never imports it.
 
 ``liboracle.so`` (built from ``oracle.c`` and ``cpu_baseline.c`` by the
 Makefile here) restates, in C, the reference's
- - packed decode of Q8_0, Q4_0, IQ4_NL, Q4_K, Q5_K, Q6_K and IQ4_XS
-   (src/native/quant.rs:46-57, 96-149, 180-206, 284-338),
+ - packed decode of Q8_0, Q4_0, IQ4_NL, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K and
+   IQ4_XS (src/native/quant.rs:46-57, 96-206, 284-338),
  - dequantization (quant.rs:1702-1711),
  - int8 activation quantizer and scalar dot (quant.rs:340-388),
  - scalar int8 / f32 column kernel (quant.rs:559-597),
@@ -30,13 +30,16 @@ LIB_PATH = os.path.join(HERE, "liboracle.so")
 
 Q4_0 = 2
 Q8_0 = 8
+Q2_K = 10
+Q3_K = 11
 Q4_K = 12
 Q5_K = 13
 Q6_K = 14
 IQ4_NL = 20
 IQ4_XS = 23
-BLOCK_BYTES = {Q8_0: 34, Q4_0: 18, IQ4_NL: 18, Q4_K: 144, Q5_K: 176, Q6_K: 210, IQ4_XS: 136}
-BLOCK_ELEMENTS = {Q8_0: 32, Q4_0: 32, IQ4_NL: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, IQ4_XS: 256}
+BLOCK_BYTES = {Q8_0: 34, Q4_0: 18, IQ4_NL: 18, Q2_K: 84, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210, IQ4_XS: 136}
+BLOCK_ELEMENTS = {Q8_0: 32, Q4_0: 32, IQ4_NL: 32, Q2_K: 256, Q3_K: 256, Q4_K: 256, Q5_K: 256, Q6_K: 256,
+                  IQ4_XS: 256}
 
 _lib = None
 
@@ -61,6 +64,8 @@ def lib():
         L.or_f16_to_f32.argtypes = [ctypes.c_uint16]
         L.or_scale_min_k4.argtypes = [ctypes.c_int, u8p, u8p, u8p]
         L.or_iq4_xs_scales.argtypes = [u8p, i8p]
+        L.or_q3_k_scales.argtypes = [u8p, i8p]
+        L.or_q3_k_scales.restype = None
         L.or_decode_run.argtypes = [ctypes.c_int, u8p, ctypes.c_int, i8p, f32p, f32p]
         L.or_dequantize_rows.argtypes = [ctypes.c_int, u8p, u64, u64, f32p]
         L.or_quantize_rows.argtypes = [f32p, u64, i8p, f32p, i32p]
@@ -110,6 +115,13 @@ def iq4_xs_scales(six):
     b = np.ascontiguousarray(six, dtype=np.uint8)
     out = np.zeros(8, np.int8)
     lib().or_iq4_xs_scales(_p(b, ctypes.c_uint8), _p(out, ctypes.c_int8))
+    return out
+
+
+def q3_k_scales(twelve):
+    b = np.ascontiguousarray(twelve, dtype=np.uint8)
+    out = np.zeros(16, np.int8)
+    lib().or_q3_k_scales(_p(b, ctypes.c_uint8), _p(out, ctypes.c_int8))
     return out
 
 

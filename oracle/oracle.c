@@ -55,6 +55,8 @@ int or_block_bytes(int fmt) {
     case OR_Q8_0: return 34;
     case OR_Q4_0: return 18;
     case OR_IQ4_NL: return 18;
+    case OR_Q2_K: return 84;
+    case OR_Q3_K: return 110;
     case OR_Q4_K: return 144;
     case OR_Q5_K: return 176;
     case OR_Q6_K: return 210;
@@ -66,7 +68,7 @@ int or_block_bytes(int fmt) {
 int or_block_elements(int fmt) {
     switch (fmt) {
     case OR_Q8_0: case OR_Q4_0: case OR_IQ4_NL: return 32;
-    case OR_Q4_K: case OR_Q5_K: case OR_Q6_K: case OR_IQ4_XS: return 256;
+    case OR_Q2_K: case OR_Q3_K: case OR_Q4_K: case OR_Q5_K: case OR_Q6_K: case OR_IQ4_XS: return 256;
     default: return 0;
     }
 }
@@ -95,6 +97,23 @@ void or_iq4_xs_scales(const uint8_t *six, int8_t out[8]) {
     }
 }
 
+/* The external `q3_k_scales` (called at quant.rs:167): the GGUF Q3_K
+ * packing of sixteen 6-bit scales in 12 bytes, unpacked as ggml does
+ * (words a0, a1, t of the bytes: scale i < 4 = low nibble of byte i with
+ * bits 2(i % 4)..+1 of t on top, ...). Values 0..63; the caller subtracts
+ * 32. Parity unpinned by the reference tree (the crate is not vendored). */
+void or_q3_k_scales(const uint8_t *twelve, int8_t out[16]) {
+    uint32_t a[3];
+    memcpy(a, twelve, 12);
+    const uint32_t k1 = 0x03030303u, k2 = 0x0f0f0f0fu, t = a[2];
+    uint32_t w[4];
+    w[0] = (a[0] & k2) | (((t >> 0) & k1) << 4);
+    w[1] = (a[1] & k2) | (((t >> 2) & k1) << 4);
+    w[2] = ((a[0] >> 4) & k2) | (((t >> 4) & k1) << 4);
+    w[3] = ((a[1] >> 4) & k2) | (((t >> 6) & k1) << 4);
+    memcpy(out, w, 16);
+}
+
 /* The external `IQ4_NL_VALUES` (quant.rs:185, 201-202): the GGUF
  * kvalues_iq4nl codebook. Parity unpinned by the reference tree. */
 static const int8_t IQ4NL[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
@@ -114,8 +133,8 @@ static float half_at(const uint8_t *b, int at) {
 }
 
 /* `decode` (src/native/quant.rs:96-206): the Q8_0 (102-109), Q4K (110-121),
- * Q5K (122-135), Q6K (136-149), Iq4Nl / Q4_0 (180-195) and Iq4Xs (196-206)
- * arms. `run` counts within the block (always 0 for 32-value blocks). */
+ * Q5K (122-135), Q6K (136-149), Q2K (150-163), Q3K (164-179), Iq4Nl / Q4_0
+ * (180-195) and Iq4Xs (196-206) arms. `run` counts within the block (always 0 for 32-value blocks). */
 void or_decode_run(int fmt, const uint8_t *block, int run, int8_t q[OR_RUN],
                    float scale[2], float min[2]) {
     min[0] = min[1] = 0.0f;
@@ -152,6 +171,29 @@ void or_decode_run(int fmt, const uint8_t *block, int run, int8_t q[OR_RUN],
         for (int i = 0; i < OR_RUN; i++)
             q[i] = (int8_t)((int)(((low[i] >> low_shift) & 0xF) | (((high[i] >> high_shift) & 3) << 4)) - 32);
         for (int p = 0; p < 2; p++) scale[p] = d * (float)(int8_t)block[192 + 8 * h + 2 * g + p];
+    } else if (fmt == OR_Q2_K) {
+        /* quant.rs:150-163 */
+        float d = half_at(block, 80), dmin = half_at(block, 82);
+        int h = run / 4, j = run % 4;
+        const uint8_t *qs = block + 16 + 32 * h;
+        for (int i = 0; i < OR_RUN; i++) q[i] = (int8_t)((qs[i] >> (2 * j)) & 3);
+        for (int p = 0; p < 2; p++) {
+            uint8_t sc = block[8 * h + 2 * j + p];
+            scale[p] = d * (float)(sc & 0xF);
+            min[p] = dmin * (float)(sc >> 4);
+        }
+    } else if (fmt == OR_Q3_K) {
+        /* quant.rs:164-179 */
+        float d = half_at(block, 108);
+        int8_t sc[16];
+        or_q3_k_scales(block + 96, sc);
+        int h = run / 4, j = run % 4;
+        const uint8_t *quants = block + 32 + 32 * h;
+        const uint8_t *mask = block;
+        int bit = 4 * h + j;
+        for (int i = 0; i < OR_RUN; i++)
+            q[i] = (int8_t)((int)(((quants[i] >> (2 * j)) & 3) | (((mask[i] >> bit) & 1) << 2)) - 4);
+        for (int p = 0; p < 2; p++) scale[p] = d * (float)(sc[8 * h + 2 * j + p] - 32);
     } else if (fmt == OR_IQ4_NL || fmt == OR_Q4_0) {
         const int8_t *table = fmt == OR_Q4_0 ? Q40 : IQ4NL;
         float d = half_at(block, 0);

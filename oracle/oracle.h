@@ -1,6 +1,6 @@
 /*
  * CPU oracle for the GGUF block-quantized matmul path (Q4_K, IQ4_XS,
- * Q8_0, Q4_0, IQ4_NL, Q5_K, Q6_K).
+ * Q8_0, Q4_0, IQ4_NL, Q2_K, Q3_K, Q5_K, Q6_K).
  *
  * TEST INFRASTRUCTURE ONLY. This library is the checker: tests, the
  * smoke check and bench.py's CPU-baseline leg load it; the product
@@ -24,6 +24,8 @@ extern "C" {
 /* ggml type ids (public GGUF spec) */
 #define OR_Q4_0 2
 #define OR_Q8_0 8
+#define OR_Q2_K 10
+#define OR_Q3_K 11
 #define OR_Q4_K 12
 #define OR_Q5_K 13
 #define OR_Q6_K 14
@@ -40,6 +42,7 @@ void or_scale_min_k4(int j, const uint8_t *q, uint8_t *sc, uint8_t *m);
 void or_iq4_xs_scales(const uint8_t *six, int8_t out[8]);
 const int8_t *or_iq4nl_values(void);
 const int8_t *or_q4_0_values(void);
+void or_q3_k_scales(const uint8_t *twelve, int8_t out[16]);
 
 /* Run `run` of one block: 32 signed values, per-half scale and min. */
 void or_decode_run(int fmt, const uint8_t *block, int run, int8_t q[OR_RUN],

@@ -5,15 +5,18 @@ import numpy as np
 
 Q4_0 = 2
 Q8_0 = 8
+Q2_K = 10
+Q3_K = 11
 Q4_K = 12
 Q5_K = 13
 Q6_K = 14
 IQ4_NL = 20
 IQ4_XS = 23
-BLOCK_BYTES = {Q8_0: 34, Q4_0: 18, IQ4_NL: 18, Q4_K: 144, Q5_K: 176, Q6_K: 210, IQ4_XS: 136}
-BLOCK_ELEMENTS = {Q8_0: 32, Q4_0: 32, IQ4_NL: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, IQ4_XS: 256}
+BLOCK_BYTES = {Q8_0: 34, Q4_0: 18, IQ4_NL: 18, Q2_K: 84, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210, IQ4_XS: 136}
+BLOCK_ELEMENTS = {Q8_0: 32, Q4_0: 32, IQ4_NL: 32, Q2_K: 256, Q3_K: 256, Q4_K: 256, Q5_K: 256, Q6_K: 256,
+                  IQ4_XS: 256}
 # the formats of the generic (planes) GPU path
-PLANE_FORMATS = [Q8_0, Q4_0, IQ4_NL, Q5_K, Q6_K]
+PLANE_FORMATS = [Q8_0, Q4_0, IQ4_NL, Q2_K, Q3_K, Q5_K, Q6_K]
 
 
 class Rng:
@@ -35,7 +38,7 @@ def half_offsets(fmt):
     """Byte offsets of each block's f16 scale fields (src/native/tests.rs:24-32)."""
     if fmt in (Q4_K, Q5_K):
         return [0, 2]
-    return [208] if fmt == Q6_K else [0]
+    return {Q6_K: [208], Q2_K: [80, 82], Q3_K: [108]}.get(fmt, [0])
 
 
 def packed(fmt, rows, cols, seed):

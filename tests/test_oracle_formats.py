@@ -1,4 +1,4 @@
-"""Pins of the oracle's Q8_0, Q4_0, IQ4_NL, Q5_K and Q6_K decode
+"""Pins of the oracle's Q8_0, Q4_0, IQ4_NL, Q2_K, Q3_K, Q5_K and Q6_K decode
 (oracle/oracle.c `or_decode_run`, restating src/native/quant.rs:102-195).
 
 The reference's own decode is run-based; the checks here are the public
@@ -15,7 +15,7 @@ import numpy as np
 import pytest
 
 import oracle
-from helpers import (BLOCK_BYTES, IQ4_NL, PLANE_FORMATS, Q4_0, Q5_K, Q6_K, Q8_0, activations,
+from helpers import (BLOCK_BYTES, IQ4_NL, PLANE_FORMATS, Q2_K, Q3_K, Q4_0, Q5_K, Q6_K, Q8_0, activations,
                      assert_close_reference, packed)
 
 
@@ -84,6 +84,41 @@ def ggml_dequantize(fmt, w, rows, cols):
             is_ = np.arange(32) // 16
             for i, q in enumerate((q1, q2, q3, q4)):
                 y[:, 128 * n + 32 * i:128 * n + 32 * i + 32] = (d[:, None] * s[:, is_ + 2 * i]) * q
+    elif fmt == Q2_K:
+        raw = w.reshape(-1, 84)
+        d, dmin = _f16(raw, 80), _f16(raw, 82)
+        sc, qs = blocks[:, 0:16], blocks[:, 16:80]
+        y = np.zeros((nblk, 256))
+        isx = 0
+        for n in range(2):  # ggml: per 128 values, shift 0, 2, 4, 6 over the same 32 bytes
+            q = qs[:, 32 * n:32 * n + 32]
+            for j in range(4):
+                for half in range(2):
+                    s_ = sc[:, isx]
+                    isx += 1
+                    vals = (q[:, 16 * half:16 * half + 16] >> (2 * j)) & 3
+                    at = 128 * n + 32 * j + 16 * half
+                    y[:, at:at + 16] = (d * (s_ & 0xF))[:, None] * vals - (dmin * (s_ >> 4))[:, None]
+    elif fmt == Q3_K:
+        raw = w.reshape(-1, 110)
+        d = _f16(raw, 108)
+        hm, qs, b = blocks[:, 0:32], blocks[:, 32:96], blocks[:, 96:108]
+        # scale i: low nibble of byte i % 8 (nibble i // 8), high 2 bits from
+        # byte 8 + i % 4 at bit 2 (i // 4)
+        scales = np.stack([((b[:, i % 8] >> (4 * (i // 8))) & 0xF) | (((b[:, 8 + i % 4] >> (2 * (i // 4))) & 3) << 4)
+                           for i in range(16)], axis=1) - 32
+        y = np.zeros((nblk, 256))
+        isx, m = 0, 1
+        for n in range(2):
+            q = qs[:, 32 * n:32 * n + 32]
+            for j in range(4):
+                for half in range(2):
+                    sl = slice(16 * half, 16 * half + 16)
+                    vals = ((q[:, sl] >> (2 * j)) & 3) - np.where(hm[:, sl] & m, 0, 4)
+                    at = 128 * n + 32 * j + 16 * half
+                    y[:, at:at + 16] = (d * scales[:, isx])[:, None] * vals
+                    isx += 1
+                m <<= 1
     else:
         raise ValueError(fmt)
     return y.reshape(rows, cols).astype(np.float32)
@@ -210,3 +245,61 @@ def test_k_must_be_whole_blocks():
     w = packed(Q5_K, 1, 256, 3)
     with pytest.raises(ValueError):
         oracle.dequantize(Q5_K, w, 1, 96)
+
+
+def test_q3_k_scale_unpacking_inverts_the_gguf_packing():
+    """Sixteen 6-bit scales packed as the GGUF Q3_K encoder packs them (low
+    nibbles into bytes 0..7, low half first; the top 2 bits into bytes
+    8..11, two bits per group of four) unpack to themselves."""
+    r = np.random.default_rng(12)
+    for _ in range(50):
+        L = r.integers(0, 64, 16)
+        packed12 = np.zeros(12, np.int64)
+        for j in range(16):
+            lj = int(L[j])
+            if j < 8:
+                packed12[j] = lj & 0xF
+            else:
+                packed12[j - 8] |= (lj & 0xF) << 4
+            packed12[8 + j % 4] |= (lj >> 4) << (2 * (j // 4))
+        np.testing.assert_array_equal(oracle.q3_k_scales(packed12.astype(np.uint8)), L)
+
+
+def test_q2_k_known_answer():
+    """d = 1, dmin = 0.5; run (h, j) half p reads scale byte 8h + 2j + p
+    (low nibble scale, high nibble min) and 2-bit field j of the half's
+    32 quant bytes."""
+    blk = np.zeros(84, np.uint8)
+    blk[80:82] = [0x00, 0x3C]  # d = 1
+    blk[82:84] = [0x00, 0x38]  # dmin = 0.5
+    blk[0:16] = [(i % 15 + 1) | ((i % 4) << 4) for i in range(16)]
+    blk[16:80] = 0b11100100  # fields j = 0..3 hold 0, 1, 2, 3
+    got = oracle.dequantize(Q2_K, blk, 1, 256)[0]
+    for v in range(256):
+        h, rem = divmod(v, 128)
+        j, l = divmod(rem, 32)
+        b = int(blk[8 * h + 2 * j + l // 16])
+        assert got[v] == np.float32((b & 0xF) * j - 0.5 * (b >> 4)), v
+
+
+def test_q3_k_high_bit_mask_and_offset():
+    """All scales 33 (scale 1 after -32), d = 1: value = 2-bit field j of the
+    quant byte, minus 4 unless bit 4h + j of the mask byte is set."""
+    blk = np.zeros(110, np.uint8)
+    blk[108:110] = [0x00, 0x3C]
+    L = np.full(16, 33)
+    twelve = np.zeros(12, np.int64)
+    for j in range(16):
+        twelve[j % 8] |= (L[j] & 0xF) << (4 * (j // 8))
+        twelve[8 + j % 4] |= (L[j] >> 4) << (2 * (j // 4))
+    blk[96:108] = twelve.astype(np.uint8)
+    blk[32:96] = 0b10110001  # fields 1, 0, 3, 2
+    blk[0:32] = (1 << (np.arange(32) % 8)).astype(np.uint8)  # value l keeps its top bit in run l % 8
+    got = oracle.dequantize(Q3_K, blk, 1, 256)[0]
+    fields = [1, 0, 3, 2]
+    for v in range(256):
+        h, rem = divmod(v, 128)
+        j, l = divmod(rem, 32)
+        run = 4 * h + j
+        exp = fields[j] - (0 if l % 8 == run else 4)
+        assert got[v] == np.float32(exp), v
