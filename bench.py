@@ -12,7 +12,7 @@ the device time.
 Also reported: the GEMV kernel alone against the 8 TB/s HBM roofline, the
 other decode shapes, one Llama-3-8B-shaped decoder layer decode step
 (device-resident, weights + KV cache bytes per step), the same GEMV and
-GEMM for Q8_0, Q6_K, Q5_K, Q4_0 and IQ4_NL weights, the M=512 prefill
+GEMM for Q8_0, Q6_K, Q5_K, Q4_0, IQ4_NL, Q3_K and Q2_K weights, the M=512 prefill
 GEMM (x[512, 4096] . W[14336, 4096]^T) in TFLOP/s against the 2.5 PFLOP/s
 dense f16 MFMA peak, and the reference's CPU path (the oracle's AVX2
 restatement) timed on this host's cores.
@@ -323,7 +323,7 @@ def formats_part(ctx, torch, per_graph, use_graph, extra):
     y = torch.empty((1, n), dtype=torch.float32, device="cuda")
     xm = torch.from_numpy(mg.gaussian(4501, 1.0, 512 * k).reshape(512, k)).cuda()
     ym = torch.empty((512, n), dtype=torch.float32, device="cuda")
-    for fmt in (mg.Q8_0, mg.Q6_K, mg.Q5_K, mg.Q4_0, mg.IQ4_NL):
+    for fmt in (mg.Q8_0, mg.Q6_K, mg.Q5_K, mg.Q4_0, mg.IQ4_NL, mg.Q3_K, mg.Q2_K):
         name = mg.FORMAT_NAMES[fmt]
         w = workloads.random_blocks(fmt, n, k, 4000 + fmt)
         copies = [ctx.upload(fmt, n, k, w) for _ in range(max(2, -(-600_000_000 // w.size)))]

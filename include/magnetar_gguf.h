@@ -28,7 +28,8 @@ float gg_f16_to_f32(uint16_t h);
 void gg_gaussian_f32(uint64_t seed, float sigma, float *out, uint64_t n);
 
 /* Bytes of one stored row of `cols` weights for Q4_0, Q8_0, IQ4_NL (32-value
- * blocks), Q4_K, Q5_K, Q6_K, IQ4_XS (256-value blocks); 0 for another type
+ * blocks), Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_XS (256-value blocks); 0 for
+ * another type
  * or cols not whole blocks. */
 uint64_t gg_row_bytes(uint32_t gguf_type, uint64_t cols);
 

@@ -25,10 +25,12 @@ extern "C" {
 #endif
 
 /* ggml type ids (public GGUF specification) of the packed formats with a
- * GPU path (the reference's PackedWeightFormat variants Q4_0, Q8_0, Q4K,
- * Q5K, Q6K, Iq4Nl, Iq4Xs; src/native/quant.rs:71-86). */
+ * GPU path (the reference's PackedWeightFormat variants Q4_0, Q8_0, Q2K,
+ * Q3K, Q4K, Q5K, Q6K, Iq4Nl, Iq4Xs; src/native/quant.rs:71-86). */
 #define MQ_TYPE_Q4_0 2u
 #define MQ_TYPE_Q8_0 8u
+#define MQ_TYPE_Q2_K 10u
+#define MQ_TYPE_Q3_K 11u
 #define MQ_TYPE_Q4_K 12u
 #define MQ_TYPE_Q5_K 13u
 #define MQ_TYPE_Q6_K 14u
@@ -66,13 +68,14 @@ const char *mq_last_error(mq_ctx *ctx);
 
 /* Uploads a packed weight: `stored_rows` rows of `stored_cols` values,
  * `len` = stored_rows * stored_cols / block_values * block_bytes checkpoint
- * bytes (Q8_0 32 / 34, Q4_0 and IQ4_NL 32 / 18, Q4_K 256 / 144, Q5_K
- * 256 / 176, Q6_K 256 / 210, IQ4_XS 256 / 136); stored_cols must be whole
+ * bytes (Q8_0 32 / 34, Q4_0 and IQ4_NL 32 / 18, Q2_K 256 / 84, Q3_K
+ * 256 / 110, Q4_K 256 / 144, Q5_K 256 / 176, Q6_K 256 / 210, IQ4_XS
+ * 256 / 136); stored_cols must be whole
  * blocks. transposed != 0: the stored rows are the logical [k, n] weight's
  * output columns; 0: an untransposed weight or table whose stored rows are
  * its logical rows. Returns MQ_DECLINED for a type without a GPU path
- * (Q2_K, Q3_K, the IQ2 / IQ3 grid formats), so the caller keeps the f32
- * path. Replaces
+ * (the IQ2 / IQ3 grid formats), so the caller keeps the f32 path.
+ * Replaces
  * `write_packed_weight_tensor` -> `PackedWeightWrite::{Stored,Declined}`
  * (src/native/mod.rs:638-653) and `PackedWeight::new` (external,
  * magnetar-provider-api; used at src/native/tests.rs:66). */

@@ -83,6 +83,8 @@ uint64_t gg_row_bytes(uint32_t gguf_type, uint64_t cols) {
     case 2: values = 32; bytes = 18; break;   /* Q4_0 */
     case 8: values = 32; bytes = 34; break;   /* Q8_0 */
     case 20: values = 32; bytes = 18; break;  /* IQ4_NL */
+    case 10: bytes = 84; break;               /* Q2_K */
+    case 11: bytes = 110; break;              /* Q3_K */
     case GG_TYPE_Q4_K: bytes = 144; break;
     case 13: bytes = 176; break;              /* Q5_K */
     case 14: bytes = 210; break;              /* Q6_K */

@@ -26,6 +26,11 @@
 //              dmin, scales; 1-2: high bits; 3-10: nibbles).
 //       Q6_K   13 planes: bytes 16p .. 16p + 15 (0-7: low nibbles, 8-11:
 //              high bits, 12: the 16 i8 scales), then the shared d plane.
+//       Q2_K   5 planes: bytes 16p .. 16p + 15 (0: the 16 scale/min bytes,
+//              1-4: the 2-bit quants), then a shared 32-byte region with
+//              each row's d and dmin (row r at byte 4 r).
+//       Q3_K   7 planes: bytes 16p .. 16p + 15 (0-1: high-bit mask, 2-5:
+//              the 2-bit quants, 6: the 12 scale bytes and d, 2 bytes pad).
 //     A row whose K is not a multiple of 256 (32-value formats) ends in a
 //     group padded with zero blocks (d = 0).
 //
@@ -51,20 +56,34 @@ constexpr int kIq4xsTileBytes = 1088;
 
 constexpr int kTypeQ4_0 = 2;
 constexpr int kTypeQ8_0 = 8;
+constexpr int kTypeQ2K = 10;
+constexpr int kTypeQ3K = 11;
 constexpr int kTypeQ5K = 13;
 constexpr int kTypeQ6K = 14;
 constexpr int kTypeIq4Nl = 20;
 
 __host__ __device__ constexpr bool is_plane_format(int type) {
-  return type == kTypeQ8_0 || type == kTypeQ4_0 || type == kTypeIq4Nl || type == kTypeQ5K || type == kTypeQ6K;
+  return type == kTypeQ8_0 || type == kTypeQ4_0 || type == kTypeIq4Nl || type == kTypeQ5K || type == kTypeQ6K ||
+         type == kTypeQ2K || type == kTypeQ3K;
 }
 
-// Per-row 16-byte planes of a plane format's tile (shared d plane apart).
+// Per-row 16-byte planes of a plane format's tile (shared region apart).
 __host__ __device__ constexpr int plane_count(int type) {
-  return type == kTypeQ8_0 ? 17 : (type == kTypeQ4_0 || type == kTypeIq4Nl) ? 9 : type == kTypeQ5K ? 11 : 13;
+  return type == kTypeQ8_0                          ? 17
+         : (type == kTypeQ4_0 || type == kTypeIq4Nl) ? 9
+         : type == kTypeQ5K                          ? 11
+         : type == kTypeQ2K                          ? 5
+         : type == kTypeQ3K                          ? 7
+                                                     : 13;
 }
 
-__host__ __device__ constexpr bool plane_shared_d(int type) { return type == kTypeQ6K; }
+// Bytes per row of the tile's shared region after the planes: Q6_K's d,
+// Q2_K's d and dmin.
+__host__ __device__ constexpr int plane_shared_width(int type) {
+  return type == kTypeQ6K ? 2 : type == kTypeQ2K ? 4 : 0;
+}
+
+__host__ __device__ constexpr bool plane_shared_d(int type) { return plane_shared_width(type) != 0; }
 
 // Checkpoint block geometry: values and bytes per block.
 __host__ __device__ constexpr int block_values(int type) {
@@ -77,13 +96,15 @@ __host__ __device__ constexpr int block_bytes_of(int type) {
          : type == kTypeQ4K ? kQ4kBlockBytes
          : type == kTypeQ5K ? 176
          : type == kTypeQ6K ? 210
+         : type == kTypeQ2K ? 84
+         : type == kTypeQ3K ? 110
          : kIq4xsBlockBytes;
 }
 
 __host__ __device__ constexpr int tile_bytes(int type) {
   return type == kTypeQ4K     ? kQ4kTileBytes
          : type == kTypeIq4Xs ? kIq4xsTileBytes
-                              : 128 * plane_count(type) + (plane_shared_d(type) ? 16 : 0);
+                              : 128 * plane_count(type) + 8 * plane_shared_width(type);
 }
 
 // The GGUF kvalues_iq4nl codebook packed 4 bytes per word (little end

@@ -1331,6 +1331,25 @@ __device__ inline void plane_run_bytes(const Planes& P, int j, uint32_t (&lo)[4]
       lo[t] = ((word_of(l0, t) >> sh) & 0x0F0F0F0Fu) | (((word_of(h0, t) >> j) & 0x01010101u) << 4);
       hi[t] = ((word_of(l1, t) >> sh) & 0x0F0F0F0Fu) | (((word_of(h1, t) >> j) & 0x01010101u) << 4);
     }
+  } else if constexpr (TYPE == kTypeQ2K) {
+    // half h = j / 4 of the 64 quant bytes (planes 1 + 2h, 2 + 2h), field j % 4
+    const int h = j >> 2, sh = 2 * (j & 3);
+    const uint4 q0 = P(1 + 2 * h), q1 = P(2 + 2 * h);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      lo[t] = (word_of(q0, t) >> sh) & 0x03030303u;
+      hi[t] = (word_of(q1, t) >> sh) & 0x03030303u;
+    }
+  } else if constexpr (TYPE == kTypeQ3K) {
+    // 2-bit field j % 4 of half j / 4 (planes 2 + 2h, 3 + 2h), high bit j of
+    // the mask (planes 0, 1): values 0..7 standing for value - 4
+    const int h = j >> 2, sh = 2 * (j & 3);
+    const uint4 q0 = P(2 + 2 * h), q1 = P(3 + 2 * h), m0 = P(0), m1 = P(1);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      lo[t] = ((word_of(q0, t) >> sh) & 0x03030303u) | (((word_of(m0, t) >> j) & 0x01010101u) << 2);
+      hi[t] = ((word_of(q1, t) >> sh) & 0x03030303u) | (((word_of(m1, t) >> j) & 0x01010101u) << 2);
+    }
   } else {  // Q6_K
     const int h = j >> 2, g = j & 3;
     const int lp = 4 * h + 2 * (g & 1), hp = 8 + 2 * h, ls = 4 * (g >> 1), hs = 2 * g;
@@ -1341,6 +1360,33 @@ __device__ inline void plane_run_bytes(const Planes& P, int j, uint32_t (&lo)[4]
       hi[t] = ((word_of(l1, t) >> ls) & 0x0F0F0F0Fu) | (((word_of(h1, t) >> hs) & 0x03030303u) << 4);
     }
   }
+}
+
+// A row's shared-region bytes (Q6_K: d; Q2_K: d | dmin << 16), 0 otherwise.
+template <int TYPE>
+__device__ inline uint32_t shared_bits(const uint8_t* tile, int r) {
+  constexpr int P = plane_count(TYPE), W = plane_shared_width(TYPE);
+  if constexpr (W == 2) return *reinterpret_cast<const uint16_t*>(tile + 128 * P + 2 * r);
+  if constexpr (W == 4) return *reinterpret_cast<const uint32_t*>(tile + 128 * P + 4 * r);
+  return 0u;
+}
+
+// Q3_K scale i (0..63, before the -32) from plane 6 (the GGUF packing: low
+// nibbles in bytes 0..7, the top two bits in bytes 8..11).
+__device__ inline int q3k_scale(const uint4& p6, int i) {
+  const uint32_t k1 = 0x03030303u, k2 = 0x0F0F0F0Fu, t = p6.z;
+  const int w = i >> 2;
+  const uint32_t word = w == 0   ? (p6.x & k2) | ((t & k1) << 4)
+                        : w == 1 ? (p6.y & k2) | (((t >> 2) & k1) << 4)
+                        : w == 2 ? ((p6.x >> 4) & k2) | (((t >> 4) & k1) << 4)
+                                 : ((p6.y >> 4) & k2) | (((t >> 6) & k1) << 4);
+  return static_cast<int>(byte_of(word, i & 3));
+}
+
+// Signed bytes from 3-bit values 0..7 standing for value - 4 (Q3_K).
+__device__ inline uint32_t three_bits_minus_4(uint32_t t) {
+  const uint32_t x = t ^ 0x04040404u;
+  return x | ((x & 0x04040404u) * 0x3Eu);  // bytes 0..3 stay, 4..7 gain 0xF8
 }
 
 // The f16 d of 32-value block j from plane 0 (Q8_0, Q4_0, IQ4_NL).
@@ -1376,6 +1422,12 @@ __device__ inline void plane_run_signed(const Planes& P, uint32_t d_bits, int j,
       lo[t] = six_bits_minus_32(lo[t]);
       hi[t] = six_bits_minus_32(hi[t]);
     }
+  } else if constexpr (TYPE == kTypeQ3K) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      lo[t] = three_bits_minus_4(lo[t]);
+      hi[t] = three_bits_minus_4(hi[t]);
+    }
   }
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
@@ -1392,18 +1444,35 @@ __device__ inline void plane_run_signed(const Planes& P, uint32_t d_bits, int j,
     const float d = half_bits(d_bits);
     scale[0] = d * static_cast<float>(q6k_scale(P, j, 0));
     scale[1] = d * static_cast<float>(q6k_scale(P, j, 1));
+  } else if constexpr (TYPE == kTypeQ2K) {
+    const float d = half_bits(d_bits), dmin = half_bits(d_bits >> 16);
+    const uint4 sc = P(0);
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const int i = 8 * (j >> 2) + 2 * (j & 3) + p;
+      const uint32_t b = byte_of(word_of(sc, i >> 2), i & 3);
+      scale[p] = d * static_cast<float>(b & 0xFu);
+      mn[p] = dmin * static_cast<float>(b >> 4);
+    }
+  } else if constexpr (TYPE == kTypeQ3K) {
+    const uint4 p6 = P(6);
+    const float d = half_bits(p6.w);
+#pragma unroll
+    for (int p = 0; p < 2; ++p) scale[p] = d * static_cast<float>(q3k_scale(p6, 8 * (j >> 2) + 2 * (j & 3) + p) - 32);
   } else {
     scale[0] = scale[1] = block_d(P, j);
   }
 }
 
-// Repack: thread per (row, group, plane); plane_count(TYPE) is the shared d
-// plane of Q6_K (2 bytes per row). Blocks past the row's K stay zero.
+// Repack: thread per (row, group, plane); plane index plane_count(TYPE) is
+// the row's shared-region bytes (Q6_K's d at block byte 208, Q2_K's d and
+// dmin at 80). Bytes past the block (Q3_K's last plane) and blocks past the
+// row's K stay zero.
 template <int TYPE>
 __global__ void repack_planes_kernel(const uint8_t* __restrict__ raw, uint64_t rows, uint64_t K, uint64_t nb,
                                      uint8_t* __restrict__ tiled) {
   constexpr int P = plane_count(TYPE), BE = block_values(TYPE), BB = block_bytes_of(TYPE);
-  constexpr int PT = P + (plane_shared_d(TYPE) ? 1 : 0);
+  constexpr int W = plane_shared_width(TYPE), PT = P + (W ? 1 : 0);
   const uint64_t t = blockIdx.x * static_cast<uint64_t>(blockDim.x) + threadIdx.x;
   if (t >= rows * nb * PT) return;
   const int p = static_cast<int>(t % PT);
@@ -1411,9 +1480,9 @@ __global__ void repack_planes_kernel(const uint8_t* __restrict__ raw, uint64_t r
   const uint64_t blocks = K / BE, row_bytes = blocks * BB;
   const uint8_t* row = raw + n * row_bytes;
   uint8_t* tile = tiled + ((n >> 3) * nb + b) * tile_bytes(TYPE);
-  if (p == P) {  // Q6_K's d: bytes 208..209
-    tile[128 * P + 2 * (n & 7)] = row[b * BB + 208];
-    tile[128 * P + 2 * (n & 7) + 1] = row[b * BB + 209];
+  if (p == P) {
+    constexpr int src = TYPE == kTypeQ6K ? 208 : 80;
+    for (int i = 0; i < W; ++i) tile[128 * P + W * (n & 7) + i] = row[b * BB + src + i];
     return;
   }
   uint8_t* dst = tile + 128 * p + 16 * (n & 7);
@@ -1431,7 +1500,7 @@ __global__ void repack_planes_kernel(const uint8_t* __restrict__ raw, uint64_t r
         off = 2 + i;
       }
     }
-    dst[i] = blk < blocks ? row[blk * BB + off] : 0;
+    dst[i] = blk < blocks && off < static_cast<uint64_t>(BB) ? row[blk * BB + off] : 0;
   }
 }
 
@@ -1448,8 +1517,7 @@ __global__ void dequantize_planes_kernel(const uint8_t* __restrict__ tiled, uint
   const int j = static_cast<int>(u % 8), r = static_cast<int>(n & 7);
   const uint8_t* tile = tiled + ((n >> 3) * nb + b) * tile_bytes(TYPE);
   auto planes = [&](int p) { return ld16(tile + 128 * p + 16 * r); };
-  const uint32_t d_bits =
-      plane_shared_d(TYPE) ? static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(tile + 128 * P + 2 * r)) : 0u;
+  const uint32_t d_bits = shared_bits<TYPE>(tile, r);
   uint32_t q[8];
   float scale[2], mn[2];
   plane_run_signed<TYPE>(planes, d_bits, j, q, scale, mn);
@@ -1475,9 +1543,11 @@ __device__ inline void load_planes(PlaneBlock<TYPE>& a, __amdgpu_buffer_rsrc_t r
 #pragma unroll
   for (int p = 0; p < P; ++p) a.p[p] = buffer_ld16(rsrc, none ? kBufferNone : offset + 128 * p + 16 * r);
   a.d_bits = 0;
-  if constexpr (plane_shared_d(TYPE)) {
+  if constexpr (plane_shared_width(TYPE) == 2) {
     const uint32_t w = buffer_ld4(rsrc, none ? kBufferNone : offset + 128 * P + 4 * (r >> 1));
     a.d_bits = (r & 1) ? (w >> 16) : (w & 0xFFFFu);
+  } else if constexpr (plane_shared_width(TYPE) == 4) {
+    a.d_bits = buffer_ld4(rsrc, none ? kBufferNone : offset + 128 * P + 4 * r);
   }
 }
 
@@ -1491,7 +1561,7 @@ __device__ inline void plane_run_int8(const PlaneBlock<TYPE>& a, int j, const ui
   uint32_t lo[4], hi[4];
   plane_run_bytes<TYPE>(planes, j, lo, hi);
   float dj = 0.0f;
-  int sc0 = 0, sc1 = 0, smin = 0;
+  int sc0 = 0, sc1 = 0, smin = 0, smin1 = 0;
   if constexpr (TYPE == kTypeQ5K) {
     uint32_t sc, m;
     q4k_sc_m(q4k_six_bit(a.p[0]), j, sc, m);
@@ -1500,6 +1570,17 @@ __device__ inline void plane_run_int8(const PlaneBlock<TYPE>& a, int j, const ui
   } else if constexpr (TYPE == kTypeQ6K) {
     sc0 = q6k_scale(planes, j, 0);
     sc1 = q6k_scale(planes, j, 1);
+  } else if constexpr (TYPE == kTypeQ2K) {
+    const int i = 8 * (j >> 2) + 2 * (j & 3);
+    const uint32_t b0 = byte_of(word_of(a.p[0], i >> 2), i & 3), b1 = byte_of(word_of(a.p[0], (i + 1) >> 2), (i + 1) & 3);
+    sc0 = static_cast<int>(b0 & 0xFu);
+    sc1 = static_cast<int>(b1 & 0xFu);
+    smin = static_cast<int>(b0 >> 4);
+    smin1 = static_cast<int>(b1 >> 4);
+  } else if constexpr (TYPE == kTypeQ3K) {
+    const int i = 8 * (j >> 2) + 2 * (j & 3);
+    sc0 = q3k_scale(a.p[6], i) - 32;
+    sc1 = q3k_scale(a.p[6], i + 1) - 32;
   } else {
     dj = block_d(planes, j);
   }
@@ -1521,6 +1602,11 @@ __device__ inline void plane_run_int8(const PlaneBlock<TYPE>& a, int j, const ui
     if constexpr (TYPE == kTypeQ5K) {
       accb[m] = fmaf(static_cast<float>(sc0 * (d0 + d1)), dx, accb[m]);
       minb[m] = fmaf(static_cast<float>(smin * (s0 + s1)), dx, minb[m]);
+    } else if constexpr (TYPE == kTypeQ2K) {
+      accb[m] = fmaf(static_cast<float>(sc0 * d0 + sc1 * d1), dx, accb[m]);
+      minb[m] = fmaf(static_cast<float>(smin * s0 + smin1 * s1), dx, minb[m]);
+    } else if constexpr (TYPE == kTypeQ3K) {
+      accb[m] = fmaf(static_cast<float>(sc0 * (d0 - 4 * s0) + sc1 * (d1 - 4 * s1)), dx, accb[m]);
     } else if constexpr (TYPE == kTypeQ6K) {
       accb[m] = fmaf(static_cast<float>(sc0 * (d0 - 32 * s0) + sc1 * (d1 - 32 * s1)), dx, accb[m]);
     } else if constexpr (TYPE == kTypeQ4_0) {
@@ -1546,8 +1632,15 @@ __device__ inline void plane_block_int8(const PlaneBlock<TYPE>& a, const uint8_t
       acc[m] = fmaf(d, accb[m], acc[m]);
       mins[m] = fmaf(dmin, minb[m], mins[m]);
     }
-  } else if constexpr (TYPE == kTypeQ6K) {
-    const float d = half_bits(a.d_bits);
+  } else if constexpr (TYPE == kTypeQ2K) {
+    const float d = half_bits(a.d_bits), dmin = half_bits(a.d_bits >> 16);
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      acc[m] = fmaf(d, accb[m], acc[m]);
+      mins[m] = fmaf(dmin, minb[m], mins[m]);
+    }
+  } else if constexpr (TYPE == kTypeQ6K || TYPE == kTypeQ3K) {
+    const float d = half_bits(TYPE == kTypeQ6K ? a.d_bits : a.p[6].w);
 #pragma unroll
     for (int m = 0; m < M; ++m) acc[m] = fmaf(d, accb[m], acc[m]);
   } else {
@@ -1705,10 +1798,8 @@ __device__ inline void row_run_values(const uint8_t* __restrict__ tiled, uint64_
       }
     }
   } else {
-    constexpr int P = plane_count(TYPE);
     auto planes = [&](int p) { return ld16(tile + 128 * p + 16 * r); };
-    const uint32_t d_bits =
-        plane_shared_d(TYPE) ? static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(tile + 128 * P + 2 * r)) : 0u;
+    const uint32_t d_bits = shared_bits<TYPE>(tile, r);
     uint32_t q[8];
     float scale[2], mn[2];
     plane_run_signed<TYPE>(planes, d_bits, j, q, scale, mn);
@@ -1974,10 +2065,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const uint8_t* __restrict__ w
           const uint8_t* tile = w + ((n >> 3) * nb + b) * tile_bytes(TYPE);
           const int r = static_cast<int>(n & 7);
           auto planes = [&](int p) { return ld16(tile + 128 * p + 16 * r); };
-          const uint32_t d_bits =
-              plane_shared_d(TYPE)
-                  ? static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(tile + 128 * plane_count(TYPE) + 2 * r))
-                  : 0u;
+          const uint32_t d_bits = shared_bits<TYPE>(tile, r);
           uint32_t q[8];
           float sc[2], mn[2];
           plane_run_signed<TYPE>(planes, d_bits, 2 * c + h, q, sc, mn);
@@ -2249,6 +2337,16 @@ __device__ inline void load_raw_pb(RawPB<TYPE, NF>& r, const uint8_t* const (&ti
 #pragma unroll
       for (int c = 0; c < 4; ++c) r.q[c][f] = ld8(t + 128 * (3 + 2 * c + hp) + off);
       r.hb[0][f] = ld8(t + 128 * (1 + hp) + off);
+    } else if constexpr (TYPE == kTypeQ2K) {
+      r.hdr[f] = ld16(t + 16 * R);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) r.q[h][f] = ld8(t + 128 * (1 + 2 * h + hp) + off);
+      r.dsh[f] = *reinterpret_cast<const uint32_t*>(t + 128 * P + 4 * R);
+    } else if constexpr (TYPE == kTypeQ3K) {
+      r.hdr[f] = ld16(t + 128 * 6 + 16 * R);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) r.q[h][f] = ld8(t + 128 * (2 + 2 * h + hp) + off);
+      r.hb[0][f] = ld8(t + 128 * hp + off);
     } else {
       r.hdr[f] = ld16(t + 128 * 12 + 16 * R);
 #pragma unroll
@@ -2296,6 +2394,20 @@ __device__ inline void dequant_pb(const RawPB<TYPE, NF>& r, int kq, half8 (&bop)
         q4k_sc_m(q4k_six_bit(r.hdr[f]), j, s6, m6);
         sc = half_bits(r.hdr[f].x) * static_cast<float>(s6);
         mn = half_bits(r.hdr[f].x >> 16) * static_cast<float>(m6);
+      } else if constexpr (TYPE == kTypeQ2K) {
+        const int hh = j >> 2, sh = 2 * (j & 3);
+        v[0] = (r.q[hh][f].x >> sh) & 0x03030303u;
+        v[1] = (r.q[hh][f].y >> sh) & 0x03030303u;
+        const int si = 8 * hh + 2 * (j & 3) + (kq >> 1);
+        const uint32_t b = byte_of(word_of(r.hdr[f], si >> 2), si & 3);
+        sc = half_bits(r.dsh[f]) * static_cast<float>(b & 0xFu);
+        mn = half_bits(r.dsh[f] >> 16) * static_cast<float>(b >> 4);
+      } else if constexpr (TYPE == kTypeQ3K) {
+        const int hh = j >> 2, sh = 2 * (j & 3);
+        const uint2 hb = r.hb[0][f];
+        v[0] = three_bits_minus_4(((r.q[hh][f].x >> sh) & 0x03030303u) | (((hb.x >> j) & 0x01010101u) << 2));
+        v[1] = three_bits_minus_4(((r.q[hh][f].y >> sh) & 0x03030303u) | (((hb.y >> j) & 0x01010101u) << 2));
+        sc = half_bits(r.hdr[f].w) * static_cast<float>(q3k_scale(r.hdr[f], 8 * hh + 2 * (j & 3) + (kq >> 1)) - 32);
       } else {
         const int hh = j >> 2, g = j & 3;
         const uint2 w = r.q[2 * hh + (g & 1)][f], hb = r.hb[hh][f];
@@ -2689,7 +2801,7 @@ bool launch_gemv_decode_fused(int type, const uint8_t* tiled, uint64_t rows, uin
 
 // ---- embedding and input-major products (any format) --------------------------
 
-#define MQ_ALL_TYPES(X) X(kTypeQ4K) X(kTypeIq4Xs) X(kTypeQ8_0) X(kTypeQ4_0) X(kTypeIq4Nl) X(kTypeQ5K) X(kTypeQ6K)
+#define MQ_ALL_TYPES(X) X(kTypeQ4K) X(kTypeIq4Xs) X(kTypeQ8_0) X(kTypeQ4_0) X(kTypeIq4Nl) X(kTypeQ2K) X(kTypeQ3K) X(kTypeQ5K) X(kTypeQ6K)
 
 void launch_embedding(int type, const uint8_t* tiled, uint64_t nb, int transposed, const uint32_t* ids,
                       uint64_t count, uint64_t dim, float scale, int scaled, float* out, hipStream_t stream) {
@@ -2748,14 +2860,14 @@ void launch_axpy(int type, const uint8_t* tiled, uint64_t nb, uint64_t k, uint64
 
 void launch_repack_planes(int type, const uint8_t* raw, uint64_t rows, uint64_t k, uint64_t nb, uint8_t* tiled,
                           hipStream_t stream) {
-  const uint64_t threads = rows * nb * (plane_count(type) + (plane_shared_d(type) ? 1 : 0));
+  const uint64_t threads = rows * nb * (plane_count(type) + (plane_shared_width(type) ? 1 : 0));
   switch (type) {
 #define X(T)                                                                                                 \
   case T:                                                                                                    \
     hipLaunchKernelGGL(repack_planes_kernel<T>, dim3(grid_for(threads, 256)), dim3(256), 0, stream, raw, rows, \
                        k, nb, tiled);                                                                        \
     break;
-    X(kTypeQ8_0) X(kTypeQ4_0) X(kTypeIq4Nl) X(kTypeQ5K) X(kTypeQ6K)
+    X(kTypeQ8_0) X(kTypeQ4_0) X(kTypeIq4Nl) X(kTypeQ2K) X(kTypeQ3K) X(kTypeQ5K) X(kTypeQ6K)
 #undef X
     default:
       break;
@@ -2771,7 +2883,7 @@ void launch_dequantize_planes(int type, const uint8_t* tiled, uint64_t rows, uin
     hipLaunchKernelGGL(dequantize_planes_kernel<T>, dim3(grid_for(threads, 256)), dim3(256), 0, stream, tiled, rows, \
                        k, nb, logical, out);                                                                        \
     break;
-    X(kTypeQ8_0) X(kTypeQ4_0) X(kTypeIq4Nl) X(kTypeQ5K) X(kTypeQ6K)
+    X(kTypeQ8_0) X(kTypeQ4_0) X(kTypeIq4Nl) X(kTypeQ2K) X(kTypeQ3K) X(kTypeQ5K) X(kTypeQ6K)
 #undef X
     default:
       break;
@@ -2827,7 +2939,7 @@ void launch_gemv_planes_int8(int type, const uint8_t* tiled, uint64_t rows, uint
                          values, scales, sums, x, y, addend, addend_stride, kk);                                  \
     break;
 #define X(T) Y(T, 1) Y(T, 2) Y(T, 3) Y(T, 4) Y(T, 5) Y(T, 6) Y(T, 7) Y(T, 8)
-    X(kTypeQ8_0) X(kTypeQ4_0) X(kTypeIq4Nl) X(kTypeQ5K) X(kTypeQ6K)
+    X(kTypeQ8_0) X(kTypeQ4_0) X(kTypeIq4Nl) X(kTypeQ2K) X(kTypeQ3K) X(kTypeQ5K) X(kTypeQ6K)
 #undef X
 #undef Y
     default:
@@ -2850,7 +2962,7 @@ void launch_gemv_planes_f32(int type, const uint8_t* tiled, uint64_t rows, uint6
                        addend_stride);                                                                             \
     break;
 #define X(T) Y(T, 1) Y(T, 2) Y(T, 3) Y(T, 4) Y(T, 5) Y(T, 6) Y(T, 7) Y(T, 8)
-    X(kTypeQ8_0) X(kTypeQ4_0) X(kTypeIq4Nl) X(kTypeQ5K) X(kTypeQ6K)
+    X(kTypeQ8_0) X(kTypeQ4_0) X(kTypeIq4Nl) X(kTypeQ2K) X(kTypeQ3K) X(kTypeQ5K) X(kTypeQ6K)
 #undef X
 #undef Y
     default:
@@ -2952,7 +3064,7 @@ void launch_gemm(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, uin
     hipLaunchKernelGGL(gemm_kernel<T>, grid, dim3(256), 0, stream, tiled, static_cast<int>(nb), rows, rows_padded, \
                        a16, m, y, addend, addend_stride, k);                                                       \
     return;
-      X(kTypeQ8_0) X(kTypeQ4_0) X(kTypeIq4Nl) X(kTypeQ5K) X(kTypeQ6K)
+      X(kTypeQ8_0) X(kTypeQ4_0) X(kTypeIq4Nl) X(kTypeQ2K) X(kTypeQ3K) X(kTypeQ5K) X(kTypeQ6K)
 #undef X
       default:
         return;

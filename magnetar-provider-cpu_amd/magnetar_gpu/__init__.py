@@ -20,15 +20,18 @@ EXECUTOR_LIB = os.path.join(PKG_DIR, "libmagnetar_executor.so")
 
 Q4_0 = 2
 Q8_0 = 8
+Q2_K = 10
+Q3_K = 11
 Q4_K = 12
 Q5_K = 13
 Q6_K = 14
 IQ4_NL = 20
 IQ4_XS = 23
-BLOCK_BYTES = {Q8_0: 34, Q4_0: 18, IQ4_NL: 18, Q4_K: 144, Q5_K: 176, Q6_K: 210, IQ4_XS: 136}
-BLOCK_VALUES = {Q8_0: 32, Q4_0: 32, IQ4_NL: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, IQ4_XS: 256}
-FORMAT_NAMES = {Q8_0: "Q8_0", Q4_0: "Q4_0", IQ4_NL: "IQ4_NL", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K",
-                IQ4_XS: "IQ4_XS"}
+BLOCK_BYTES = {Q8_0: 34, Q4_0: 18, IQ4_NL: 18, Q2_K: 84, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210, IQ4_XS: 136}
+BLOCK_VALUES = {Q8_0: 32, Q4_0: 32, IQ4_NL: 32, Q2_K: 256, Q3_K: 256, Q4_K: 256, Q5_K: 256, Q6_K: 256,
+                IQ4_XS: 256}
+FORMAT_NAMES = {Q8_0: "Q8_0", Q4_0: "Q4_0", IQ4_NL: "IQ4_NL", Q2_K: "Q2_K", Q3_K: "Q3_K", Q4_K: "Q4_K",
+                Q5_K: "Q5_K", Q6_K: "Q6_K", IQ4_XS: "IQ4_XS"}
 
 OK = 0
 ERR_SHAPE = 1

@@ -14,7 +14,7 @@ import functools
 
 import numpy as np
 
-from . import BLOCK_BYTES, BLOCK_VALUES, IQ4_XS, Q4_K, Q5_K, Q6_K, gaussian, quantize
+from . import BLOCK_BYTES, BLOCK_VALUES, IQ4_XS, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, gaussian, quantize
 
 # name -> (gguf type, stored rows N, stored cols K, workload seed, weight index)
 WEIGHTS = {
@@ -59,7 +59,7 @@ def scale_offsets(fmt):
     """Byte offsets of a block's f16 scale fields."""
     if fmt in (Q4_K, Q5_K):
         return (0, 2)
-    return (208,) if fmt == Q6_K else (0,)
+    return {Q6_K: (208,), Q2_K: (80, 82), Q3_K: (108,)}.get(fmt, (0,))
 
 
 def random_blocks(fmt, rows, cols, seed):
