@@ -2564,6 +2564,304 @@ __global__ __launch_bounds__(256) void gemm_rb_kernel(const uint8_t* __restrict_
   }
 }
 
+// ---------------------------------------------------------------------------
+// Q4_K prefill GEMM, K-split form (`gemm_ks_kernel`).
+//
+// 512 threads = 8 waves, two per SIMD: wave = nw + 4 kw. A work-group owns a
+// 128 (M) x 256 (N) output tile; wave (nw, kw) computes its 128 x 64 part over
+// the K half kw (super-blocks [kw nbh, (kw + 1) nbh)) on v_mfma_f32_32x32x16_f16,
+// and the two halves are summed through LDS at the end. Splitting K inside the
+// work-group gives 224 work-groups at 512 x 14336 (one per CU) with two waves
+// per SIMD, so one wave's dequantization overlaps the other's MFMAs.
+//
+// A (f16 activations): per K half a 4-stage LDS ring, one 64-wide K-step
+//   (128 rows x 128 B) per stage, filled 3 K-steps ahead by buffer_load ... lds
+//   (16 B chunks XOR-swizzled by row so the 32 rows of a fragment read hit
+//   distinct banks). One barrier per K-step, issued without a vmcnt(0) fence:
+//   each wave waits only for the stage it reads next.
+// B (Q4_K weight rows): each lane holds column 32 f + l32 of its 64 and the K
+//   slot 8 kh .. 8 kh + 7 of every 16-wide MFMA slice; the chunk bytes (two
+//   8-byte pieces per fragment) are loaded 3 K-steps ahead, the super-block
+//   header one super-block ahead. Operands are dequantized one slice ahead of
+//   their MFMAs: value = s q - m is computed as s (1024 + q) + (-m - 1024 s)
+//   on the f16 1024 + q that a byte permute builds from the nibble
+//   (v_fma_mix, f32 arithmetic, one rounding to f16); high nibbles use
+//   s / 16 on 1024 + 16 q.
+// ---------------------------------------------------------------------------
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int kKsThreads = 512;
+constexpr int kKsBM = 128, kKsBN = 256;
+constexpr int kKsStage = kKsBM * 128;  // bytes per A stage
+constexpr int kKsDma = 4;              // 1 KB buffer_load ... lds per wave per stage
+
+__device__ inline void lds_dma16(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t offset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(lds), 16,
+                                           static_cast<int>(offset), 0, 0, 0);
+}
+
+// gfx9 s_waitcnt immediate for vmcnt(n) alone (expcnt 7, lgkmcnt 15 = no wait)
+constexpr int wait_vmcnt(int n) { return (n & 15) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
+
+// Work-group barrier without the memory fence __syncthreads() adds (which
+// waits for every outstanding load); the clobber keeps memory operations on
+// their side of it.
+__device__ inline void wg_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// f16 pair (lo, hi) = s * x.lo + c, s * x.hi + c for the f16 halves of x,
+// computed in f32 and rounded once.
+__device__ inline uint32_t fma_mix_pair(float s, uint32_t x, float c) {
+  uint32_t r;
+  asm("v_fma_mixlo_f16 %0, %1, %2, %3 op_sel_hi:[0,1,0]" : "=v"(r) : "v"(s), "v"(x), "v"(c));
+  asm("v_fma_mixhi_f16 %0, %1, %2, %3 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "+v"(r) : "v"(s), "v"(x), "v"(c));
+  return r;
+}
+
+struct KsScales {
+  float s[2][2], c[2][2];  // [run of the chunk][fragment]
+};
+
+// Scales of chunk C (runs 2C, 2C + 1) for both fragments.
+template <int C>
+__device__ inline void ks_scales(const uint4 (&hdr)[2], KsScales& cs) {
+#pragma unroll
+  for (int f = 0; f < 2; ++f) {
+    const Q4kSixBit six = q4k_six_bit(hdr[f]);
+    uint32_t sc0, mm0, sc1, mm1;
+    q4k_sc_m(six, 2 * C, sc0, mm0);
+    q4k_sc_m(six, 2 * C + 1, sc1, mm1);
+    const float d = half_bits(hdr[f].x), dmin = half_bits(hdr[f].x >> 16);
+    const float s0 = d * static_cast<float>(sc0), s1 = d * static_cast<float>(sc1) * 0.0625f;
+    cs.s[0][f] = s0;
+    cs.s[1][f] = s1;
+    cs.c[0][f] = fmaf(-1024.0f, s0, -(dmin * static_cast<float>(mm0)));
+    cs.c[1][f] = fmaf(-1024.0f, s1, -(dmin * static_cast<float>(mm1)));
+  }
+}
+
+// Slice SL (16 K values) of a chunk: run SL >> 1, chunk bytes 16 (SL & 1) + 8 kh
+// .. + 7 (q[f] = the two 8-byte pieces: .xy bytes 8 kh.., .zw bytes 16 + 8 kh..).
+template <int SL>
+__device__ inline void ks_slice(const uint4 (&q)[2], const KsScales& cs, half8 (&bop)[2]) {
+  constexpr int run = SL >> 1;
+  const uint32_t mask = run ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
+#pragma unroll
+  for (int f = 0; f < 2; ++f) {
+    const uint32_t x0 = ((SL & 1) ? q[f].z : q[f].x) & mask, x1 = ((SL & 1) ? q[f].w : q[f].y) & mask;
+    const float s = cs.s[run][f], c = cs.c[run][f];
+    uint32_t p[4];
+    // bytes (x.b0, 0x64, x.b1, 0x64) and (x.b2, 0x64, x.b3, 0x64): f16 1024 + byte
+    p[0] = fma_mix_pair(s, __builtin_amdgcn_perm(0x64646464u, x0, 0x04010400u), c);
+    p[1] = fma_mix_pair(s, __builtin_amdgcn_perm(0x64646464u, x0, 0x04030402u), c);
+    p[2] = fma_mix_pair(s, __builtin_amdgcn_perm(0x64646464u, x1, 0x04010400u), c);
+    p[3] = fma_mix_pair(s, __builtin_amdgcn_perm(0x64646464u, x1, 0x04030402u), c);
+    bop[f] = *reinterpret_cast<half8*>(p);
+  }
+}
+
+__global__ __launch_bounds__(kKsThreads) void gemm_ks_kernel(const uint8_t* __restrict__ w, int nb, uint64_t rows,
+                                                              uint64_t rows_padded, const uint16_t* __restrict__ a16,
+                                                              uint64_t m_rows, float* __restrict__ y,
+                                                              const float* __restrict__ addend,
+                                                              uint64_t addend_stride) {
+  constexpr int MF = 4, NF = 2, D = kKsDma;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * 4 * kKsStage];  // [kw][stage]
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int nw = wave & 3, kw = wave >> 2;
+  const int l32 = lane & 31, kh = lane >> 5;
+  const uint64_t m0 = static_cast<uint64_t>(blockIdx.y) * kKsBM;
+  const uint64_t n0 = static_cast<uint64_t>(blockIdx.x) * kKsBN + static_cast<uint64_t>(nw) * 64;
+  const uint64_t K = static_cast<uint64_t>(nb) * 256;
+  const int nbh = (nb + 1) / 2, sb0 = kw * nbh;
+  const int sb_end = sb0 + nbh < nb ? sb0 + nbh : nb;  // this half's super-blocks [sb0, sb_end)
+  const int ksteps = 4 * nbh;                          // K-steps per half (both halves run as many)
+  uint8_t* const ring = lds + kw * 4 * kKsStage;
+  auto swz = [](int row) { return (row >> 1) & 7; };
+
+  // A: the tile's rows as one buffer resource (rows past m_rows read zeros)
+  const uint64_t a_rows = m_rows - m0 < static_cast<uint64_t>(kKsBM) ? m_rows - m0 : kKsBM;
+  const __amdgpu_buffer_rsrc_t rsA = buffer_rsrc(a16 + m0 * K, static_cast<uint32_t>(a_rows * K * 2));
+  uint32_t a_off[D];  // this lane's 16 bytes of each of its DMA instructions: row, swizzled chunk
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    const int row = 8 * (nw * D + d) + (lane >> 3), cs = lane & 7;
+    a_off[d] = static_cast<uint32_t>(row * K * 2 + (cs ^ swz(row)) * 16);
+  }
+  uint32_t a_rd[4][MF];  // fragment i, slice sl: row 32 i + l32, chunk 2 sl + kh
+#pragma unroll
+  for (int sl = 0; sl < 4; ++sl)
+#pragma unroll
+    for (int i = 0; i < MF; ++i) {
+      const int row = 32 * i + l32, c = 2 * sl + kh;
+      a_rd[sl][i] = row * 128 + ((c ^ swz(row)) * 16);
+    }
+
+  // B: this wave's 64 weight rows = 8 row groups
+  const uint64_t groups = rows_padded / 8, group_bytes = static_cast<uint64_t>(nb) * kQ4kTileBytes;
+  const uint64_t wg0 = n0 / 8;
+  const uint64_t wspan = wg0 < groups ? (groups - wg0 < 4 * NF ? groups - wg0 : 4 * NF) * group_bytes : 0;
+  const __amdgpu_buffer_rsrc_t rsB =
+      buffer_rsrc(w + (wg0 < groups ? wg0 : 0) * group_bytes, static_cast<uint32_t>(wspan));
+  uint32_t b_lane[NF];
+#pragma unroll
+  for (int f = 0; f < NF; ++f) {
+    const int nl = 32 * f + l32;
+    b_lane[f] = static_cast<uint32_t>((nl >> 3) * group_bytes) + (nl & 7) * 16;
+  }
+  // local K-step j = chunk j % 4 of super-block sb0 + j / 4
+  auto load_chunk = [&](uint4 (&q)[NF], int j) {
+    const int sb = sb0 + j / 4, c = j % 4;
+    const bool ok = j < ksteps && sb < sb_end;
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+      const uint32_t t = b_lane[f] + static_cast<uint32_t>(sb) * kQ4kTileBytes + 128 * (1 + 2 * c) + 8 * kh;
+      const uint2 lo = buffer_ld8(rsB, ok ? t : kBufferNone);
+      const uint2 hi = buffer_ld8(rsB, ok ? t + 128 : kBufferNone);
+      q[f] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+    }
+  };
+  auto load_hdr = [&](uint4 (&h)[NF], int bl) {
+    const int sb = sb0 + bl;
+    const bool ok = bl < nbh && sb < sb_end;
+#pragma unroll
+    for (int f = 0; f < NF; ++f)
+      h[f] = buffer_ld16(rsB, ok ? b_lane[f] + static_cast<uint32_t>(sb) * kQ4kTileBytes : kBufferNone);
+  };
+  auto dma = [&](int stage, int j) {
+    const bool live = j < ksteps && sb0 + j / 4 < sb_end;
+    const uint32_t kglob = static_cast<uint32_t>(4 * sb0 + j);
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+      lds_dma16(rsA, ring + stage * kKsStage + (nw * D + d) * 1024, live ? a_off[d] + kglob * 128 : kBufferNone);
+  };
+  auto read_a = [&](int stage, int sl, half8 (&dst)[MF]) {
+#pragma unroll
+    for (int i = 0; i < MF; ++i) dst[i] = *reinterpret_cast<const half8*>(ring + stage * kKsStage + a_rd[sl][i]);
+  };
+
+  floatx16 acc[MF][NF];
+#pragma unroll
+  for (int i = 0; i < MF; ++i)
+#pragma unroll
+    for (int f = 0; f < NF; ++f)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][f][e] = 0.f;
+
+  uint4 hb[2][NF];  // headers of the even / odd local super-blocks
+  uint4 qb[4][NF];  // chunk bytes, buffer j % 4
+  // issue order (vmcnt): header, chunks 0..2, stages 0..2
+  load_hdr(hb[0], 0);
+  load_chunk(qb[0], 0);
+  load_chunk(qb[1], 1);
+  load_chunk(qb[2], 2);
+  dma(0, 0);
+  dma(1, 1);
+  dma(2, 2);
+  __builtin_amdgcn_s_waitcnt(wait_vmcnt(2 * D));  // stage 0 (and every B load) complete
+  wg_barrier();
+  half8 af[MF], an[MF], bc[NF], bn[NF];
+  read_a(0, 0, af);
+  KsScales sc_cur, sc_nxt;
+  ks_scales<0>(hb[0], sc_cur);
+  ks_slice<0>(qb[0], sc_cur, bc);
+
+  // Slice SL of K-step j = 4 bl + C: read the next slice's A, dequantize the
+  // next slice's B, 8 MFMAs on the current ones.
+#define MQ_KS_SLICE(C, HB, SL)                                                                 \
+  {                                                                                            \
+    if (SL < 3) read_a(C, SL + 1, an); else read_a((C + 1) % 4, 0, an);                        \
+    if (SL < 3) {                                                                              \
+      ks_slice<(SL + 1) % 4>(qb[C], sc_cur, bn);                                               \
+    } else {                                                                                   \
+      if (C < 3) ks_scales<(C + 1) % 4>(hb[HB], sc_nxt); else ks_scales<0>(hb[HB ^ 1], sc_nxt); \
+      ks_slice<0>(qb[(C + 1) % 4], sc_nxt, bn);                                                \
+    }                                                                                          \
+    _Pragma("unroll") for (int i = 0; i < MF; ++i)                                             \
+      _Pragma("unroll") for (int f = 0; f < NF; ++f)                                           \
+        acc[i][f] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bc[f], acc[i][f], 0, 0, 0);  \
+    _Pragma("unroll") for (int i = 0; i < MF; ++i) af[i] = an[i];                              \
+    _Pragma("unroll") for (int f = 0; f < NF; ++f) bc[f] = bn[f];                              \
+  }
+  // K-step j = 4 bl + C: chunk bytes in qb[C], header of super-block bl in hb[HB].
+  // Issue order per K-step: chunk j + 3 (4 loads), at C == 1 header bl + 1 (2),
+  // then after two slices the wait for stage j + 1, the barrier and stage j + 3
+  // (4 DMAs). At that wait the newest 8 loads are this K-step's B loads and
+  // (part of) stage j + 2, so vmcnt(8) completes stage j + 1 for this wave; the
+  // barrier makes it complete for all waves of the half.
+#define MQ_KS_STEP(C, HB)                                                                      \
+  {                                                                                            \
+    const int j = 4 * bl + C;                                                                  \
+    load_chunk(qb[(C + 3) % 4], j + 3);                                                        \
+    if (C == 1) load_hdr(hb[HB ^ 1], bl + 1);                                                  \
+    MQ_KS_SLICE(C, HB, 0)                                                                      \
+    MQ_KS_SLICE(C, HB, 1)                                                                      \
+    __builtin_amdgcn_s_waitcnt(wait_vmcnt(2 * D));                                             \
+    wg_barrier();                                                                              \
+    dma((C + 3) % 4, j + 3);                                                                   \
+    MQ_KS_SLICE(C, HB, 2)                                                                      \
+    MQ_KS_SLICE(C, HB, 3)                                                                      \
+    sc_cur = sc_nxt;                                                                           \
+  }
+  // two super-blocks per iteration (header buffers alternate); a half with an
+  // odd count runs one super-block of zeros (every load past the half reads 0)
+  for (int bl = 0; bl < nbh; bl += 2) {
+    MQ_KS_STEP(0, 0)
+    MQ_KS_STEP(1, 0)
+    MQ_KS_STEP(2, 0)
+    MQ_KS_STEP(3, 0)
+    ++bl;
+    MQ_KS_STEP(0, 1)
+    MQ_KS_STEP(1, 1)
+    MQ_KS_STEP(2, 1)
+    MQ_KS_STEP(3, 1)
+    --bl;
+  }
+#undef MQ_KS_STEP
+#undef MQ_KS_SLICE
+
+  // K halves summed through LDS: wave (nw, 1) hands its tile to wave (nw, 0).
+  // Every wave's DMAs (including the zero-filled ones past the end) must land
+  // before the ring is reused.
+  __builtin_amdgcn_s_waitcnt(wait_vmcnt(0));
+  wg_barrier();
+  float4* red = reinterpret_cast<float4*>(lds + nw * 32768);
+  if (kw == 1) {
+#pragma unroll
+    for (int i = 0; i < MF; ++i)
+#pragma unroll
+      for (int f = 0; f < NF; ++f)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          red[((i * NF + f) * 4 + g) * 64 + lane] =
+              make_float4(acc[i][f][4 * g], acc[i][f][4 * g + 1], acc[i][f][4 * g + 2], acc[i][f][4 * g + 3]);
+  }
+  wg_barrier();
+  if (kw == 0) {
+    // D layout (32 x 32): lane holds column l32, rows 8 g + 4 kh + e of fragment element 4 g + e
+#pragma unroll
+    for (int i = 0; i < MF; ++i)
+#pragma unroll
+      for (int f = 0; f < NF; ++f) {
+        const uint64_t col = n0 + 32 * f + l32;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const float4 o = red[((i * NF + f) * 4 + g) * 64 + lane];
+          const float ov[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint64_t row = m0 + 32 * i + 8 * g + 4 * kh + e;
+            if (row < m_rows && col < rows) {
+              float v = acc[i][f][4 * g + e] + ov[e];
+              if (addend) v = v + addend[row * addend_stride + col];
+              y[row * rows + col] = v;
+            }
+          }
+        }
+      }
+  }
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -3042,7 +3340,9 @@ uint64_t tiles(uint64_t rows, uint64_t m, uint64_t bn, uint64_t bm) {
 
 }  // namespace
 
-int gemm_default_variant(uint64_t rows, uint64_t m) {
+int gemm_default_variant(int type, uint64_t rows, uint64_t m) {
+  // Q4_K: the K-split form once its 128 x 256 tiles cover most CUs.
+  if (type == kTypeQ4K && tiles(rows, m, kKsBN, kKsBM) >= 160) return 5;
   // Register-B 128 x 128 tiles (two work-groups per CU fit, 2 waves per
   // SIMD); the 128 x 256 tile only once there are work-groups for every CU
   // several times over.
@@ -3070,8 +3370,15 @@ void launch_gemm(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, uin
         return;
     }
   }
-  if (variant == 0) variant = gemm_default_variant(rows, m);
+  if (variant == 0) variant = gemm_default_variant(type, rows, m);
+  if (variant == 5 && type != kTypeQ4K) variant = 3;
   switch (variant) {
+    case 5: {
+      dim3 ks_grid(static_cast<unsigned>((rows + kKsBN - 1) / kKsBN), static_cast<unsigned>((m + kKsBM - 1) / kKsBM));
+      hipLaunchKernelGGL(gemm_ks_kernel, ks_grid, dim3(kKsThreads), 0, stream, tiled, static_cast<int>(nb), rows,
+                         rows_padded, a16, m, y, addend, addend_stride);
+      return;
+    }
     case 2:
       launch_gemm_rb<8, 4>(type, tiled, rows, nb, a16, m, y, addend, addend_stride, stream);
       return;

@@ -86,12 +86,14 @@ void launch_gemv_f32(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb,
 
 // Prefill GEMM on MFMA: y[m][rows] = a16[m][K] . dequant(W)^T, f32 out.
 // variant 1: B dequantized through LDS (128 x 128 tiles); 2, 3, 4: B in
-// registers with 128 x 256, 128 x 128 and 64 x 256 tiles; 0: choose.
-// k = the logical row length; plane formats always take variant 1.
+// registers with 128 x 256, 128 x 128 and 64 x 256 tiles; 5 (Q4_K): the
+// K-split form, 128 x 256 tiles of 8 waves; 0: choose.
+// k = the logical row length; plane formats whose rows end inside a group
+// take variant 1.
 void launch_gemm(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, uint64_t k,
                  const uint16_t* a16, uint64_t m, float* y, const float* addend, uint64_t addend_stride,
                  int variant, hipStream_t stream);
-int gemm_default_variant(uint64_t rows, uint64_t m);
+int gemm_default_variant(int type, uint64_t rows, uint64_t m);
 
 // Plane formats (Q8_0, Q4_0, IQ4_NL, Q5_K, Q6_K; layout in mq_device.h).
 // k is the logical row length (a multiple of the format's block), nb =

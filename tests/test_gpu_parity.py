@@ -215,6 +215,63 @@ def test_prefill_gemm(ctx, name, m, int8):
     assert np.isfinite(got).all()
 
 
+@pytest.fixture(scope="module")
+def ks_ctx():
+    """A context whose GEMMs all take the Q4_K K-split form (variant 5),
+    whatever the shape."""
+    import os
+
+    old = os.environ.get("MQ_GEMM_VARIANT")
+    os.environ["MQ_GEMM_VARIANT"] = "5"
+    try:
+        c = mg.Context(0)
+    finally:
+        if old is None:
+            del os.environ["MQ_GEMM_VARIANT"]
+        else:
+            os.environ["MQ_GEMM_VARIANT"] = old
+    yield c
+    c.close()
+
+
+@pytest.mark.parametrize("m,n,k", [(200, 300, 768), (17, 520, 256), (129, 257, 1280), (512, 1024, 4096),
+                                   (40, 8, 512)])
+@pytest.mark.parametrize("int8", [True, False])
+def test_gemm_k_split_form_ragged(ks_ctx, m, n, k, int8):
+    """The K-split GEMM on ragged M and N (partial 128 x 256 tiles, a row
+    group of zero padding) and on odd super-block counts (K = 768, 1280: one
+    K half ends with a block of zeros; K = 256: the second half has none)."""
+    w = packed(Q4_K, n, k, 5 + m + n)
+    a = activations(m, k, 70 + m)
+    h = ks_ctx.upload(Q4_K, n, k, w)
+    try:
+        got = ks_ctx.matmul(h, a, int8=int8)
+    finally:
+        h.release()
+    assert_row_tolerance(got, expected(Q4_K, w, n, k, a, int8), f"{m}x{n}x{k}")
+
+
+def test_gemm_k_split_form_residual(ks_ctx):
+    """matmul-residual through the K-split epilogue: y = x W^T + r with r of
+    one broadcast row and of M rows."""
+    m, n, k = 160, 384, 1024
+    w = packed(Q4_K, n, k, 9)
+    a = activations(m, k, 71)
+    h = ks_ctx.upload(Q4_K, n, k, w)
+    try:
+        base = expected(Q4_K, w, n, k, a, True)
+        x = dev(a)
+        for r_rows in (1, m):
+            r = activations(r_rows, n, 72 + r_rows)
+            rd = dev(r)
+            y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+            ks_ctx.matmul_add_dev(h, x.data_ptr(), m, k, rd.data_ptr(), r_rows, y.data_ptr())
+            torch.cuda.synchronize()
+            assert_row_tolerance(y.cpu().numpy(), (base + r).astype(np.float32), f"residual rows {r_rows}")
+    finally:
+        h.release()
+
+
 # ---- properties at full size -------------------------------------------------------
 
 @pytest.mark.parametrize("m", [1, 8, 512])
