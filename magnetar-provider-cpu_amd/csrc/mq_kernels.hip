@@ -2596,9 +2596,23 @@ constexpr int kKsBM = 128, kKsBN = 256;
 constexpr int kKsStage = kKsBM * 128;  // bytes per A stage
 constexpr int kKsDma = 4;              // 1 KB buffer_load ... lds per wave per stage
 
-__device__ inline void lds_dma16(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t offset) {
+// 16 bytes per lane from a buffer straight into LDS (lane l writes lds + 16 l);
+// voffset per lane, soffset uniform.
+__device__ inline void lds_dma16_so(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voffset, uint32_t soffset) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(lds), 16,
-                                           static_cast<int>(offset), 0, 0, 0);
+                                           static_cast<int>(voffset), static_cast<int>(soffset), 0, 0);
+}
+
+__device__ inline uint2 buffer_ld8_so(__amdgpu_buffer_rsrc_t r, uint32_t voffset, uint32_t soffset) {
+  typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+  const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, static_cast<int>(voffset), static_cast<int>(soffset), 0);
+  return make_uint2(v.x, v.y);
+}
+
+__device__ inline uint4 buffer_ld16_so(__amdgpu_buffer_rsrc_t r, uint32_t voffset, uint32_t soffset) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(voffset), static_cast<int>(soffset), 0);
+  return make_uint4(v.x, v.y, v.z, v.w);
 }
 
 // gfx9 s_waitcnt immediate for vmcnt(n) alone (expcnt 7, lgkmcnt 15 = no wait)
@@ -2710,30 +2724,36 @@ __global__ __launch_bounds__(kKsThreads) void gemm_ks_kernel(const uint8_t* __re
     b_lane[f] = static_cast<uint32_t>((nl >> 3) * group_bytes) + (nl & 7) * 16;
   }
   // local K-step j = chunk j % 4 of super-block sb0 + j / 4
+  // Per-lane offsets stay in VGPRs; the K position goes in the uniform
+  // soffset, and steps past this half's super-blocks read through a
+  // zero-length resource (zeros), so the loads cost no per-lane selects.
+  const __amdgpu_buffer_rsrc_t rsZ = buffer_rsrc(w, 0);
+  uint32_t b_q[NF];
+#pragma unroll
+  for (int f = 0; f < NF; ++f) b_q[f] = b_lane[f] + 128 + 8 * kh;
   auto load_chunk = [&](uint4 (&q)[NF], int j) {
     const int sb = sb0 + j / 4, c = j % 4;
-    const bool ok = j < ksteps && sb < sb_end;
+    const __amdgpu_buffer_rsrc_t rs = j < ksteps && sb < sb_end ? rsB : rsZ;
+    const uint32_t so = static_cast<uint32_t>(sb) * kQ4kTileBytes + 256 * c;
 #pragma unroll
     for (int f = 0; f < NF; ++f) {
-      const uint32_t t = b_lane[f] + static_cast<uint32_t>(sb) * kQ4kTileBytes + 128 * (1 + 2 * c) + 8 * kh;
-      const uint2 lo = buffer_ld8(rsB, ok ? t : kBufferNone);
-      const uint2 hi = buffer_ld8(rsB, ok ? t + 128 : kBufferNone);
+      const uint2 lo = buffer_ld8_so(rs, b_q[f], so);
+      const uint2 hi = buffer_ld8_so(rs, b_q[f] + 128, so);
       q[f] = make_uint4(lo.x, lo.y, hi.x, hi.y);
     }
   };
   auto load_hdr = [&](uint4 (&h)[NF], int bl) {
     const int sb = sb0 + bl;
-    const bool ok = bl < nbh && sb < sb_end;
+    const __amdgpu_buffer_rsrc_t rs = bl < nbh && sb < sb_end ? rsB : rsZ;
 #pragma unroll
-    for (int f = 0; f < NF; ++f)
-      h[f] = buffer_ld16(rsB, ok ? b_lane[f] + static_cast<uint32_t>(sb) * kQ4kTileBytes : kBufferNone);
+    for (int f = 0; f < NF; ++f) h[f] = buffer_ld16_so(rs, b_lane[f], static_cast<uint32_t>(sb) * kQ4kTileBytes);
   };
+  const __amdgpu_buffer_rsrc_t rsAZ = buffer_rsrc(a16, 0);
   auto dma = [&](int stage, int j) {
-    const bool live = j < ksteps && sb0 + j / 4 < sb_end;
-    const uint32_t kglob = static_cast<uint32_t>(4 * sb0 + j);
+    const __amdgpu_buffer_rsrc_t rs = j < ksteps && sb0 + j / 4 < sb_end ? rsA : rsAZ;
+    const uint32_t so = static_cast<uint32_t>(4 * sb0 + j) * 128;
 #pragma unroll
-    for (int d = 0; d < D; ++d)
-      lds_dma16(rsA, ring + stage * kKsStage + (nw * D + d) * 1024, live ? a_off[d] + kglob * 128 : kBufferNone);
+    for (int d = 0; d < D; ++d) lds_dma16_so(rs, ring + stage * kKsStage + (nw * D + d) * 1024, a_off[d], so);
   };
   auto read_a = [&](int stage, int sl, half8 (&dst)[MF]) {
 #pragma unroll
