@@ -36,6 +36,11 @@ extern "C" {
 #define MQ_TYPE_Q6_K 14u
 #define MQ_TYPE_IQ4_NL 20u
 #define MQ_TYPE_IQ4_XS 23u
+#define MQ_TYPE_IQ2_XXS 16u
+#define MQ_TYPE_IQ2_XS 17u
+#define MQ_TYPE_IQ3_XXS 18u
+#define MQ_TYPE_IQ3_S 21u
+#define MQ_TYPE_IQ2_S 22u
 
 /* Status codes. */
 #define MQ_OK 0
@@ -66,15 +71,28 @@ void mq_destroy(mq_ctx *ctx);
  * Mirrors the `reason` text of KernelError (src/native/mod.rs:119-124). */
 const char *mq_last_error(mq_ctx *ctx);
 
+/* Fills the context device's copy of the IQ2 / IQ3 grid tables that the
+ * grid formats decode with (`iq_grids::IQ2XXS_GRID` 256, `IQ2XS_GRID` 512,
+ * `IQ2S_GRID` 1024 u64 entries of 8 magnitude bytes; `IQ3XXS_GRID` 256,
+ * `IQ3S_GRID` 512 u32 entries of 4), synchronously; every context on the
+ * device shares them. The reference reads these statics from the external
+ * magnetar-provider-api crate (src/native/quant.rs:14, 1057-1061): a Rust
+ * binding passes them once at start-up. Waits for this context's queued
+ * work first; work queued on other streams must not be running. */
+int mq_set_iq_grids(mq_ctx *ctx, const uint64_t *iq2xxs, const uint64_t *iq2xs, const uint64_t *iq2s,
+                    const uint32_t *iq3xxs, const uint32_t *iq3s);
+
 /* Uploads a packed weight: `stored_rows` rows of `stored_cols` values,
  * `len` = stored_rows * stored_cols / block_values * block_bytes checkpoint
  * bytes (Q8_0 32 / 34, Q4_0 and IQ4_NL 32 / 18, Q2_K 256 / 84, Q3_K
  * 256 / 110, Q4_K 256 / 144, Q5_K 256 / 176, Q6_K 256 / 210, IQ4_XS
- * 256 / 136); stored_cols must be whole
+ * 256 / 136, IQ2_XXS 256 / 66, IQ2_XS 256 / 74, IQ2_S 256 / 82, IQ3_XXS
+ * 256 / 98, IQ3_S 256 / 110); stored_cols must be whole
  * blocks. transposed != 0: the stored rows are the logical [k, n] weight's
  * output columns; 0: an untransposed weight or table whose stored rows are
  * its logical rows. Returns MQ_DECLINED for a type without a GPU path
- * (the IQ2 / IQ3 grid formats), so the caller keeps the f32 path.
+ * (any other type, and the IQ2 / IQ3 grid formats until mq_set_iq_grids
+ * has run on the context's device), so the caller keeps the f32 path.
  * Replaces
  * `write_packed_weight_tensor` -> `PackedWeightWrite::{Stored,Declined}`
  * (src/native/mod.rs:638-653) and `PackedWeight::new` (external,

@@ -10,6 +10,7 @@
 #include <cstring>
 #include <map>
 #include <mutex>
+#include <set>
 #include <vector>
 #include <string>
 #include <thread>
@@ -96,10 +97,21 @@ int hip_fail(mq_ctx* ctx, hipError_t e, const char* where) {
   } while (0)
 
 bool known_type(uint32_t type) {
-  return type == MQ_TYPE_Q4_K || type == MQ_TYPE_IQ4_XS || mq::is_plane_format(static_cast<int>(type));
+  return type == MQ_TYPE_Q4_K || type == MQ_TYPE_IQ4_XS || mq::is_plane_format(static_cast<int>(type)) ||
+         mq::is_grid_format(static_cast<int>(type));
 }
 
 bool plane_type(uint32_t type) { return mq::is_plane_format(static_cast<int>(type)); }
+bool grid_type(uint32_t type) { return mq::is_grid_format(static_cast<int>(type)); }
+
+// Devices whose copy of the IQ2 / IQ3 grid tables has been filled.
+std::mutex g_grid_mu;
+std::set<int> g_grid_devices;
+
+bool grids_ready(int device) {
+  std::lock_guard<std::mutex> lock(g_grid_mu);
+  return g_grid_devices.count(device) != 0;
+}
 
 class DeviceGuard {
  public:
@@ -237,6 +249,23 @@ int gemv_locked(mq_ctx* ctx, const Weight& w, const float* x, uint64_t m, uint64
                 hipStream_t stream, const float* addend, uint64_t addend_stride) {
   mq::GemvSplitK sk;
   int rc = MQ_OK;
+  if (grid_type(w.type)) {
+    int8_t* values = nullptr;
+    float* scales = nullptr;
+    if (int8) {
+      const size_t vb = align256(m * k), sb = align256(m * k / 32 * 4), hb = align256(m * k / 32 * 8);
+      rc = acquire_workspace(ctx, stream, vb + sb + hb);
+      if (rc) return rc;
+      auto* base = static_cast<uint8_t*>(ctx->ws);
+      values = reinterpret_cast<int8_t*>(base);
+      scales = reinterpret_cast<float*>(base + vb);
+      mq::launch_quantize_activations(x, m, k, values, scales, reinterpret_cast<int32_t*>(base + vb + sb), nullptr, 1,
+                                      stream);
+    }
+    mq::launch_gemv_grid(static_cast<int>(w.type), w.dev, w.nb, w.rows, values, scales, x, m, int8 ? 1 : 0, y, addend,
+                         addend_stride, stream);
+    return MQ_OK;
+  }
   if (int8) {
     rc = order_stream(ctx, stream);
     if (!rc) rc = acquire_splitk(ctx, stream, w, m, sk);
@@ -298,7 +327,8 @@ int matmul_locked(mq_ctx* ctx, const Weight& w, const float* x, uint64_t m, uint
     if (rc) return rc;
     mq::launch_axpy(static_cast<int>(w.type), w.dev, w.nb, k, n, x, m, y, addend, addend_stride,
                     static_cast<float*>(ctx->ws), ks, stream);
-  } else if (m <= kGemvChunkRows || k < kGemmMinK) {
+  } else if (m <= kGemvChunkRows || k < kGemmMinK || grid_type(w.type)) {
+    // (the grid formats have no MFMA form: their prefill is 8-row GEMVs)
     for (uint64_t r0 = 0; r0 < m; r0 += kGemvMaxRows) {
       const uint64_t mc = m - r0 < kGemvMaxRows ? m - r0 : kGemvMaxRows;
       const float* ad = addend ? addend + (addend_stride ? r0 * w.rows : 0) : nullptr;
@@ -440,12 +470,35 @@ const char* mq_last_error(mq_ctx* ctx) {
   return ctx->errors[std::this_thread::get_id()].c_str();
 }
 
+int mq_set_iq_grids(mq_ctx* ctx, const uint64_t* iq2xxs, const uint64_t* iq2xs, const uint64_t* iq2s,
+                    const uint32_t* iq3xxs, const uint32_t* iq3s) {
+  if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_set_iq_grids: null context");
+  if (!iq2xxs || !iq2xs || !iq2s || !iq3xxs || !iq3s) return fail(ctx, MQ_ERR_ARGUMENT, "mq_set_iq_grids: null table");
+  std::vector<uint8_t> tables(mq::kGridTableBytes);
+  std::memcpy(tables.data() + mq::kGridIq2Xxs, iq2xxs, 256 * sizeof(uint64_t));
+  std::memcpy(tables.data() + mq::kGridIq2Xs, iq2xs, 512 * sizeof(uint64_t));
+  std::memcpy(tables.data() + mq::kGridIq2S, iq2s, 1024 * sizeof(uint64_t));
+  std::memcpy(tables.data() + mq::kGridIq3Xxs, iq3xxs, 256 * sizeof(uint32_t));
+  std::memcpy(tables.data() + mq::kGridIq3S, iq3s, 512 * sizeof(uint32_t));
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  DeviceGuard guard(ctx->device);
+  // queued work of this context may still read the previous tables
+  MQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  MQ_HIP(ctx, mq::grid_tables_upload(tables.data(), ctx->stream));
+  std::lock_guard<std::mutex> glock(g_grid_mu);
+  g_grid_devices.insert(ctx->device);
+  return MQ_OK;
+}
+
 int mq_weight_upload(mq_ctx* ctx, uint32_t gguf_type, uint64_t stored_rows, uint64_t stored_cols, int transposed,
                      const uint8_t* bytes, size_t len, uint64_t* handle) {
   if (!ctx || !handle) return fail(ctx, MQ_ERR_ARGUMENT, "mq_weight_upload: null argument");
   *handle = 0;
   if (!known_type(gguf_type))
     return fail(ctx, MQ_DECLINED, "packed weight format " + std::to_string(gguf_type) + " has no GPU path");
+  if (grid_type(gguf_type) && !grids_ready(ctx->device))
+    return fail(ctx, MQ_DECLINED, "packed weight format " + std::to_string(gguf_type) +
+                                      " needs the IQ2 / IQ3 grid tables (mq_set_iq_grids) on this device");
   const int type = static_cast<int>(gguf_type);
   const uint64_t be = static_cast<uint64_t>(mq::block_values(type)), bb = static_cast<uint64_t>(mq::block_bytes_of(type));
   if (stored_rows == 0 || stored_cols == 0 || stored_cols % be != 0)
@@ -467,7 +520,21 @@ int mq_weight_upload(mq_ctx* ctx, uint32_t gguf_type, uint64_t stored_rows, uint
   w.nb = nb;
   w.rows_padded = (stored_rows + 7) / 8 * 8;
   w.transposed = transposed;
-  w.dev_bytes = w.rows_padded / 8 * nb * static_cast<uint64_t>(mq::tile_bytes(type));
+  w.dev_bytes = grid_type(gguf_type) ? len : w.rows_padded / 8 * nb * static_cast<uint64_t>(mq::tile_bytes(type));
+  if (grid_type(gguf_type)) {
+    // the checkpoint's blocks as they are
+    hipError_t e = hipMalloc(&w.dev, w.dev_bytes);
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipMalloc(weight)");
+    e = hipMemcpyAsync(w.dev, bytes, len, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+      (void)hipFree(w.dev);
+      return hip_fail(ctx, e, "mq_weight_upload");
+    }
+    *handle = ctx->next_handle++;
+    ctx->weights.emplace(*handle, w);
+    return MQ_OK;
+  }
   uint8_t* raw = nullptr;
   hipError_t e = hipMalloc(&raw, len);
   if (e != hipSuccess) return hip_fail(ctx, e, "hipMalloc(staging)");
@@ -633,6 +700,12 @@ int mq_matmul_prequantized_dev(mq_ctx* ctx, uint64_t handle, const int8_t* value
     return fail(ctx, MQ_ERR_ARGUMENT, "mq_matmul_prequantized_dev: null pointer");
   DeviceGuard guard(ctx->device);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (grid_type(w->type)) {
+    mq::launch_gemv_grid(static_cast<int>(w->type), w->dev, w->nb, w->rows, values_dev, scales_dev, nullptr, m, 1,
+                         y_dev, nullptr, 0, s);
+    MQ_HIP(ctx, hipGetLastError());
+    return MQ_OK;
+  }
   mq::GemvSplitK sk;
   rc = order_stream(ctx, s);
   if (!rc) rc = acquire_splitk(ctx, s, *w, m, sk);
@@ -674,6 +747,7 @@ int mq_matmul_f16_dev(mq_ctx* ctx, uint64_t handle, const uint16_t* a16_dev, uin
   if (rc) return rc;
   if (m == 0) return MQ_OK;
   if (!a16_dev || !y_dev) return fail(ctx, MQ_ERR_ARGUMENT, "mq_matmul_f16_dev: null pointer");
+  if (grid_type(w->type)) return fail(ctx, MQ_DECLINED, "the IQ2 / IQ3 grid formats have no f16 MFMA GEMM");
   DeviceGuard guard(ctx->device);
   hipStream_t s = static_cast<hipStream_t>(stream);
   mq::launch_gemm(static_cast<int>(w->type), w->dev, w->rows, w->nb, w->cols, a16_dev, m, y_dev, nullptr, 0,
@@ -690,7 +764,9 @@ int mq_dequantize_dev(mq_ctx* ctx, uint64_t handle, int logical, float* out_dev,
   if (!out_dev) return fail(ctx, MQ_ERR_ARGUMENT, "mq_dequantize_dev: null output");
   DeviceGuard guard(ctx->device);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (plane_type(w->type))
+  if (grid_type(w->type))
+    mq::launch_dequantize_grid(static_cast<int>(w->type), w->dev, w->rows, w->nb, logical, out_dev, s);
+  else if (plane_type(w->type))
     mq::launch_dequantize_planes(static_cast<int>(w->type), w->dev, w->rows, w->cols, w->nb, logical, out_dev, s);
   else
     mq::launch_dequantize(static_cast<int>(w->type), w->dev, w->rows, w->nb, logical, out_dev, s);
@@ -708,7 +784,9 @@ int mq_dequantize(mq_ctx* ctx, uint64_t handle, int logical, float* out) {
   const size_t bytes = w->rows * w->cols * sizeof(float);
   float* dev = nullptr;
   MQ_HIP(ctx, hipMalloc(&dev, bytes));
-  if (plane_type(w->type))
+  if (grid_type(w->type))
+    mq::launch_dequantize_grid(static_cast<int>(w->type), w->dev, w->rows, w->nb, logical, dev, ctx->stream);
+  else if (plane_type(w->type))
     mq::launch_dequantize_planes(static_cast<int>(w->type), w->dev, w->rows, w->cols, w->nb, logical, dev,
                                  ctx->stream);
   else
@@ -734,7 +812,7 @@ int mq_decode_matmul_dev(mq_ctx* ctx, uint64_t handle, const float* x_dev, uint6
   const uint32_t orient = w->transposed ? 0u : MQ_TRANSPOSE_B;  // stored rows are the outputs
   int rc = check_k(ctx, *w, k, orient);
   if (rc) return rc;
-  if (plane_type(w->type))
+  if (plane_type(w->type) || grid_type(w->type))
     return fail(ctx, MQ_DECLINED, "decode-step fusions cover Q4_K and IQ4_XS weights");
   if (f->norm_weight && !(f->norm_epsilon > 0.0f))
     return fail(ctx, MQ_ERR_SHAPE, "rmsnorm epsilon must be positive");

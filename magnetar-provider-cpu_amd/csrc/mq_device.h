@@ -62,6 +62,25 @@ constexpr int kTypeQ5K = 13;
 constexpr int kTypeQ6K = 14;
 constexpr int kTypeIq4Nl = 20;
 
+// IQ2 / IQ3 grid formats: the weight keeps the checkpoint's block order
+// (stored row after stored row, nb blocks each); their decode reads the
+// grid tables the caller supplies once per device.
+constexpr int kTypeIq2Xxs = 16;
+constexpr int kTypeIq2Xs = 17;
+constexpr int kTypeIq3Xxs = 18;
+constexpr int kTypeIq3S = 21;
+constexpr int kTypeIq2S = 22;
+
+__host__ __device__ constexpr bool is_grid_format(int type) {
+  return type == kTypeIq2Xxs || type == kTypeIq2Xs || type == kTypeIq2S || type == kTypeIq3Xxs || type == kTypeIq3S;
+}
+
+// Byte offsets of each grid table in the device copy: IQ2_XXS 256, IQ2_XS
+// 512 and IQ2_S 1024 entries of 8 magnitudes, IQ3_XXS 256 and IQ3_S 512
+// entries of 4.
+constexpr int kGridIq2Xxs = 0, kGridIq2Xs = 2048, kGridIq2S = 6144, kGridIq3Xxs = 14336, kGridIq3S = 15360;
+constexpr int kGridTableBytes = 17408;
+
 __host__ __device__ constexpr bool is_plane_format(int type) {
   return type == kTypeQ8_0 || type == kTypeQ4_0 || type == kTypeIq4Nl || type == kTypeQ5K || type == kTypeQ6K ||
          type == kTypeQ2K || type == kTypeQ3K;
@@ -98,6 +117,11 @@ __host__ __device__ constexpr int block_bytes_of(int type) {
          : type == kTypeQ6K ? 210
          : type == kTypeQ2K ? 84
          : type == kTypeQ3K ? 110
+         : type == kTypeIq2Xxs ? 66
+         : type == kTypeIq2Xs ? 74
+         : type == kTypeIq2S ? 82
+         : type == kTypeIq3Xxs ? 98
+         : type == kTypeIq3S ? 110
          : kIq4xsBlockBytes;
 }
 

@@ -1509,7 +1509,6 @@ __global__ void repack_planes_kernel(const uint8_t* __restrict__ raw, uint64_t r
 template <int TYPE>
 __global__ void dequantize_planes_kernel(const uint8_t* __restrict__ tiled, uint64_t rows, uint64_t K, uint64_t nb,
                                          int logical, float* __restrict__ out) {
-  constexpr int P = plane_count(TYPE);
   const uint64_t runs = K / 32;
   const uint64_t t = blockIdx.x * static_cast<uint64_t>(blockDim.x) + threadIdx.x;
   if (t >= rows * runs) return;
@@ -1757,6 +1756,209 @@ __global__ __launch_bounds__(512) void gemv_planes_f32_kernel(const uint8_t* __r
 }
 
 // ---------------------------------------------------------------------------
+// IQ2 / IQ3 grid formats (src/native/quant.rs:207-277). A weight keeps the
+// checkpoint's blocks, stored row after stored row; every format's block is
+// an even number of bytes, so blocks are read with 16-bit loads. The grid
+// tables are one device-global copy per device, filled by the host
+// (mq_set_iq_grids) before any such weight is uploaded.
+// ---------------------------------------------------------------------------
+
+__device__ __attribute__((aligned(16))) uint8_t g_iq_grids[kGridTableBytes];
+
+__device__ inline uint32_t ld_u16(const uint8_t* p) { return *reinterpret_cast<const uint16_t*>(p); }
+__device__ inline uint32_t ld_u32_a2(const uint8_t* p) { return ld_u16(p) | (ld_u16(p + 2) << 16); }
+
+// `iq_signs`: the 7-bit index with its parity in bit 7 (an even number of
+// the 8 values is negated).
+__device__ inline uint32_t iq_sign_byte(uint32_t index) {
+  const uint32_t v = index & 0x7Fu;
+  return v | ((static_cast<uint32_t>(__builtin_popcount(v)) & 1u) << 7);
+}
+
+// One run of a grid format as `decode` produces it: 32 magnitudes (the grid
+// entries' bytes, 4 per word, read as i8), 32 sign bits (bit i negates value
+// i: `signed_grid`, quant.rs:60-69) and the two 16-value scales.
+struct GridRun {
+  uint32_t mag[8];
+  uint32_t signs;
+  float scale[2];
+};
+
+template <int TYPE>
+__device__ inline void grid_run(const uint8_t* __restrict__ blk, int run, GridRun& g) {
+  const float d = half_bits(ld_u16(blk));
+  const uint8_t* grids = g_iq_grids;
+  g.signs = 0;
+  if constexpr (TYPE == kTypeIq2Xxs) {
+    const uint32_t idx = ld_u32_a2(blk + 2 + 8 * run), aux = ld_u32_a2(blk + 6 + 8 * run);
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+      const uint2 e = *reinterpret_cast<const uint2*>(grids + kGridIq2Xxs + 8 * ((idx >> (8 * l)) & 0xFFu));
+      g.mag[2 * l] = e.x;
+      g.mag[2 * l + 1] = e.y;
+      g.signs |= iq_sign_byte(aux >> (7 * l)) << (8 * l);
+    }
+    g.scale[0] = g.scale[1] = d * (0.5f + static_cast<float>(aux >> 28)) * 0.25f;
+  } else if constexpr (TYPE == kTypeIq2Xs) {
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+      const uint32_t code = ld_u16(blk + 2 + 2 * (4 * run + l));
+      const uint2 e = *reinterpret_cast<const uint2*>(grids + kGridIq2Xs + 8 * (code & 511u));
+      g.mag[2 * l] = e.x;
+      g.mag[2 * l + 1] = e.y;
+      g.signs |= iq_sign_byte(code >> 9) << (8 * l);
+    }
+    const uint32_t sc = blk[66 + run];
+    g.scale[0] = d * (0.5f + static_cast<float>(sc & 0xFu)) * 0.25f;
+    g.scale[1] = d * (0.5f + static_cast<float>(sc >> 4)) * 0.25f;
+  } else if constexpr (TYPE == kTypeIq2S) {
+    const uint32_t qh = blk[66 + run];
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+      const uint32_t index = blk[2 + 4 * run + l] | (((qh >> (2 * l)) & 3u) << 8);
+      const uint2 e = *reinterpret_cast<const uint2*>(grids + kGridIq2S + 8 * index);
+      g.mag[2 * l] = e.x;
+      g.mag[2 * l + 1] = e.y;
+      g.signs |= static_cast<uint32_t>(blk[34 + 4 * run + l]) << (8 * l);
+    }
+    const uint32_t sc = blk[74 + run];
+    g.scale[0] = d * (0.5f + static_cast<float>(sc & 0xFu)) * 0.25f;
+    g.scale[1] = d * (0.5f + static_cast<float>(sc >> 4)) * 0.25f;
+  } else if constexpr (TYPE == kTypeIq3Xxs) {
+    const uint32_t aux = ld_u32_a2(blk + 66 + 4 * run);
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+      g.mag[2 * l] = *reinterpret_cast<const uint32_t*>(grids + kGridIq3Xxs + 4 * blk[2 + 8 * run + 2 * l]);
+      g.mag[2 * l + 1] = *reinterpret_cast<const uint32_t*>(grids + kGridIq3Xxs + 4 * blk[3 + 8 * run + 2 * l]);
+      g.signs |= iq_sign_byte(aux >> (7 * l)) << (8 * l);
+    }
+    g.scale[0] = g.scale[1] = d * (0.5f + static_cast<float>(aux >> 28)) * 0.5f;
+  } else {
+    static_assert(TYPE == kTypeIq3S, "grid format");
+    const uint32_t qh = blk[66 + run];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t index = blk[2 + 8 * run + i] | (((qh >> i) & 1u) << 8);
+      g.mag[i] = *reinterpret_cast<const uint32_t*>(grids + kGridIq3S + 4 * index);
+    }
+#pragma unroll
+    for (int l = 0; l < 4; ++l) g.signs |= static_cast<uint32_t>(blk[74 + 4 * run + l]) << (8 * l);
+    const uint32_t sc = (blk[106 + run / 2] >> (4 * (run % 2))) & 0xFu;
+    g.scale[0] = g.scale[1] = d * static_cast<float>(1 + 2 * sc);
+  }
+}
+
+// Value i of a decoded run: the magnitude as i8, negated (as i8) where its
+// sign bit is set.
+__device__ inline int grid_value(const GridRun& g, int i) {
+  const int8_t m = static_cast<int8_t>(byte_of(g.mag[i >> 2], i & 3));
+  return ((g.signs >> i) & 1u) ? static_cast<int8_t>(-m) : m;
+}
+
+// Bytes 0xFF where bit b of the 4-bit `s4` is set (byte b), else 0.
+__device__ inline uint32_t sign_mask4(uint32_t s4) { return (((s4 & 0xFu) * 0x00204081u) & 0x01010101u) * 0xFFu; }
+
+// Integer dots of a run with 32 int8 activations, per 16-value half:
+// sum(+-m a) = sum(m a) - 2 sum over the negated values of m a (exact in
+// int32; equal to the reference's i8 values for every magnitude but -128,
+// which no grid holds).
+__device__ inline void grid_dots(const GridRun& g, const uint32_t (&a)[8], int (&dot)[2]) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    int all = 0, neg = 0;
+#pragma unroll
+    for (int w = 4 * h; w < 4 * h + 4; ++w) {
+      all = sdot4(g.mag[w], a[w], all);
+      neg = sdot4(g.mag[w] & sign_mask4(g.signs >> (4 * w)), a[w], neg);
+    }
+    dot[h] = all - 2 * neg;
+  }
+}
+
+template <int TYPE>
+__global__ void dequantize_grid_kernel(const uint8_t* __restrict__ w, uint64_t rows, uint64_t nb, int logical,
+                                       float* __restrict__ out) {
+  constexpr int BB = block_bytes_of(TYPE);
+  const uint64_t runs = nb * 8, K = nb * 256;
+  const uint64_t t = blockIdx.x * static_cast<uint64_t>(blockDim.x) + threadIdx.x;
+  if (t >= rows * runs) return;
+  const uint64_t row = t / runs, u = t % runs;
+  GridRun g;
+  grid_run<TYPE>(w + (row * nb + (u >> 3)) * BB, static_cast<int>(u & 7), g);
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    const float v = g.scale[i >> 4] * static_cast<float>(grid_value(g, i));
+    const uint64_t col = 32 * u + i;
+    if (logical)
+      out[col * rows + row] = v;
+    else
+      out[row * K + col] = v;
+  }
+}
+
+// Decode GEMV of a grid format (m <= 8): one wave per stored row, lanes
+// over its runs, a fixed-order shuffle reduction. INT8: the reference's
+// int8 path (per half: scale * integer dot, times d_act per run); else its
+// f32 column loop (w = scale * q, acc += w * x per value).
+template <int TYPE, int M, bool INT8>
+__global__ __launch_bounds__(256) void gemv_grid_kernel(const uint8_t* __restrict__ w, uint64_t nb, uint64_t rows,
+                                                        const int8_t* __restrict__ xv, const float* __restrict__ xs,
+                                                        const float* __restrict__ xf, float* __restrict__ y,
+                                                        const float* __restrict__ addend, uint64_t addend_stride) {
+  constexpr int BB = block_bytes_of(TYPE);
+  const int lane = threadIdx.x & 63;
+  const uint64_t row = static_cast<uint64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;  // the whole wave
+  const uint64_t runs = nb * 8, K = nb * 256;
+  const uint8_t* base = w + row * nb * BB;
+  float acc[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) acc[m] = 0.0f;
+  for (uint64_t u = lane; u < runs; u += 64) {
+    GridRun g;
+    grid_run<TYPE>(base + (u >> 3) * BB, static_cast<int>(u & 7), g);
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      if constexpr (INT8) {
+        const uint4* ap = reinterpret_cast<const uint4*>(xv + m * K + 32 * u);
+        const uint4 a0 = ap[0], a1 = ap[1];
+        const uint32_t a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+        int dot[2];
+        grid_dots(g, a, dot);
+        float t = g.scale[0] * static_cast<float>(dot[0]);
+        t = t + g.scale[1] * static_cast<float>(dot[1]);
+        acc[m] += xs[m * runs + u] * t;
+      } else {
+        const float4* xp = reinterpret_cast<const float4*>(xf + m * K + 32 * u);
+#pragma unroll
+        for (int q4 = 0; q4 < 8; ++q4) {
+          const float4 xq = xp[q4];
+          const float xv4[4] = {xq.x, xq.y, xq.z, xq.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int i = 4 * q4 + e;
+            const float wv = g.scale[i >> 4] * static_cast<float>(grid_value(g, i));
+            acc[m] += wv * xv4[e];
+          }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) acc[m] += __shfl_xor(acc[m], off);
+  if (lane == 0) {
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      float v = acc[m];
+      if (addend) v = v + addend[m * addend_stride + row];
+      y[m * rows + row] = v;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Run u of stored row `row` as f32 values, any format: value = scale * q -
 // min with the product and difference each rounded once, bit for bit the
 // reference's `RunReader::read` + `dequantize_row` arithmetic
@@ -1767,8 +1969,13 @@ __device__ inline void row_run_values(const uint8_t* __restrict__ tiled, uint64_
                                       float (&v)[32]) {
   const uint64_t b = u >> 3;
   const int j = static_cast<int>(u & 7), r = static_cast<int>(row & 7);
-  const uint8_t* tile = tiled + ((row >> 3) * nb + b) * tile_bytes(TYPE);
-  if constexpr (TYPE == kTypeQ4K) {
+  if constexpr (is_grid_format(TYPE)) {
+    GridRun g;
+    grid_run<TYPE>(tiled + (row * nb + b) * block_bytes_of(TYPE), j, g);
+#pragma unroll
+    for (int i = 0; i < 32; ++i) v[i] = g.scale[i >> 4] * static_cast<float>(grid_value(g, i));
+  } else if constexpr (TYPE == kTypeQ4K) {
+    const uint8_t* tile = tiled + ((row >> 3) * nb + b) * tile_bytes(TYPE);
     const uint8_t* t = tile + 16 * r;
     const uint4 hdr = ld16(t);
     const int c = j >> 1, shift = 4 * (j & 1);
@@ -1784,6 +1991,7 @@ __device__ inline void row_run_values(const uint8_t* __restrict__ tiled, uint64_
       v[i] = p - mn;
     }
   } else if constexpr (TYPE == kTypeIq4Xs) {
+    const uint8_t* tile = tiled + ((row >> 3) * nb + b) * tile_bytes(TYPE);
     const uint2 hdr = ld8(tile + 8 * r);
     const uint4 qq = ld16(tile + 64 + 128 * j + 16 * r);
     const float scale = half_bits(hdr.x) * static_cast<float>(iq4xs_ls(hdr, j));
@@ -1798,6 +2006,7 @@ __device__ inline void row_run_values(const uint8_t* __restrict__ tiled, uint64_
       }
     }
   } else {
+    const uint8_t* tile = tiled + ((row >> 3) * nb + b) * tile_bytes(TYPE);
     auto planes = [&](int p) { return ld16(tile + 128 * p + 16 * r); };
     const uint32_t d_bits = shared_bits<TYPE>(tile, r);
     uint32_t q[8];
@@ -3120,6 +3329,8 @@ bool launch_gemv_decode_fused(int type, const uint8_t* tiled, uint64_t rows, uin
 // ---- embedding and input-major products (any format) --------------------------
 
 #define MQ_ALL_TYPES(X) X(kTypeQ4K) X(kTypeIq4Xs) X(kTypeQ8_0) X(kTypeQ4_0) X(kTypeIq4Nl) X(kTypeQ2K) X(kTypeQ3K) X(kTypeQ5K) X(kTypeQ6K)
+#define MQ_GRID_TYPES(X) X(kTypeIq2Xxs) X(kTypeIq2Xs) X(kTypeIq2S) X(kTypeIq3Xxs) X(kTypeIq3S)
+#define MQ_TABLE_TYPES(X) MQ_ALL_TYPES(X) MQ_GRID_TYPES(X)
 
 void launch_embedding(int type, const uint8_t* tiled, uint64_t nb, int transposed, const uint32_t* ids,
                       uint64_t count, uint64_t dim, float scale, int scaled, float* out, hipStream_t stream) {
@@ -3134,7 +3345,7 @@ void launch_embedding(int type, const uint8_t* tiled, uint64_t nb, int transpose
       hipLaunchKernelGGL(embed_rows_kernel<T>, dim3(grid_for(threads, 256)), dim3(256), 0, stream, tiled, nb, ids, \
                          count, dim, scale, scaled, out);                                                          \
     break;
-    MQ_ALL_TYPES(X)
+    MQ_TABLE_TYPES(X)
 #undef X
     default:
       break;
@@ -3163,7 +3374,7 @@ void launch_axpy(int type, const uint8_t* tiled, uint64_t nb, uint64_t k, uint64
     hipLaunchKernelGGL((axpy_kernel<T, MM>), grid, dim3(256), 0, stream, tiled, nb, k, n, x + r0 * k, rows, kchunk, \
                        part);                                                                                       \
     break;
-      MQ_ALL_TYPES(X)
+      MQ_TABLE_TYPES(X)
 #undef X
       default:
         break;
@@ -3171,6 +3382,62 @@ void launch_axpy(int type, const uint8_t* tiled, uint64_t nb, uint64_t k, uint64
     hipLaunchKernelGGL(axpy_finish_kernel, dim3(grid_for(rows * n, 256)), dim3(256), 0, stream, part, ks, MM, rows, n,
                        y + r0 * n, addend ? addend + (addend_stride ? r0 * addend_stride : 0) : nullptr,
                        addend_stride);
+  }
+}
+
+// ---- IQ2 / IQ3 grid formats ---------------------------------------------------
+
+hipError_t grid_tables_upload(const uint8_t* host, hipStream_t stream) {
+  hipError_t e = hipMemcpyToSymbolAsync(HIP_SYMBOL(g_iq_grids), host, kGridTableBytes, 0, hipMemcpyHostToDevice,
+                                        stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(stream);
+  return e;
+}
+
+void launch_dequantize_grid(int type, const uint8_t* w, uint64_t rows, uint64_t nb, int logical, float* out,
+                            hipStream_t stream) {
+  const uint64_t threads = rows * nb * 8;
+  switch (type) {
+#define X(T)                                                                                                   \
+  case T:                                                                                                      \
+    hipLaunchKernelGGL(dequantize_grid_kernel<T>, dim3(grid_for(threads, 256)), dim3(256), 0, stream, w, rows, \
+                       nb, logical, out);                                                                      \
+    break;
+    MQ_GRID_TYPES(X)
+#undef X
+    default:
+      break;
+  }
+}
+
+void launch_gemv_grid(int type, const uint8_t* w, uint64_t nb, uint64_t rows, const int8_t* xv, const float* xs,
+                      const float* xf, uint64_t m, int int8, float* y, const float* addend, uint64_t addend_stride,
+                      hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>((rows + 3) / 4)), block(256);
+  switch (type) {
+#define MQ_GRID_M(T, MM)                                                                                            \
+  case MM:                                                                                                          \
+    if (int8)                                                                                                       \
+      hipLaunchKernelGGL((gemv_grid_kernel<T, MM, true>), grid, block, 0, stream, w, nb, rows, xv, xs, xf, y, addend, \
+                         addend_stride);                                                                            \
+    else                                                                                                            \
+      hipLaunchKernelGGL((gemv_grid_kernel<T, MM, false>), grid, block, 0, stream, w, nb, rows, xv, xs, xf, y,      \
+                         addend, addend_stride);                                                                    \
+    break;
+#define X(T)                                                                                                 \
+  case T:                                                                                                    \
+    switch (m) {                                                                                             \
+      MQ_GRID_M(T, 1) MQ_GRID_M(T, 2) MQ_GRID_M(T, 3) MQ_GRID_M(T, 4) MQ_GRID_M(T, 5) MQ_GRID_M(T, 6)        \
+      MQ_GRID_M(T, 7) MQ_GRID_M(T, 8)                                                                        \
+      default:                                                                                               \
+        break;                                                                                               \
+    }                                                                                                        \
+    break;
+    MQ_GRID_TYPES(X)
+#undef X
+#undef MQ_GRID_M
+    default:
+      break;
   }
 }
 

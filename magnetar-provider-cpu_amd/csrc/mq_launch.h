@@ -95,6 +95,18 @@ void launch_gemm(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, uin
                  int variant, hipStream_t stream);
 int gemm_default_variant(int type, uint64_t rows, uint64_t m);
 
+// IQ2 / IQ3 grid formats (raw checkpoint blocks; mq_device.h). The grid
+// tables (kGridTableBytes, layout in mq_device.h) are copied to this
+// device's copy, synchronously on `stream`.
+hipError_t grid_tables_upload(const uint8_t* host, hipStream_t stream);
+void launch_dequantize_grid(int type, const uint8_t* w, uint64_t rows, uint64_t nb, int logical, float* out,
+                            hipStream_t stream);
+// m <= 8 rows; int8: xv [m][k] int8 + xs [m][k / 32] scales (quantized
+// activations), else xf [m][k] f32.
+void launch_gemv_grid(int type, const uint8_t* w, uint64_t nb, uint64_t rows, const int8_t* xv, const float* xs,
+                      const float* xf, uint64_t m, int int8, float* y, const float* addend, uint64_t addend_stride,
+                      hipStream_t stream);
+
 // Plane formats (Q8_0, Q4_0, IQ4_NL, Q5_K, Q6_K; layout in mq_device.h).
 // k is the logical row length (a multiple of the format's block), nb =
 // ceil(k / 256) groups.

@@ -27,11 +27,21 @@ Q5_K = 13
 Q6_K = 14
 IQ4_NL = 20
 IQ4_XS = 23
-BLOCK_BYTES = {Q8_0: 34, Q4_0: 18, IQ4_NL: 18, Q2_K: 84, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210, IQ4_XS: 136}
+IQ2_XXS = 16
+IQ2_XS = 17
+IQ3_XXS = 18
+IQ3_S = 21
+IQ2_S = 22
+GRID_FORMATS = (IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S)
+BLOCK_BYTES = {Q8_0: 34, Q4_0: 18, IQ4_NL: 18, Q2_K: 84, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210, IQ4_XS: 136,
+               IQ2_XXS: 66, IQ2_XS: 74, IQ2_S: 82, IQ3_XXS: 98, IQ3_S: 110}
 BLOCK_VALUES = {Q8_0: 32, Q4_0: 32, IQ4_NL: 32, Q2_K: 256, Q3_K: 256, Q4_K: 256, Q5_K: 256, Q6_K: 256,
-                IQ4_XS: 256}
+                IQ4_XS: 256, IQ2_XXS: 256, IQ2_XS: 256, IQ2_S: 256, IQ3_XXS: 256, IQ3_S: 256}
 FORMAT_NAMES = {Q8_0: "Q8_0", Q4_0: "Q4_0", IQ4_NL: "IQ4_NL", Q2_K: "Q2_K", Q3_K: "Q3_K", Q4_K: "Q4_K",
-                Q5_K: "Q5_K", Q6_K: "Q6_K", IQ4_XS: "IQ4_XS"}
+                Q5_K: "Q5_K", Q6_K: "Q6_K", IQ4_XS: "IQ4_XS", IQ2_XXS: "IQ2_XXS", IQ2_XS: "IQ2_XS", IQ2_S: "IQ2_S",
+                IQ3_XXS: "IQ3_XXS", IQ3_S: "IQ3_S"}
+# the grid tables mq_set_iq_grids takes, in order: (entries, dtype)
+GRID_TABLES = ((256, np.uint64), (512, np.uint64), (1024, np.uint64), (256, np.uint32), (512, np.uint32))
 
 OK = 0
 ERR_SHAPE = 1
@@ -95,6 +105,9 @@ def gpu_lib():
         L.mq_weight_upload.argtypes = [_vp, ctypes.c_uint32, _u64, _u64, ctypes.c_int, _u8p,
                                        ctypes.c_size_t, ctypes.POINTER(_u64)]
         L.mq_weight_release.argtypes = [_vp, _u64]
+        L.mq_set_iq_grids.argtypes = [_vp, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64),
+                                      ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint32),
+                                      ctypes.POINTER(ctypes.c_uint32)]
         L.mq_weight_info.argtypes = [_vp, _u64, ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(_u64),
                                      ctypes.POINTER(_u64), ctypes.POINTER(ctypes.c_int), ctypes.POINTER(_u64)]
         L.mq_matmul.argtypes = [_vp, _u64, _f32p, _u64, _u64, ctypes.c_uint32, _f32p]
@@ -218,6 +231,21 @@ class Context:
             raise Declined(rc, self.last_error())
         if rc:
             raise GpuError(rc, self.last_error())
+
+    def set_iq_grids(self, tables):
+        """The IQ2 / IQ3 grid tables (five arrays in GRID_TABLES order:
+        IQ2_XXS, IQ2_XS, IQ2_S u64; IQ3_XXS, IQ3_S u32) for this context's
+        device (mq_set_iq_grids)."""
+        arrs = []
+        for (n, dt), t in zip(GRID_TABLES, tables):
+            a = np.ascontiguousarray(t, dtype=dt)
+            if a.shape != (n,):
+                raise ValueError(f"grid table needs {n} entries, got {a.shape}")
+            arrs.append(a)
+        if len(arrs) != 5:
+            raise ValueError("five grid tables")
+        ptrs = [_p(a, ctypes.c_uint64 if a.dtype == np.uint64 else ctypes.c_uint32) for a in arrs]
+        self._check(gpu_lib().mq_set_iq_grids(self.ptr, *ptrs))
 
     def upload(self, gguf_type, rows, cols, data, transposed=True):
         b = np.ascontiguousarray(data, dtype=np.uint8).reshape(-1)

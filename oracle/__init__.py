@@ -6,8 +6,9 @@ product library (``magnetar-provider-cpu_amd``) never imports it.
 
 ``liboracle.so`` (built from ``oracle.c`` and ``cpu_baseline.c`` by the
 Makefile here) restates, in C, the reference's
- - packed decode of Q8_0, Q4_0, IQ4_NL, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K and
-   IQ4_XS (src/native/quant.rs:46-57, 96-206, 284-338),
+ - packed decode of Q8_0, Q4_0, IQ4_NL, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K,
+   IQ4_XS and the IQ2 / IQ3 grid formats (src/native/quant.rs:46-57,
+   96-279, 284-338), the grids set by the caller (`set_iq_grids`),
  - dequantization (quant.rs:1702-1711),
  - int8 activation quantizer and scalar dot (quant.rs:340-388),
  - scalar int8 / f32 column kernel (quant.rs:559-597),
@@ -37,9 +38,19 @@ Q5_K = 13
 Q6_K = 14
 IQ4_NL = 20
 IQ4_XS = 23
-BLOCK_BYTES = {Q8_0: 34, Q4_0: 18, IQ4_NL: 18, Q2_K: 84, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210, IQ4_XS: 136}
+IQ2_XXS = 16
+IQ2_XS = 17
+IQ3_XXS = 18
+IQ3_S = 21
+IQ2_S = 22
+GRID_FORMATS = (IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S)
+BLOCK_BYTES = {Q8_0: 34, Q4_0: 18, IQ4_NL: 18, Q2_K: 84, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210, IQ4_XS: 136,
+               IQ2_XXS: 66, IQ2_XS: 74, IQ2_S: 82, IQ3_XXS: 98, IQ3_S: 110}
 BLOCK_ELEMENTS = {Q8_0: 32, Q4_0: 32, IQ4_NL: 32, Q2_K: 256, Q3_K: 256, Q4_K: 256, Q5_K: 256, Q6_K: 256,
-                  IQ4_XS: 256}
+                  IQ4_XS: 256, IQ2_XXS: 256, IQ2_XS: 256, IQ2_S: 256, IQ3_XXS: 256, IQ3_S: 256}
+# entries and entry dtype of each grid table, in the order set_iq_grids takes them
+GRID_TABLES = ((IQ2_XXS, 256, np.uint64), (IQ2_XS, 512, np.uint64), (IQ2_S, 1024, np.uint64),
+               (IQ3_XXS, 256, np.uint32), (IQ3_S, 512, np.uint32))
 
 _lib = None
 
@@ -87,6 +98,11 @@ def lib():
         L.or_silu_mul.argtypes = [f32p, f32p, u64, f32p]
         L.or_silu_mul.restype = None
         L.or_add.argtypes = [f32p, u64, f32p, u64, f32p]
+        u64p = ctypes.POINTER(ctypes.c_uint64)
+        u32p = ctypes.POINTER(ctypes.c_uint32)
+        L.or_set_iq_grids.argtypes = [u64p, u64p, u64p, u32p, u32p]
+        L.or_iq_signs.restype = ctypes.c_uint8
+        L.or_iq_signs.argtypes = [ctypes.c_uint32]
         _lib = L
     return _lib
 
@@ -123,6 +139,28 @@ def q3_k_scales(twelve):
     out = np.zeros(16, np.int8)
     lib().or_q3_k_scales(_p(b, ctypes.c_uint8), _p(out, ctypes.c_int8))
     return out
+
+
+def set_iq_grids(tables):
+    """The IQ2 / IQ3 grid tables the grid formats decode with: a sequence
+    of five arrays in GRID_TABLES order (IQ2_XXS, IQ2_XS, IQ2_S u64;
+    IQ3_XXS, IQ3_S u32)."""
+    arrs = []
+    for (fmt, n, dt), t in zip(GRID_TABLES, tables):
+        a = np.ascontiguousarray(t, dtype=dt)
+        if a.shape != (n,):
+            raise ValueError(f"grid table of format {fmt} must hold {n} entries")
+        arrs.append(a)
+    lib().or_set_iq_grids(*(_p(a, ctypes.c_uint64 if a.dtype == np.uint64 else ctypes.c_uint32) for a in arrs))
+    global _grids_keepalive
+    _grids_keepalive = arrs
+
+
+_grids_keepalive = None
+
+
+def iq_signs(index):
+    return int(lib().or_iq_signs(int(index)))
 
 
 def decode_run(fmt, block, run):

@@ -61,6 +61,11 @@ int or_block_bytes(int fmt) {
     case OR_Q5_K: return 176;
     case OR_Q6_K: return 210;
     case OR_IQ4_XS: return 136;
+    case OR_IQ2_XXS: return 66;
+    case OR_IQ2_XS: return 74;
+    case OR_IQ2_S: return 82;
+    case OR_IQ3_XXS: return 98;
+    case OR_IQ3_S: return 110;
     default: return 0;
     }
 }
@@ -69,6 +74,7 @@ int or_block_elements(int fmt) {
     switch (fmt) {
     case OR_Q8_0: case OR_Q4_0: case OR_IQ4_NL: return 32;
     case OR_Q2_K: case OR_Q3_K: case OR_Q4_K: case OR_Q5_K: case OR_Q6_K: case OR_IQ4_XS: return 256;
+    case OR_IQ2_XXS: case OR_IQ2_XS: case OR_IQ2_S: case OR_IQ3_XXS: case OR_IQ3_S: return 256;
     default: return 0;
     }
 }
@@ -132,9 +138,46 @@ static float half_at(const uint8_t *b, int at) {
     return or_f16_to_f32((uint16_t)(b[at] | (b[at + 1] << 8)));
 }
 
-/* `decode` (src/native/quant.rs:96-206): the Q8_0 (102-109), Q4K (110-121),
+static uint32_t word_at(const uint8_t *b, int at) {
+    return (uint32_t)b[at] | ((uint32_t)b[at + 1] << 8) | ((uint32_t)b[at + 2] << 16) | ((uint32_t)b[at + 3] << 24);
+}
+
+/* The grid tables, set by the caller (the reference links them from the
+ * external crate). */
+static uint64_t IQ2XXS_GRID[256], IQ2XS_GRID[512], IQ2S_GRID[1024];
+static uint32_t IQ3XXS_GRID[256], IQ3S_GRID[512];
+
+int or_set_iq_grids(const uint64_t *iq2xxs, const uint64_t *iq2xs, const uint64_t *iq2s,
+                    const uint32_t *iq3xxs, const uint32_t *iq3s) {
+    memcpy(IQ2XXS_GRID, iq2xxs, sizeof IQ2XXS_GRID);
+    memcpy(IQ2XS_GRID, iq2xs, sizeof IQ2XS_GRID);
+    memcpy(IQ2S_GRID, iq2s, sizeof IQ2S_GRID);
+    memcpy(IQ3XXS_GRID, iq3xxs, sizeof IQ3XXS_GRID);
+    memcpy(IQ3S_GRID, iq3s, sizeof IQ3S_GRID);
+    return 0;
+}
+
+/* `iq_signs` (external; the reference tables it at src/native/quant.rs:
+ * 986-997 because it is a parity): low 7 bits as given, bit 7 = their
+ * parity, so every sign byte negates an even number of values. */
+uint8_t or_iq_signs(uint32_t index) {
+    uint32_t v = index & 0x7F, p = 0;
+    for (int i = 0; i < 7; i++) p ^= (v >> i) & 1;
+    return (uint8_t)(v | (p << 7));
+}
+
+/* `signed_grid` (src/native/quant.rs:60-69): value j = the grid's byte j as
+ * i8, negated where bit j of `signs` is set. */
+static void signed_grid(uint64_t grid, uint8_t signs, int8_t *out) {
+    for (int j = 0; j < 8; j++) {
+        int8_t magnitude = (int8_t)((grid >> (8 * j)) & 0xFF);
+        out[j] = ((signs >> j) & 1) ? (int8_t)-magnitude : magnitude;
+    }
+}
+
+/* `decode` (src/native/quant.rs:96-279): the Q8_0 (102-109), Q4K (110-121),
  * Q5K (122-135), Q6K (136-149), Q2K (150-163), Q3K (164-179), Iq4Nl / Q4_0
- * (180-195) and Iq4Xs (196-206) arms. `run` counts within the block (always 0 for 32-value blocks). */
+ * (180-195), Iq4Xs (196-206) and IQ2 / IQ3 grid (207-277) arms. `run` counts within the block (always 0 for 32-value blocks). */
 void or_decode_run(int fmt, const uint8_t *block, int run, int8_t q[OR_RUN],
                    float scale[2], float min[2]) {
     min[0] = min[1] = 0.0f;
@@ -203,6 +246,61 @@ void or_decode_run(int fmt, const uint8_t *block, int run, int8_t q[OR_RUN],
             q[l + 16] = table[byte >> 4];
         }
         scale[0] = scale[1] = d;
+    } else if (fmt == OR_IQ2_XXS) {
+        /* quant.rs:207-218 */
+        float d = half_at(block, 0);
+        uint32_t grids = word_at(block, 2 + 8 * run), aux = word_at(block, 6 + 8 * run);
+        for (int l = 0; l < 4; l++)
+            signed_grid(IQ2XXS_GRID[(grids >> (8 * l)) & 0xFF], or_iq_signs(aux >> (7 * l)), q + 8 * l);
+        float s = d * (0.5f + (float)(aux >> 28)) * 0.25f;
+        scale[0] = scale[1] = s;
+    } else if (fmt == OR_IQ2_XS) {
+        /* quant.rs:219-232 */
+        float d = half_at(block, 0);
+        for (int l = 0; l < 4; l++) {
+            int at = 2 + 2 * (4 * run + l);
+            uint32_t code = (uint32_t)block[at] | ((uint32_t)block[at + 1] << 8);
+            signed_grid(IQ2XS_GRID[code & 511], or_iq_signs(code >> 9), q + 8 * l);
+        }
+        for (int p = 0; p < 2; p++) {
+            uint8_t sc = (block[66 + run] >> (4 * p)) & 0xF;
+            scale[p] = d * (0.5f + (float)sc) * 0.25f;
+        }
+    } else if (fmt == OR_IQ2_S) {
+        /* quant.rs:233-250 */
+        float d = half_at(block, 0);
+        for (int l = 0; l < 4; l++) {
+            int index = block[2 + 4 * run + l] | (((block[66 + run] >> (2 * l)) & 3) << 8);
+            signed_grid(IQ2S_GRID[index], block[34 + 4 * run + l], q + 8 * l);
+        }
+        for (int p = 0; p < 2; p++) {
+            uint8_t sc = (block[74 + run] >> (4 * p)) & 0xF;
+            scale[p] = d * (0.5f + (float)sc) * 0.25f;
+        }
+    } else if (fmt == OR_IQ3_XXS) {
+        /* quant.rs:251-262 */
+        float d = half_at(block, 0);
+        uint32_t aux = word_at(block, 66 + 4 * run);
+        for (int l = 0; l < 4; l++) {
+            uint64_t low = IQ3XXS_GRID[block[2 + 8 * run + 2 * l]];
+            uint64_t high = IQ3XXS_GRID[block[3 + 8 * run + 2 * l]];
+            signed_grid(low | (high << 32), or_iq_signs(aux >> (7 * l)), q + 8 * l);
+        }
+        float s = d * (0.5f + (float)(aux >> 28)) * 0.5f;
+        scale[0] = scale[1] = s;
+    } else if (fmt == OR_IQ3_S) {
+        /* quant.rs:263-277 */
+        float d = half_at(block, 0);
+        for (int l = 0; l < 4; l++) {
+            int i0 = 2 * l, i1 = 2 * l + 1;
+            int index0 = block[2 + 8 * run + i0] | (((block[66 + run] >> i0) & 1) << 8);
+            int index1 = block[2 + 8 * run + i1] | (((block[66 + run] >> i1) & 1) << 8);
+            uint64_t low = IQ3S_GRID[index0], high = IQ3S_GRID[index1];
+            signed_grid(low | (high << 32), block[74 + 4 * run + l], q + 8 * l);
+        }
+        uint8_t sc = (block[106 + run / 2] >> (4 * (run % 2))) & 0xF;
+        float s = d * (float)(1 + 2 * sc);
+        scale[0] = scale[1] = s;
     } else {
         float d = half_at(block, 0);
         int8_t ls[8];

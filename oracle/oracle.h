@@ -31,6 +31,11 @@ extern "C" {
 #define OR_Q6_K 14
 #define OR_IQ4_NL 20
 #define OR_IQ4_XS 23
+#define OR_IQ2_XXS 16
+#define OR_IQ2_XS 17
+#define OR_IQ3_XXS 18
+#define OR_IQ3_S 21
+#define OR_IQ2_S 22
 
 /* Values per run (src/native/quant.rs:18-19). */
 #define OR_RUN 32
@@ -43,6 +48,15 @@ void or_iq4_xs_scales(const uint8_t *six, int8_t out[8]);
 const int8_t *or_iq4nl_values(void);
 const int8_t *or_q4_0_values(void);
 void or_q3_k_scales(const uint8_t *twelve, int8_t out[16]);
+
+/* The IQ2 / IQ3 grid tables (magnetar-provider-api `iq_grids`, external):
+ * the decode of those formats reads them from here. Entries: IQ2_XXS 256,
+ * IQ2_XS 512, IQ2_S 1024 (u64: 8 magnitudes), IQ3_XXS 256, IQ3_S 512 (u32:
+ * 4 magnitudes). Copied; returns 0. */
+int or_set_iq_grids(const uint64_t *iq2xxs, const uint64_t *iq2xs, const uint64_t *iq2s,
+                    const uint32_t *iq3xxs, const uint32_t *iq3s);
+/* `iq_signs` (external): the 7-bit index with its parity in bit 7. */
+uint8_t or_iq_signs(uint32_t index);
 
 /* Run `run` of one block: 32 signed values, per-half scale and min. */
 void or_decode_run(int fmt, const uint8_t *block, int run, int8_t q[OR_RUN],

@@ -12,11 +12,37 @@ Q5_K = 13
 Q6_K = 14
 IQ4_NL = 20
 IQ4_XS = 23
-BLOCK_BYTES = {Q8_0: 34, Q4_0: 18, IQ4_NL: 18, Q2_K: 84, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210, IQ4_XS: 136}
+IQ2_XXS = 16
+IQ2_XS = 17
+IQ3_XXS = 18
+IQ3_S = 21
+IQ2_S = 22
+BLOCK_BYTES = {Q8_0: 34, Q4_0: 18, IQ4_NL: 18, Q2_K: 84, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210, IQ4_XS: 136,
+               IQ2_XXS: 66, IQ2_XS: 74, IQ2_S: 82, IQ3_XXS: 98, IQ3_S: 110}
 BLOCK_ELEMENTS = {Q8_0: 32, Q4_0: 32, IQ4_NL: 32, Q2_K: 256, Q3_K: 256, Q4_K: 256, Q5_K: 256, Q6_K: 256,
-                  IQ4_XS: 256}
+                  IQ4_XS: 256, IQ2_XXS: 256, IQ2_XS: 256, IQ2_S: 256, IQ3_XXS: 256, IQ3_S: 256}
 # the formats of the generic (planes) GPU path
 PLANE_FORMATS = [Q8_0, Q4_0, IQ4_NL, Q2_K, Q3_K, Q5_K, Q6_K]
+# the IQ2 / IQ3 formats, whose decode reads the grid tables
+GRID_FORMATS = [IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S]
+
+
+def synthetic_iq_grids(seed=1):
+    """Stand-in grid tables (the real ones live in the external
+    magnetar-provider-api crate, absent here): the ggml tables' shapes and
+    magnitude alphabets (IQ2: 8 bytes from {8, 25, 43}; IQ3_XXS: 4 bytes from
+    {4, 12, ..., 62}; IQ3_S: 4 odd bytes 1..15), entries drawn at random.
+    Returns the five arrays in the order set_iq_grids takes them."""
+    rng = np.random.default_rng(seed)
+
+    def table(n, width, alphabet, dtype):
+        b = rng.choice(np.array(alphabet, np.uint8), size=(n, width))
+        return b.view(dtype).reshape(n)
+
+    iq2 = [8, 25, 43]
+    return (table(256, 8, iq2, np.uint64), table(512, 8, iq2, np.uint64), table(1024, 8, iq2, np.uint64),
+            table(256, 4, [4, 12, 20, 28, 36, 44, 52, 62], np.uint32), table(512, 4, [1, 3, 5, 7, 9, 11, 13, 15],
+                                                                               np.uint32))
 
 
 class Rng:

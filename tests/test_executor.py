@@ -71,9 +71,9 @@ def test_executor_stores_packed_weights(executor):
         assert not declining.write_packed_weight_tensor("w", Q4_K, 4, 256, w)
     finally:
         declining.close()
-    # a format without a GPU path (IQ2_XXS) is declined; an untransposed
+    # a format without a GPU path (IQ1_S) is declined; an untransposed
     # weight is stored with its logical shape [stored_rows, stored_cols]
-    assert not executor.write_packed_weight_tensor("iq2", 16, 2, 256, np.zeros(2 * 66, np.uint8))
+    assert not executor.write_packed_weight_tensor("iq1", 19, 2, 256, np.zeros(2 * 50, np.uint8))
     assert executor.write_packed_weight_tensor("t", Q4_K, 4, 256, w, transposed=False)
     assert executor.resident_shape("t") == [4, 256]
 

@@ -350,7 +350,7 @@ def test_device_entry_points_agree_with_host_entry_point(ctx):
 def test_boundary_errors_and_declines(ctx):
     w = packed(Q4_K, 4, 256, 41)
     with pytest.raises(mg.Declined):
-        ctx.upload(16, 4, 256, np.zeros(4 * 66, np.uint8))  # IQ2_XXS has no GPU path
+        ctx.upload(19, 4, 256, np.zeros(4 * 50, np.uint8))  # IQ1_S has no GPU path
     with pytest.raises(mg.GpuError) as e:
         ctx.upload(Q4_K, 4, 256, w[:, :100])
     assert e.value.code == mg.ERR_SHAPE
