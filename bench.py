@@ -351,6 +351,35 @@ def formats_part(ctx, torch, per_graph, use_graph, extra):
             f"M=512 gemm {tg * 1e6:.1f} us, {tflops:.1f} TFLOP/s")
         for h in copies:
             h.release()
+    # the IQ2 / IQ3 grid formats (stand-in grid tables of the real shapes): the
+    # decode GEMV, and M = 512 as the 8-row GEMVs these formats' prefill runs
+    ctx.set_iq_grids(workloads.synthetic_iq_grids(1))
+    for fmt in mg.GRID_FORMATS:
+        name = mg.FORMAT_NAMES[fmt]
+        w = workloads.random_blocks(fmt, n, k, 4000 + fmt)
+        copies = [ctx.upload(fmt, n, k, w) for _ in range(max(2, -(-600_000_000 // w.size)))]
+
+        def gv(i, stream, copies=copies):
+            ctx.matmul_dev(copies[i % len(copies)], x.data_ptr(), 1, k, y.data_ptr(), int8=True, stream=stream)
+
+        r = GraphRunner(torch, gv, per_graph, use_graph)
+        r.time(per_graph)
+        t = r.time(5 * per_graph) / (5 * per_graph)
+        extra[f"{name}_gemv_kernel_us"] = round(t * 1e6, 3)
+        extra[f"{name}_gemv_GBps"] = round(w.size / t / 1e9, 1)
+        extra[f"{name}_gemv_frac_hbm"] = round(w.size / t / 1e9 / HBM_PEAK_GBS, 4)
+
+        def gm(i, stream, copies=copies):
+            ctx.matmul_dev(copies[i % len(copies)], xm.data_ptr(), 512, k, ym.data_ptr(), int8=True, stream=stream)
+
+        rg = GraphRunner(torch, gm, 2, use_graph)
+        rg.time(2)
+        tg = rg.time(4) / 4
+        extra[f"{name}_prefill512_us"] = round(tg * 1e6, 1)
+        log(f"{name}: gemv {t * 1e6:.2f} us, {w.size / t / 1e9:.1f} GB/s ({w.size} B); "
+            f"M=512 as 8-row GEMVs {tg * 1e6:.0f} us")
+        for h in copies:
+            h.release()
 
 
 def gemm_part(ctx, torch, workloads, use_graph, args):

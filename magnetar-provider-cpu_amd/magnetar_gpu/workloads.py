@@ -75,3 +75,21 @@ def random_blocks(fmt, rows, cols, seed):
         blocks[:, at] = bits & 0xFF
         blocks[:, at + 1] = bits >> 8
     return blocks.reshape(rows, cols // bv * bb)
+
+
+def synthetic_iq_grids(seed=1):
+    """Stand-in IQ2 / IQ3 grid tables (the real ones are the caller's:
+    magnetar-provider-api `iq_grids`): the ggml tables' shapes and magnitude
+    alphabets (IQ2: 8 bytes from {8, 25, 43}; IQ3_XXS: 4 bytes from
+    {4, 12, ..., 62}; IQ3_S: 4 odd bytes 1..15), entries drawn at random.
+    The five arrays in the order mq_set_iq_grids takes them."""
+    rng = np.random.default_rng(seed)
+
+    def table(n, width, alphabet, dtype):
+        b = rng.choice(np.array(alphabet, np.uint8), size=(n, width))
+        return b.view(dtype).reshape(n)
+
+    iq2 = [8, 25, 43]
+    return (table(256, 8, iq2, np.uint64), table(512, 8, iq2, np.uint64), table(1024, 8, iq2, np.uint64),
+            table(256, 4, [4, 12, 20, 28, 36, 44, 52, 62], np.uint32),
+            table(512, 4, [1, 3, 5, 7, 9, 11, 13, 15], np.uint32))

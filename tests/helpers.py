@@ -29,20 +29,10 @@ GRID_FORMATS = [IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S]
 
 def synthetic_iq_grids(seed=1):
     """Stand-in grid tables (the real ones live in the external
-    magnetar-provider-api crate, absent here): the ggml tables' shapes and
-    magnitude alphabets (IQ2: 8 bytes from {8, 25, 43}; IQ3_XXS: 4 bytes from
-    {4, 12, ..., 62}; IQ3_S: 4 odd bytes 1..15), entries drawn at random.
-    Returns the five arrays in the order set_iq_grids takes them."""
-    rng = np.random.default_rng(seed)
+    magnetar-provider-api crate, absent here), as the bench uses them."""
+    from magnetar_gpu.workloads import synthetic_iq_grids as tables
 
-    def table(n, width, alphabet, dtype):
-        b = rng.choice(np.array(alphabet, np.uint8), size=(n, width))
-        return b.view(dtype).reshape(n)
-
-    iq2 = [8, 25, 43]
-    return (table(256, 8, iq2, np.uint64), table(512, 8, iq2, np.uint64), table(1024, 8, iq2, np.uint64),
-            table(256, 4, [4, 12, 20, 28, 36, 44, 52, 62], np.uint32), table(512, 4, [1, 3, 5, 7, 9, 11, 13, 15],
-                                                                               np.uint32))
+    return tables(seed)
 
 
 class Rng:
