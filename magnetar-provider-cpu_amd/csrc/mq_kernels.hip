@@ -1241,37 +1241,67 @@ __global__ __launch_bounds__(512) void gemv_lds_int8_kernel(
   const uint32_t lane_off = static_cast<uint32_t>((lane >> 3) * group_bytes);
   auto block_off = [&](int b) { return b < b1 ? lane_off + static_cast<uint32_t>(b) * kTile : kBufferNone; };
 
-  // 1. activation loads
-  FusedStage<TYPE, M, NORM> fs;
-  QuantizedStage<TYPE, M> qs;
-  if (FUSED)
-    fs.load(xf, K, k0, kn, kn, fu.norm_w);
-  else
-    qs.load(xv, xs, xsum, K, k0, kn, kn);
-  // 2. the wave's first weight block
-  RawRowBlock A;
-  const int bA = b0 + s;
-  load_row_block<TYPE>(A, rsrc, block_off(bA), r);
-  // 3. activations into LDS (rmsnorm'd first under NORM)
-  float nscale = 1.0f;
-  if constexpr (NORM) nscale = row_norm_scale(xf, K, fu.norm_eps);
-  if (FUSED)
-    fs.store(xf, K, k0, kn, kn, lds, nscale, fu.norm_w);
-  else
-    qs.store(xv, xs, xsum, K, k0, kn, kn, lds);
-  __syncthreads();
-
   float acc[M], mins[M];
 #pragma unroll
   for (int m = 0; m < M; ++m) acc[m] = mins[m] = 0.0f;
   Chunk<M> next;
-  if (PIPE && bA < b1) read_chunk<TYPE, M>(next, lds, kn, kruns, bA - b0, 0);
-  for (int b = bA; b < b1; b += S) {
-    const RawRowBlock cur = A;
-    load_row_block<TYPE>(A, rsrc, block_off(b + S), r);
-    // with more rows the scheduler would sink the prefetch below the math
-    if (!PIPE) __builtin_amdgcn_sched_barrier(0);
-    row_block<TYPE, M, PIPE>(cur, lds, kn, kruns, b - b0, b + S - b0, b + S < b1, next, acc, mins);
+  const int bA = b0 + s;
+  bool done = false;
+  if constexpr (PIPE && FUSED && !NORM) {
+    // Wave-local staging (when every wave has at most two blocks; the bound
+    // is work-group uniform): each wave quantizes the activations of its own
+    // blocks into their LDS slots and needs no work-group barrier, so it
+    // starts on its first block as soon as that block and its x have
+    // landed, and both of its weight blocks are in flight from the start (x
+    // first: per-wave returns are in issue order). Bit-identical to the
+    // work-group staging: the same quantize4 on the same 32 values.
+    if (b1 - b0 <= 2 * S) {
+      const int bB = bA + S;
+      const float4 xa = bA < b1 ? reinterpret_cast<const float4*>(xf)[64 * static_cast<uint64_t>(bA) + lane]
+                                : make_float4(0.f, 0.f, 0.f, 0.f);
+      const float4 xb = bB < b1 ? reinterpret_cast<const float4*>(xf)[64 * static_cast<uint64_t>(bB) + lane]
+                                : make_float4(0.f, 0.f, 0.f, 0.f);
+      RawRowBlock A0, A1;
+      load_row_block<TYPE>(A0, rsrc, block_off(bA), r);
+      load_row_block<TYPE>(A1, rsrc, block_off(bB), r);
+      const Quant4 qa = quantize4(xa), qb = quantize4(xb);
+      if (bA < b1) FusedStage<TYPE, M, false>::put(qa, 64 * (bA - b0) + lane, lds, M * kn);
+      if (bB < b1) FusedStage<TYPE, M, false>::put(qb, 64 * (bB - b0) + lane, lds, M * kn);
+      if (bA < b1) {
+        read_chunk<TYPE, M>(next, lds, kn, kruns, bA - b0, 0);
+        row_block<TYPE, M, PIPE>(A0, lds, kn, kruns, bA - b0, bB - b0, bB < b1, next, acc, mins);
+      }
+      if (bB < b1) row_block<TYPE, M, PIPE>(A1, lds, kn, kruns, bB - b0, bB + S - b0, false, next, acc, mins);
+      done = true;
+    }
+  }
+  if (!done) {
+    // 1. activation loads
+    FusedStage<TYPE, M, NORM> fs;
+    QuantizedStage<TYPE, M> qs;
+    if (FUSED)
+      fs.load(xf, K, k0, kn, kn, fu.norm_w);
+    else
+      qs.load(xv, xs, xsum, K, k0, kn, kn);
+    // 2. the wave's first weight block
+    RawRowBlock A;
+    load_row_block<TYPE>(A, rsrc, block_off(bA), r);
+    // 3. activations into LDS (rmsnorm'd first under NORM)
+    float nscale = 1.0f;
+    if constexpr (NORM) nscale = row_norm_scale(xf, K, fu.norm_eps);
+    if (FUSED)
+      fs.store(xf, K, k0, kn, kn, lds, nscale, fu.norm_w);
+    else
+      qs.store(xv, xs, xsum, K, k0, kn, kn, lds);
+    __syncthreads();
+    if (PIPE && bA < b1) read_chunk<TYPE, M>(next, lds, kn, kruns, bA - b0, 0);
+    for (int b = bA; b < b1; b += S) {
+      const RawRowBlock cur = A;
+      load_row_block<TYPE>(A, rsrc, block_off(b + S), r);
+      // with more rows the scheduler would sink the prefetch below the math
+      if (!PIPE) __builtin_amdgcn_sched_barrier(0);
+      row_block<TYPE, M, PIPE>(cur, lds, kn, kruns, b - b0, b + S - b0, b + S < b1, next, acc, mins);
+    }
   }
   finish_rows<M, EPI>(acc, mins, rows, y, addend, addend_stride, reinterpret_cast<float*>(lds), sk.partials,
                       sk.counters, sk.ks, fu);
