@@ -1247,28 +1247,80 @@ __global__ __launch_bounds__(512) void gemv_lds_int8_kernel(
   Chunk<M> next;
   const int bA = b0 + s;
   bool done = false;
-  if constexpr (PIPE && FUSED && !NORM) {
-    // Wave-local staging (when every wave has at most two blocks; the bound
-    // is work-group uniform): each wave quantizes the activations of its own
-    // blocks into their LDS slots and needs no work-group barrier, so it
-    // starts on its first block as soon as that block and its x have
-    // landed, and both of its weight blocks are in flight from the start (x
-    // first: per-wave returns are in issue order). Bit-identical to the
-    // work-group staging: the same quantize4 on the same 32 values.
+  if constexpr (FUSED && !NORM && M <= 4) {
+    // Wave-local staging (up to 4 activation rows, when every wave has at
+    // most two blocks; the bound is work-group uniform): each wave quantizes
+    // the activations of its own blocks into their LDS slots and needs no
+    // work-group barrier, so it starts on its first block as soon as that
+    // block and its x have landed, and both of its weight blocks are in
+    // flight from the start (x first: per-wave returns are in issue order).
+    // Bit-identical to the work-group staging: the same quantize4 on the
+    // same 32 values.
     if (b1 - b0 <= 2 * S) {
       const int bB = bA + S;
-      const float4 xa = bA < b1 ? reinterpret_cast<const float4*>(xf)[64 * static_cast<uint64_t>(bA) + lane]
-                                : make_float4(0.f, 0.f, 0.f, 0.f);
-      const float4 xb = bB < b1 ? reinterpret_cast<const float4*>(xf)[64 * static_cast<uint64_t>(bB) + lane]
-                                : make_float4(0.f, 0.f, 0.f, 0.f);
+      float4 xa[M], xb[M];
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        const float4* xr = reinterpret_cast<const float4*>(xf + m * K);
+        xa[m] = bA < b1 ? xr[64 * static_cast<uint64_t>(bA) + lane] : make_float4(0.f, 0.f, 0.f, 0.f);
+        xb[m] = bB < b1 ? xr[64 * static_cast<uint64_t>(bB) + lane] : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
       RawRowBlock A0, A1;
       load_row_block<TYPE>(A0, rsrc, block_off(bA), r);
       load_row_block<TYPE>(A1, rsrc, block_off(bB), r);
-      const Quant4 qa = quantize4(xa), qb = quantize4(xb);
-      if (bA < b1) FusedStage<TYPE, M, false>::put(qa, 64 * (bA - b0) + lane, lds, M * kn);
-      if (bB < b1) FusedStage<TYPE, M, false>::put(qb, 64 * (bB - b0) + lane, lds, M * kn);
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        const Quant4 qa = quantize4(xa[m]), qb = quantize4(xb[m]);
+        if (bA < b1) FusedStage<TYPE, M, false>::put(qa, m * (kn / 4) + 64 * (bA - b0) + lane, lds, M * kn);
+        if (bB < b1) FusedStage<TYPE, M, false>::put(qb, m * (kn / 4) + 64 * (bB - b0) + lane, lds, M * kn);
+      }
       if (bA < b1) {
-        read_chunk<TYPE, M>(next, lds, kn, kruns, bA - b0, 0);
+        if (PIPE) read_chunk<TYPE, M>(next, lds, kn, kruns, bA - b0, 0);
+        row_block<TYPE, M, PIPE>(A0, lds, kn, kruns, bA - b0, bB - b0, bB < b1, next, acc, mins);
+      }
+      if (bB < b1) row_block<TYPE, M, PIPE>(A1, lds, kn, kruns, bB - b0, bB + S - b0, false, next, acc, mins);
+      done = true;
+    }
+  }
+  if constexpr (!FUSED && M <= 4) {
+    // The same wave-local staging on pre-quantized activations: lanes 0..31
+    // copy the two blocks' int8 values (16 B each), lanes 32..47 their runs'
+    // scales (and sums), through buffer loads predicated by offset (no
+    // branch for the merge to wait on), issued before the weight blocks.
+    if (b1 - b0 <= 2 * S) {
+      const int bB = bA + S;
+      const uint32_t runs = static_cast<uint32_t>(K / 32);
+      const __amdgpu_buffer_rsrc_t rsv = buffer_rsrc(xv, static_cast<uint32_t>(M * K));
+      const __amdgpu_buffer_rsrc_t rss = buffer_rsrc(xs, static_cast<uint32_t>(M * runs * 4));
+      const __amdgpu_buffer_rsrc_t rsh = buffer_rsrc(xsum, TYPE == kTypeQ4K ? static_cast<uint32_t>(M * runs * 8) : 0u);
+      const bool is_val = lane < 32, is_run = lane >= 32 && lane < 48;
+      const int blk = is_val ? (lane < 16 ? bA : bB) : (lane < 40 ? bA : bB);
+      const bool live = blk < b1 && (is_val || is_run);
+      uint4 vv[M];
+      uint32_t dd[M];
+      uint2 hh[M];
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        const uint32_t c16 = static_cast<uint32_t>(m * K + 256 * blk + 16 * (lane & 15));
+        const uint32_t src = static_cast<uint32_t>(m) * runs + 8 * blk + (lane & 7);
+        vv[m] = buffer_ld16(rsv, live && is_val ? c16 : kBufferNone);
+        dd[m] = buffer_ld4(rss, live && is_run ? 4 * src : kBufferNone);
+        hh[m] = buffer_ld8(rsh, live && is_run ? 8 * src : kBufferNone);
+      }
+      RawRowBlock A0, A1;
+      load_row_block<TYPE>(A0, rsrc, block_off(bA), r);
+      load_row_block<TYPE>(A1, rsrc, block_off(bB), r);
+      float* rs = reinterpret_cast<float*>(lds + M * kn);
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        if (live && is_val)
+          reinterpret_cast<uint4*>(lds)[m * (kn / 16) + 16 * (blk - b0) + (lane & 15)] = vv[m];
+        if (live && is_run)
+          QuantizedStage<TYPE, M>::put_run(rs, m * kruns + 8 * (blk - b0) + (lane & 7), __uint_as_float(dd[m]),
+                                           static_cast<int>(hh[m].x + hh[m].y), static_cast<int>(hh[m].y));
+      }
+      if (bA < b1) {
+        if (PIPE) read_chunk<TYPE, M>(next, lds, kn, kruns, bA - b0, 0);
         row_block<TYPE, M, PIPE>(A0, lds, kn, kruns, bA - b0, bB - b0, bB < b1, next, acc, mins);
       }
       if (bB < b1) row_block<TYPE, M, PIPE>(A1, lds, kn, kruns, bB - b0, bB + S - b0, false, next, acc, mins);

@@ -345,6 +345,33 @@ def test_device_entry_points_agree_with_host_entry_point(ctx):
         h.release()
 
 
+@pytest.mark.parametrize("fmt", [Q4_K, IQ4_XS])
+@pytest.mark.parametrize("n,k", [(37, 512), (300, 4096), (520, 8192), (9, 256)])
+def test_prequantized_every_m_matches_fused(ctx, fmt, n, k):
+    """The pre-quantized GEMV (activations quantized by the caller) equals
+    the fused one bit for bit at m = 1..8, over block counts that take the
+    wave-local staging (<= 2 blocks per wave) and ones that do not."""
+    w = packed(fmt, n, k, 95 + n)
+    h = ctx.upload(fmt, n, k, w)
+    stream = torch.cuda.current_stream().cuda_stream
+    try:
+        for m in range(1, 9):
+            a = activations(m, k, 96 + m)
+            host = ctx.matmul(h, a)
+            assert_row_tolerance(host, expected(fmt, w, n, k, a, True), f"m {m}")
+            xd = dev(a)
+            v = torch.empty(m * k, dtype=torch.int8, device="cuda")
+            sc = torch.empty(m * k // 32, dtype=torch.float32, device="cuda")
+            sm = torch.empty(m * k // 16, dtype=torch.int32, device="cuda")
+            ctx.quantize_activations_dev(xd.data_ptr(), m, k, v.data_ptr(), sc.data_ptr(), sm.data_ptr(), stream)
+            y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+            ctx.matmul_prequantized_dev(h, v.data_ptr(), sc.data_ptr(), sm.data_ptr(), m, k, y.data_ptr(), stream)
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(y.cpu().numpy(), host, err_msg=f"m {m}")
+    finally:
+        h.release()
+
+
 # ---- boundary behaviour ---------------------------------------------------------------
 
 def test_boundary_errors_and_declines(ctx):
