@@ -57,6 +57,7 @@ struct mq_ctx {
   size_t sk_bytes = 0;
   uint64_t sk_counters = 0;
   int gemv_ksplit_override = 0;
+  int gemv_narrow_override = -1;
   int gemv_splits_override = 0;
   int gemv_variant = 0;
   int gemm_variant = 0;
@@ -158,6 +159,7 @@ int acquire_workspace(mq_ctx* ctx, hipStream_t stream, size_t bytes) {
 int acquire_splitk(mq_ctx* ctx, hipStream_t stream, const Weight& w, uint64_t m, mq::GemvSplitK& sk) {
   sk = mq::GemvSplitK{};
   sk.ks = ctx->gemv_ksplit_override > 0 ? ctx->gemv_ksplit_override : mq::gemv_default_ksplit(w.rows, w.nb);
+  sk.narrow = ctx->gemv_narrow_override;
   if (plane_type(w.type)) {
     // the plane GEMV has no other form: its LDS staging must fit
     const int need = mq::gemv_planes_min_ksplit(w.nb, m);
@@ -442,6 +444,7 @@ int mq_create(int device, mq_ctx** out) {
   ctx->ws_stream = ctx->stream;
   if (const char* s = std::getenv("MQ_GEMV_SPLITS")) ctx->gemv_splits_override = std::atoi(s);
   if (const char* s = std::getenv("MQ_GEMV_KSPLIT")) ctx->gemv_ksplit_override = std::atoi(s);
+  if (const char* s = std::getenv("MQ_GEMV_NARROW")) ctx->gemv_narrow_override = std::atoi(s);
   if (const char* s = std::getenv("MQ_GEMV_VARIANT")) ctx->gemv_variant = std::atoi(s);
   if (const char* s = std::getenv("MQ_GEMM_VARIANT")) ctx->gemm_variant = std::atoi(s);
   *out = ctx;

@@ -1214,6 +1214,75 @@ __device__ inline void row_block(const RawRowBlock& a, const uint8_t* lds, int k
   }
 }
 
+// Wave-local staging of two super-blocks bA and bB (bB past b1 is skipped)
+// of the K range that starts at block b0: the wave that multiplies them
+// stages their activations into their LDS slots itself, so no work-group
+// barrier orders staging before math. load() issues the global reads (before
+// the wave's weight blocks: per-wave returns come in issue order), put()
+// writes LDS. Fused: quantize4 of each block's 256 f32 values, the
+// arithmetic of the work-group staging (bit-identical). Pre-quantized: lanes
+// 0..31 copy the two blocks' int8 values (16 B each), lanes 32..47 their
+// runs' scales (and sums), through buffer loads predicated by offset (no
+// branch for a merge to wait on).
+template <int TYPE, int M, bool FUSED>
+struct WaveStage {
+  float4 xa[M], xb[M];
+  uint4 vv[M];
+  uint32_t dd[M];
+  uint2 hh[M];
+
+  __device__ void load(const float* __restrict__ xf, const int8_t* __restrict__ xv, const float* __restrict__ xs,
+                       const int32_t* __restrict__ xsum, uint64_t K, int bA, int bB, int b1, int lane) {
+    if constexpr (FUSED) {
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        const float4* xr = reinterpret_cast<const float4*>(xf + m * K);
+        xa[m] = bA < b1 ? xr[64 * static_cast<uint64_t>(bA) + lane] : make_float4(0.f, 0.f, 0.f, 0.f);
+        xb[m] = bB < b1 ? xr[64 * static_cast<uint64_t>(bB) + lane] : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    } else {
+      const uint32_t runs = static_cast<uint32_t>(K / 32);
+      const __amdgpu_buffer_rsrc_t rsv = buffer_rsrc(xv, static_cast<uint32_t>(M * K));
+      const __amdgpu_buffer_rsrc_t rss = buffer_rsrc(xs, static_cast<uint32_t>(M * runs * 4));
+      const __amdgpu_buffer_rsrc_t rsh = buffer_rsrc(xsum, TYPE == kTypeQ4K ? static_cast<uint32_t>(M * runs * 8) : 0u);
+      const bool is_val = lane < 32, is_run = lane >= 32 && lane < 48;
+      const int blk = is_val ? (lane < 16 ? bA : bB) : (lane < 40 ? bA : bB);
+      const bool live = blk < b1 && (is_val || is_run);
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        const uint32_t c16 = static_cast<uint32_t>(m * K + 256 * blk + 16 * (lane & 15));
+        const uint32_t src = static_cast<uint32_t>(m) * runs + 8 * blk + (lane & 7);
+        vv[m] = buffer_ld16(rsv, live && is_val ? c16 : kBufferNone);
+        dd[m] = buffer_ld4(rss, live && is_run ? 4 * src : kBufferNone);
+        hh[m] = buffer_ld8(rsh, live && is_run ? 8 * src : kBufferNone);
+      }
+    }
+  }
+
+  __device__ void put(uint8_t* lds, int kn, int kruns, int b0, int bA, int bB, int b1, int lane) const {
+    if constexpr (FUSED) {
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        const Quant4 qa = quantize4(xa[m]), qb = quantize4(xb[m]);
+        if (bA < b1) FusedStage<TYPE, M, false>::put(qa, m * (kn / 4) + 64 * (bA - b0) + lane, lds, M * kn);
+        if (bB < b1) FusedStage<TYPE, M, false>::put(qb, m * (kn / 4) + 64 * (bB - b0) + lane, lds, M * kn);
+      }
+    } else {
+      const bool is_val = lane < 32, is_run = lane >= 32 && lane < 48;
+      const int blk = is_val ? (lane < 16 ? bA : bB) : (lane < 40 ? bA : bB);
+      const bool live = blk < b1 && (is_val || is_run);
+      float* rs = reinterpret_cast<float*>(lds + M * kn);
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        if (live && is_val) reinterpret_cast<uint4*>(lds)[m * (kn / 16) + 16 * (blk - b0) + (lane & 15)] = vv[m];
+        if (live && is_run)
+          QuantizedStage<TYPE, M>::put_run(rs, m * kruns + 8 * (blk - b0) + (lane & 7), __uint_as_float(dd[m]),
+                                           static_cast<int>(hh[m].x + hh[m].y), static_cast<int>(hh[m].y));
+      }
+    }
+  }
+};
+
 template <int TYPE, int M, bool FUSED, bool NORM = false, int EPI = kEpiPlain>
 __global__ __launch_bounds__(512) void gemv_lds_int8_kernel(
     const uint8_t* __restrict__ w, int nb, uint64_t rows, const int8_t* __restrict__ xv,
@@ -1247,78 +1316,19 @@ __global__ __launch_bounds__(512) void gemv_lds_int8_kernel(
   Chunk<M> next;
   const int bA = b0 + s;
   bool done = false;
-  if constexpr (FUSED && !NORM && M <= 4) {
+  if constexpr (!NORM && M <= 4) {
     // Wave-local staging (up to 4 activation rows, when every wave has at
-    // most two blocks; the bound is work-group uniform): each wave quantizes
-    // the activations of its own blocks into their LDS slots and needs no
-    // work-group barrier, so it starts on its first block as soon as that
-    // block and its x have landed, and both of its weight blocks are in
-    // flight from the start (x first: per-wave returns are in issue order).
-    // Bit-identical to the work-group staging: the same quantize4 on the
-    // same 32 values.
+    // most two blocks; the bound is work-group uniform): the wave starts on
+    // its first block as soon as that block and its activations have
+    // landed, and both of its weight blocks are in flight from the start.
     if (b1 - b0 <= 2 * S) {
       const int bB = bA + S;
-      float4 xa[M], xb[M];
-#pragma unroll
-      for (int m = 0; m < M; ++m) {
-        const float4* xr = reinterpret_cast<const float4*>(xf + m * K);
-        xa[m] = bA < b1 ? xr[64 * static_cast<uint64_t>(bA) + lane] : make_float4(0.f, 0.f, 0.f, 0.f);
-        xb[m] = bB < b1 ? xr[64 * static_cast<uint64_t>(bB) + lane] : make_float4(0.f, 0.f, 0.f, 0.f);
-      }
+      WaveStage<TYPE, M, FUSED> ws;
+      ws.load(xf, xv, xs, xsum, K, bA, bB, b1, lane);
       RawRowBlock A0, A1;
       load_row_block<TYPE>(A0, rsrc, block_off(bA), r);
       load_row_block<TYPE>(A1, rsrc, block_off(bB), r);
-#pragma unroll
-      for (int m = 0; m < M; ++m) {
-        const Quant4 qa = quantize4(xa[m]), qb = quantize4(xb[m]);
-        if (bA < b1) FusedStage<TYPE, M, false>::put(qa, m * (kn / 4) + 64 * (bA - b0) + lane, lds, M * kn);
-        if (bB < b1) FusedStage<TYPE, M, false>::put(qb, m * (kn / 4) + 64 * (bB - b0) + lane, lds, M * kn);
-      }
-      if (bA < b1) {
-        if (PIPE) read_chunk<TYPE, M>(next, lds, kn, kruns, bA - b0, 0);
-        row_block<TYPE, M, PIPE>(A0, lds, kn, kruns, bA - b0, bB - b0, bB < b1, next, acc, mins);
-      }
-      if (bB < b1) row_block<TYPE, M, PIPE>(A1, lds, kn, kruns, bB - b0, bB + S - b0, false, next, acc, mins);
-      done = true;
-    }
-  }
-  if constexpr (!FUSED && M <= 4) {
-    // The same wave-local staging on pre-quantized activations: lanes 0..31
-    // copy the two blocks' int8 values (16 B each), lanes 32..47 their runs'
-    // scales (and sums), through buffer loads predicated by offset (no
-    // branch for the merge to wait on), issued before the weight blocks.
-    if (b1 - b0 <= 2 * S) {
-      const int bB = bA + S;
-      const uint32_t runs = static_cast<uint32_t>(K / 32);
-      const __amdgpu_buffer_rsrc_t rsv = buffer_rsrc(xv, static_cast<uint32_t>(M * K));
-      const __amdgpu_buffer_rsrc_t rss = buffer_rsrc(xs, static_cast<uint32_t>(M * runs * 4));
-      const __amdgpu_buffer_rsrc_t rsh = buffer_rsrc(xsum, TYPE == kTypeQ4K ? static_cast<uint32_t>(M * runs * 8) : 0u);
-      const bool is_val = lane < 32, is_run = lane >= 32 && lane < 48;
-      const int blk = is_val ? (lane < 16 ? bA : bB) : (lane < 40 ? bA : bB);
-      const bool live = blk < b1 && (is_val || is_run);
-      uint4 vv[M];
-      uint32_t dd[M];
-      uint2 hh[M];
-#pragma unroll
-      for (int m = 0; m < M; ++m) {
-        const uint32_t c16 = static_cast<uint32_t>(m * K + 256 * blk + 16 * (lane & 15));
-        const uint32_t src = static_cast<uint32_t>(m) * runs + 8 * blk + (lane & 7);
-        vv[m] = buffer_ld16(rsv, live && is_val ? c16 : kBufferNone);
-        dd[m] = buffer_ld4(rss, live && is_run ? 4 * src : kBufferNone);
-        hh[m] = buffer_ld8(rsh, live && is_run ? 8 * src : kBufferNone);
-      }
-      RawRowBlock A0, A1;
-      load_row_block<TYPE>(A0, rsrc, block_off(bA), r);
-      load_row_block<TYPE>(A1, rsrc, block_off(bB), r);
-      float* rs = reinterpret_cast<float*>(lds + M * kn);
-#pragma unroll
-      for (int m = 0; m < M; ++m) {
-        if (live && is_val)
-          reinterpret_cast<uint4*>(lds)[m * (kn / 16) + 16 * (blk - b0) + (lane & 15)] = vv[m];
-        if (live && is_run)
-          QuantizedStage<TYPE, M>::put_run(rs, m * kruns + 8 * (blk - b0) + (lane & 7), __uint_as_float(dd[m]),
-                                           static_cast<int>(hh[m].x + hh[m].y), static_cast<int>(hh[m].y));
-      }
+      ws.put(lds, kn, kruns, b0, bA, bB, b1, lane);
       if (bA < b1) {
         if (PIPE) read_chunk<TYPE, M>(next, lds, kn, kruns, bA - b0, 0);
         row_block<TYPE, M, PIPE>(A0, lds, kn, kruns, bA - b0, bB - b0, bB < b1, next, acc, mins);
@@ -1357,6 +1367,244 @@ __global__ __launch_bounds__(512) void gemv_lds_int8_kernel(
   }
   finish_rows<M, EPI>(acc, mins, rows, y, addend, addend_stride, reinterpret_cast<float*>(lds), sk.partials,
                       sk.counters, sk.ks, fu);
+}
+
+// ---------------------------------------------------------------------------
+// Narrow form of the LDS-staged int8 GEMV (Q4_K, IQ4_XS) for long rows over
+// few output rows, e.g. the FFN down projection 4096 x 14336: 16 rows per
+// work-group instead of 64, so 4096 rows fill the 256 CUs with 256
+// work-groups and need no K split, whose cross-work-group reduction (the
+// partials' agent-scope stores, the ticket, the re-read) costs several
+// microseconds of round trips to memory. Lane = (quarter c = lane >> 4, row
+// group (lane >> 3) & 1, row lane & 7): the four quarters of a wave take
+// the four 64-value chunks of one super-block, so each lane loads only its
+// chunk's two planes and the row's header, and the quarters' activation
+// reads fall in distinct LDS banks. Wave s takes blocks s, s + S, ...,
+// kNarrowDepth of them in flight and the next kNarrowDepth prefetched. The
+// quarters' sums meet by lane shuffles, the waves' through LDS. Sums are
+// formed per chunk (d * (scaled chunk dot)), so results agree with the
+// wide form to rounding, not bit for bit.
+// ---------------------------------------------------------------------------
+
+constexpr int kNarrowRows = 16;
+constexpr int kNarrowDepth = 4;
+
+struct NarrowChunk {
+  uint4 hdr;     // Q4_K: d | dmin, 12 scale bytes; IQ4_XS: d | scales_h, scales_l in .x, .y
+  uint4 qa, qb;  // this row's two 16-byte planes of the chunk
+};
+
+template <int TYPE>
+__device__ inline void load_narrow(NarrowChunk& a, __amdgpu_buffer_rsrc_t rsrc, uint32_t hdr_off, uint32_t plane_off,
+                                   bool live) {
+  if (TYPE == kTypeQ4K) {
+    a.hdr = buffer_ld16(rsrc, live ? hdr_off : kBufferNone);
+  } else {
+    const uint2 h = buffer_ld8(rsrc, live ? hdr_off : kBufferNone);
+    a.hdr = make_uint4(h.x, h.y, 0, 0);
+  }
+  a.qa = buffer_ld16(rsrc, live ? plane_off : kBufferNone);
+  a.qb = buffer_ld16(rsrc, live ? plane_off + 128 : kBufferNone);
+}
+
+// Chunk c (runs 2c, 2c + 1) of block bl of one row against the staged
+// activations of M rows: acc += d * (sc * dot * d_act), mins += dmin * (m *
+// d_act * sum) (Q4_K), acc += d * (ls * dot * d_act) (IQ4_XS).
+template <int TYPE, int M>
+__device__ inline void narrow_chunk(const NarrowChunk& a, int c, const uint8_t* lds, int kn, int kruns, int bl,
+                                    float (&acc)[M], float (&mins)[M]) {
+  const uint8_t* xb = opaque(lds, bl * 256) + 64 * c;
+  uint32_t lo[2][4], hi[2][4];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint4 qq = h ? a.qb : a.qa;
+    const uint32_t w4[4] = {qq.x, qq.y, qq.z, qq.w};
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      lo[h][t] = w4[t] & 0x0F0F0F0Fu;
+      hi[h][t] = (w4[t] >> 4) & 0x0F0F0F0Fu;
+      if (TYPE == kTypeIq4Xs) {
+        lo[h][t] = iq4_lookup4(lo[h][t]);
+        hi[h][t] = iq4_lookup4(hi[h][t]);
+      }
+    }
+  }
+  if constexpr (TYPE == kTypeQ4K) {
+    // runs 2c (low nibbles of both planes) and 2c + 1 (high nibbles)
+    const uint32_t sc_w = c < 2 ? (a.hdr.y & 0x3F3F3F3Fu) : ((a.hdr.w & 0x0F0F0F0Fu) | ((a.hdr.y >> 2) & 0x30303030u));
+    const uint32_t m_w =
+        c < 2 ? (a.hdr.z & 0x3F3F3F3Fu) : (((a.hdr.w >> 4) & 0x0F0F0F0Fu) | ((a.hdr.z >> 2) & 0x30303030u));
+    const int sh = 16 * (c & 1);
+    const int sc0 = static_cast<int>((sc_w >> sh) & 0xFFu), sc1 = static_cast<int>((sc_w >> (sh + 8)) & 0xFFu);
+    const float m0 = static_cast<float>((m_w >> sh) & 0xFFu), m1 = static_cast<float>((m_w >> (sh + 8)) & 0xFFu);
+    const float d = half_bits(a.hdr.x), dmin = half_bits(a.hdr.x >> 16);
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const uint4* x = reinterpret_cast<const uint4*>(xb + m * kn);
+      const uint4 x0 = x[0], x1 = x[1], x2 = x[2], x3 = x[3];
+      int dlo = sdot4(lo[0][0], x0.x, 0);
+      dlo = sdot4(lo[0][1], x0.y, dlo);
+      dlo = sdot4(lo[0][2], x0.z, dlo);
+      dlo = sdot4(lo[0][3], x0.w, dlo);
+      dlo = sdot4(lo[1][0], x1.x, dlo);
+      dlo = sdot4(lo[1][1], x1.y, dlo);
+      dlo = sdot4(lo[1][2], x1.z, dlo);
+      dlo = sdot4(lo[1][3], x1.w, dlo);
+      int dhi = sdot4(hi[0][0], x2.x, 0);
+      dhi = sdot4(hi[0][1], x2.y, dhi);
+      dhi = sdot4(hi[0][2], x2.z, dhi);
+      dhi = sdot4(hi[0][3], x2.w, dhi);
+      dhi = sdot4(hi[1][0], x3.x, dhi);
+      dhi = sdot4(hi[1][1], x3.y, dhi);
+      dhi = sdot4(hi[1][2], x3.z, dhi);
+      dhi = sdot4(hi[1][3], x3.w, dhi);
+      const float4 r = reinterpret_cast<const float4*>(lds + M * kn)[m * (kruns / 2) + bl * 4 + c];
+      float accb = static_cast<float>(__mul24(dlo, sc0)) * r.x;
+      accb = fmaf(static_cast<float>(__mul24(dhi, sc1)), r.z, accb);
+      float minb = m0 * r.y;
+      minb = fmaf(m1, r.w, minb);
+      acc[m] = fmaf(d, accb, acc[m]);
+      mins[m] = fmaf(dmin, minb, mins[m]);
+    }
+  } else {
+    // runs 2c (plane qa: values 0..15 low nibbles, 16..31 high) and 2c + 1 (qb)
+    const uint2 hdr = make_uint2(a.hdr.x, a.hdr.y);
+    const int ls0 = iq4xs_ls(hdr, 2 * c), ls1 = iq4xs_ls(hdr, 2 * c + 1);
+    const float d = half_bits(a.hdr.x);
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const uint4* x = reinterpret_cast<const uint4*>(xb + m * kn);
+      const uint4 x0 = x[0], x1 = x[1], x2 = x[2], x3 = x[3];
+      int d0 = sdot4(lo[0][0], x0.x, 0);
+      d0 = sdot4(lo[0][1], x0.y, d0);
+      d0 = sdot4(lo[0][2], x0.z, d0);
+      d0 = sdot4(lo[0][3], x0.w, d0);
+      d0 = sdot4(hi[0][0], x1.x, d0);
+      d0 = sdot4(hi[0][1], x1.y, d0);
+      d0 = sdot4(hi[0][2], x1.z, d0);
+      d0 = sdot4(hi[0][3], x1.w, d0);
+      int d1 = sdot4(lo[1][0], x2.x, 0);
+      d1 = sdot4(lo[1][1], x2.y, d1);
+      d1 = sdot4(lo[1][2], x2.z, d1);
+      d1 = sdot4(lo[1][3], x2.w, d1);
+      d1 = sdot4(hi[1][0], x3.x, d1);
+      d1 = sdot4(hi[1][1], x3.y, d1);
+      d1 = sdot4(hi[1][2], x3.z, d1);
+      d1 = sdot4(hi[1][3], x3.w, d1);
+      const float2 sv = reinterpret_cast<const float2*>(lds + M * kn)[m * (kruns / 2) + bl * 4 + c];
+      float accb = static_cast<float>(__mul24(d0, ls0)) * sv.x;
+      accb = fmaf(static_cast<float>(__mul24(d1, ls1)), sv.y, accb);
+      acc[m] = fmaf(d, accb, acc[m]);
+    }
+  }
+}
+
+template <int TYPE, int M, bool FUSED>
+__global__ __launch_bounds__(512) void gemv_narrow_kernel(const uint8_t* __restrict__ w, int nb, uint64_t rows,
+                                                          const int8_t* __restrict__ xv, const float* __restrict__ xs,
+                                                          const int32_t* __restrict__ xsum,
+                                                          const float* __restrict__ xf, float* __restrict__ y,
+                                                          const float* __restrict__ addend, uint64_t addend_stride) {
+  constexpr int kTile = TYPE == kTypeQ4K ? kQ4kTileBytes : kIq4xsTileBytes;
+  constexpr int D = kNarrowDepth;
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int lane = threadIdx.x & 63;
+  const int s = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int S = blockDim.x >> 6;
+  const int r = lane & 7, c = lane >> 4;
+  const uint64_t K = static_cast<uint64_t>(nb) * 256;
+  const int kn = nb * 256, kruns = kn / 32;
+  // the work-group's 2 row groups as one buffer resource (a missing second
+  // group reads as zeros; its results are not stored)
+  const uint64_t groups = (rows + 7) / 8, group_bytes = static_cast<uint64_t>(nb) * kTile;
+  const uint64_t g0 = static_cast<uint64_t>(blockIdx.x) * (kNarrowRows / 8);
+  const uint64_t span = (groups - g0 < 2 ? groups - g0 : 2) * group_bytes;
+  const __amdgpu_buffer_rsrc_t rsrc = buffer_rsrc(w + g0 * group_bytes, static_cast<uint32_t>(span));
+  const uint32_t lane_off = static_cast<uint32_t>(((lane >> 3) & 1) * group_bytes);
+  const uint32_t hdr_in = lane_off + (TYPE == kTypeQ4K ? 16u * r : 8u * r);
+  const uint32_t plane_in = lane_off + (TYPE == kTypeQ4K ? 128u : 64u) + 256u * c + 16u * r;
+
+  // Wave s multiplies blocks s, s + S, ...: with at most two per wave (and
+  // up to 4 activation rows) it stages their activations itself, with no
+  // work-group barrier; otherwise the work-group stages all of K.
+  constexpr bool kWaveFit = M <= 4;
+  const bool wave_staged = kWaveFit && nb <= 2 * S;  // work-group uniform
+  FusedStage<TYPE, M, false> fs;
+  QuantizedStage<TYPE, M> qs;
+  WaveStage<TYPE, kWaveFit ? M : 1, FUSED> ws;
+  if (wave_staged) {
+    if constexpr (kWaveFit) ws.load(xf, xv, xs, xsum, K, s, s + S, nb, lane);
+  } else if (FUSED) {
+    fs.load(xf, K, 0, kn, kn);
+  } else {
+    qs.load(xv, xs, xsum, K, 0, kn, kn);
+  }
+  NarrowChunk cur[D];
+#pragma unroll
+  for (int j = 0; j < D; ++j) {
+    const int b = s + j * S;
+    load_narrow<TYPE>(cur[j], rsrc, hdr_in + b * kTile, plane_in + b * kTile, b < nb);
+  }
+  if (wave_staged) {
+    if constexpr (kWaveFit) ws.put(lds, kn, kruns, 0, s, s + S, nb, lane);
+  } else {
+    if (FUSED)
+      fs.store(xf, K, 0, kn, kn, lds, 1.0f, nullptr);
+    else
+      qs.store(xv, xs, xsum, K, 0, kn, kn, lds);
+    __syncthreads();
+  }
+
+  float acc[M], mins[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) acc[m] = mins[m] = 0.0f;
+  for (int base = s; base < nb; base += D * S) {
+    NarrowChunk nxt[D];
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      const int b = base + (D + j) * S;
+      load_narrow<TYPE>(nxt[j], rsrc, hdr_in + b * kTile, plane_in + b * kTile, b < nb);
+    }
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      const int b = base + j * S;  // wave-uniform
+      if (b < nb) narrow_chunk<TYPE, M>(cur[j], c, lds, kn, kruns, b, acc, mins);
+    }
+#pragma unroll
+    for (int j = 0; j < D; ++j) cur[j] = nxt[j];
+  }
+  // the four quarters of each row (lanes l, l ^ 16, l ^ 32, l ^ 48), then the waves
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    acc[m] += __shfl_xor(acc[m], 16);
+    acc[m] += __shfl_xor(acc[m], 32);
+    mins[m] += __shfl_xor(mins[m], 16);
+    mins[m] += __shfl_xor(mins[m], 32);
+  }
+  __syncthreads();  // every wave is done reading activations
+  float* red = reinterpret_cast<float*>(lds);
+  if (lane < kNarrowRows) {
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      red[((s * M + m) * 2 + 0) * kNarrowRows + lane] = acc[m];
+      red[((s * M + m) * 2 + 1) * kNarrowRows + lane] = mins[m];
+    }
+  }
+  __syncthreads();
+  if (s != 0 || lane >= kNarrowRows) return;
+  const uint64_t row = static_cast<uint64_t>(blockIdx.x) * kNarrowRows + lane;
+  if (row >= rows) return;
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    float a = red[(m * 2 + 0) * kNarrowRows + lane], mn = red[(m * 2 + 1) * kNarrowRows + lane];
+    for (int i = 1; i < S; ++i) {
+      a += red[((i * M + m) * 2 + 0) * kNarrowRows + lane];
+      mn += red[((i * M + m) * 2 + 1) * kNarrowRows + lane];
+    }
+    float v = a - mn;
+    if (addend) v = v + addend[m * addend_stride + row];
+    y[m * rows + row] = v;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -3245,11 +3493,68 @@ size_t gemv_lds_bytes(int type, uint64_t nbk, uint64_t m, int splits) {
 
 int lds_form_max_splits(uint64_t) { return 8; }  // launch bound 512
 
+// The 16-row form, when asked or by default where the 64-row form would
+// split K and the 16-row grid is 128..256 work-groups (one round over the
+// CUs; measured at 4096 rows: 4096 x 4096 6.2 us against 6.8, IQ4_XS
+// 4096 x 14336 pre-quantized 10.2 us against 12.8; at 6144 rows, 384
+// work-groups, 9.8 against 7.1). Fused quantization only up to 16 blocks of
+// K: each work-group quantizes all of K, which at 4096 x 14336 costs more
+// (12.3 us) than the K split saves (10.4). Its LDS (all of K staged) must
+// fit.
+bool narrow_form(int type, uint64_t rows, uint64_t nb, uint64_t m, bool fused, const GemvSplitK& sk, size_t& lds) {
+  if (sk.narrow == 0) return false;
+  if (sk.narrow < 0) {
+    const uint64_t wgs = (rows + kNarrowRows - 1) / kNarrowRows;
+    if (sk.ks <= 1 || wgs < 128 || wgs > 256 || (fused && nb > 16)) return false;
+  }
+  lds = gemv_lds_bytes(type, nb, m, 8);
+  return lds <= 65536;
+}
+
+template <bool FUSED>
+void launch_gemv_narrow(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, const int8_t* values,
+                        const float* scales, const int32_t* sums, const float* x, uint64_t m, float* y,
+                        const float* addend, uint64_t addend_stride, size_t lds, hipStream_t stream) {
+  dim3 grid(static_cast<unsigned>((rows + kNarrowRows - 1) / kNarrowRows)), block(512);
+  const int inb = static_cast<int>(nb);
+  if (type == kTypeQ4K) {
+    switch (m) {
+#define X(MM)                                                                                                  \
+  case MM:                                                                                                     \
+    hipLaunchKernelGGL((gemv_narrow_kernel<kTypeQ4K, MM, FUSED>), grid, block, lds, stream, tiled, inb, rows,   \
+                       values, scales, sums, x, y, addend, addend_stride);                                     \
+    break;
+      MQ_GEMV_CASES(X)
+#undef X
+      default:
+        break;
+    }
+  } else {
+    switch (m) {
+#define X(MM)                                                                                                    \
+  case MM:                                                                                                       \
+    hipLaunchKernelGGL((gemv_narrow_kernel<kTypeIq4Xs, MM, FUSED>), grid, block, lds, stream, tiled, inb, rows,   \
+                       values, scales, nullptr, x, y, addend, addend_stride);                                    \
+    break;
+      MQ_GEMV_CASES(X)
+#undef X
+      default:
+        break;
+    }
+  }
+}
+
 template <bool FUSED>
 void launch_gemv_lds(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, const int8_t* values,
                      const float* scales, const int32_t* sums, const float* x, uint64_t m, float* y,
                      const float* addend, uint64_t addend_stride, int splits, const GemvSplitK& sk, size_t lds,
                      hipStream_t stream) {
+  size_t narrow_lds = 0;
+  if (narrow_form(type, rows, nb, m, FUSED, sk, narrow_lds)) {
+    launch_gemv_narrow<FUSED>(type, tiled, rows, nb, values, scales, sums, x, m, y, addend, addend_stride,
+                              narrow_lds, stream);
+    return;
+  }
   dim3 grid(static_cast<unsigned>((rows + 63) / 64), static_cast<unsigned>(sk.ks)), block(64 * splits);
   const int inb = static_cast<int>(nb);
   const SplitK k{sk.partials, sk.counters, sk.ks};

@@ -30,11 +30,14 @@ void launch_activations_f16(const float* x, uint64_t m, uint64_t k, uint16_t* a1
 // Split-K across work-groups for the LDS-staged GEMV: ks work-groups share
 // each 64-row block; partials holds ks * m * 2 * (row blocks * 64) f32 and
 // counters one zero-initialised u32 per row block (each launch leaves them
-// zero again). ks == 1 needs neither.
+// zero again). ks == 1 needs neither. narrow: 1 = the 16-row form instead
+// (no K split; used when its LDS fits), 0 = never, -1 = where the 64-row
+// form would split K.
 struct GemvSplitK {
   float* partials = nullptr;
   uint32_t* counters = nullptr;
   int ks = 1;
+  int narrow = -1;
 };
 int gemv_default_ksplit(uint64_t rows, uint64_t nb);
 

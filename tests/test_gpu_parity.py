@@ -439,6 +439,50 @@ def _context_with(env):
 
 
 @pytest.mark.parametrize("fmt", [Q4_K, IQ4_XS])
+def test_gemv_narrow_form(fmt):
+    """The 16-row form (four lane quarters over the chunks of a block, no K
+    split), forced for every shape: ragged row counts, 1..32 blocks (wave-
+    and work-group-staged activations), m = 1..8, fused and pre-quantized
+    (bit-identical to each other and when repeated), and with a residual;
+    within the reference's tolerance of the dense oracle."""
+    c = _context_with({"MQ_GEMV_NARROW": 1})
+    stream = torch.cuda.current_stream().cuda_stream
+    try:
+        for n, k in ((1000, 2048), (37, 1280), (300, 4608), (9, 256), (40, 8192)):
+            w = mg.quantize(fmt, mg.gaussian(n + k + 7, 0.02, n * k).reshape(n, k))
+            h = c.upload(fmt, n, k, w)
+            try:
+                for m in (1, 3, 4, 5, 8):
+                    a = mg.gaussian(500 + m, 1.0, m * k).reshape(m, k)
+                    got = c.matmul(h, a)
+                    np.testing.assert_array_equal(got.view(np.uint32), c.matmul(h, a).view(np.uint32))
+                    exp = expected(fmt, w, n, k, a, True)
+                    assert_close_reference(got, exp, f"n {n} k {k} m {m}")
+                    xd = dev(a)
+                    v = torch.empty(m * k, dtype=torch.int8, device="cuda")
+                    sc = torch.empty(m * k // 32, dtype=torch.float32, device="cuda")
+                    sm = torch.empty(m * k // 16, dtype=torch.int32, device="cuda")
+                    c.quantize_activations_dev(xd.data_ptr(), m, k, v.data_ptr(), sc.data_ptr(), sm.data_ptr(),
+                                               stream)
+                    y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+                    c.matmul_prequantized_dev(h, v.data_ptr(), sc.data_ptr(), sm.data_ptr(), m, k, y.data_ptr(),
+                                              stream)
+                    torch.cuda.synchronize()
+                    np.testing.assert_array_equal(y.cpu().numpy(), got, err_msg=f"pre-quantized n {n} m {m}")
+                    r = mg.gaussian(600 + m, 1.0, m * n).reshape(m, n)
+                    rd = dev(r)
+                    y2 = torch.empty((m, n), dtype=torch.float32, device="cuda")
+                    c.matmul_add_dev(h, xd.data_ptr(), m, k, rd.data_ptr(), m, y2.data_ptr())
+                    torch.cuda.synchronize()
+                    np.testing.assert_array_equal(y2.cpu().numpy(), (got + r).astype(np.float32),
+                                                  err_msg=f"residual n {n} m {m}")
+            finally:
+                h.release()
+    finally:
+        c.close()
+
+
+@pytest.mark.parametrize("fmt", [Q4_K, IQ4_XS])
 @pytest.mark.parametrize("variant,ksplit,splits", [(0, 1, 0), (0, 2, 0), (0, 3, 4), (0, 5, 8), (0, 16, 16),
                                                    (3, 4, 2), (3, 7, 0), (2, 1, 8), (1, 1, 4)])
 def test_gemv_forms_and_k_splits(fmt, variant, ksplit, splits):
