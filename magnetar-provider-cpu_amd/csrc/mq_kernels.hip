@@ -623,24 +623,32 @@ __device__ inline float wave_sum64(float v) {
   return v;
 }
 
-// 1 / sqrt(mean(x^2) + eps) of the activation row, over the work-group
-// (the whole row, whatever the work-group's K range).
-__device__ inline float row_norm_scale(const float* __restrict__ x, uint64_t K, float eps) {
+// Thread t's share of the row's sum of squares: float4 elements t,
+// t + blockDim, ... in that order.
+__device__ inline void add_squares(float& ss, float4 a) {
+  ss += a.x * a.x;
+  ss += a.y * a.y;
+  ss += a.z * a.z;
+  ss += a.w * a.w;
+}
+
+// 1 / sqrt(mean(x^2) + eps) from the threads' shares, over the work-group.
+__device__ inline float norm_from_squares(float ss, uint64_t K, float eps) {
   __shared__ float part[8];
-  float ss = 0.0f;
-  for (uint64_t i = threadIdx.x; i < K / 4; i += blockDim.x) {
-    const float4 a = reinterpret_cast<const float4*>(x)[i];
-    ss += a.x * a.x;
-    ss += a.y * a.y;
-    ss += a.z * a.z;
-    ss += a.w * a.w;
-  }
   ss = wave_sum64(ss);
   if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
   __syncthreads();
   float total = 0.0f;
   for (int i = 0; i < static_cast<int>(blockDim.x >> 6); ++i) total += part[i];
   return 1.0f / sqrtf(total / static_cast<float>(K) + eps);
+}
+
+// 1 / sqrt(mean(x^2) + eps) of the activation row, over the work-group
+// (the whole row, whatever the work-group's K range).
+__device__ inline float row_norm_scale(const float* __restrict__ x, uint64_t K, float eps) {
+  float ss = 0.0f;
+  for (uint64_t i = threadIdx.x; i < K / 4; i += blockDim.x) add_squares(ss, reinterpret_cast<const float4*>(x)[i]);
+  return norm_from_squares(ss, K, eps);
 }
 
 // Stores one lane's row results (every lane of the wave calls it: the
@@ -827,6 +835,20 @@ struct FusedStage {
         rs[run] = q.d;
       }
     }
+  }
+
+  // The rmsnorm scale of the (one) activation row. When the registers hold
+  // the whole row (no K split, K / 4 <= kPre * blockDim) its squares add up
+  // from them, the elements and order of row_norm_scale (the same value),
+  // without reading x again behind the weight loads already issued.
+  __device__ float norm_scale(const float* __restrict__ xf, uint64_t K, int kn, float eps) const {
+    if (static_cast<uint64_t>(kn) != K || K / 4 > kPre * static_cast<uint64_t>(blockDim.x))
+      return row_norm_scale(xf, K, eps);
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kPre; ++j)
+      if (static_cast<uint64_t>(j) * blockDim.x + threadIdx.x < K / 4) add_squares(ss, v[j]);
+    return norm_from_squares(ss, K, eps);
   }
 
   __device__ void store(const float* __restrict__ xf, uint64_t K, uint64_t k0, int kn, int kv, uint8_t* lds,
@@ -1350,7 +1372,7 @@ __global__ __launch_bounds__(512) void gemv_lds_int8_kernel(
     load_row_block<TYPE>(A, rsrc, block_off(bA), r);
     // 3. activations into LDS (rmsnorm'd first under NORM)
     float nscale = 1.0f;
-    if constexpr (NORM) nscale = row_norm_scale(xf, K, fu.norm_eps);
+    if constexpr (NORM) nscale = fs.norm_scale(xf, K, kn, fu.norm_eps);
     if (FUSED)
       fs.store(xf, K, k0, kn, kn, lds, nscale, fu.norm_w);
     else
@@ -1380,14 +1402,14 @@ __global__ __launch_bounds__(512) void gemv_lds_int8_kernel(
 // the four 64-value chunks of one super-block, so each lane loads only its
 // chunk's two planes and the row's header, and the quarters' activation
 // reads fall in distinct LDS banks. Wave s takes blocks s, s + S, ...,
-// kNarrowDepth of them in flight and the next kNarrowDepth prefetched. The
+// kNarrowDepth of them in the math and the next kNarrowDepth in flight. The
 // quarters' sums meet by lane shuffles, the waves' through LDS. Sums are
 // formed per chunk (d * (scaled chunk dot)), so results agree with the
 // wide form to rounding, not bit for bit.
 // ---------------------------------------------------------------------------
 
 constexpr int kNarrowRows = 16;
-constexpr int kNarrowDepth = 4;
+constexpr int kNarrowDepth = 2;  // measured at 4096 x 14336 IQ4_XS: depth 1 9.4 us, 2 8.7, 4 10.4, 8 12.1
 
 struct NarrowChunk {
   uint4 hdr;     // Q4_K: d | dmin, 12 scale bytes; IQ4_XS: d | scales_h, scales_l in .x, .y
@@ -1499,12 +1521,15 @@ __device__ inline void narrow_chunk(const NarrowChunk& a, int c, const uint8_t* 
   }
 }
 
-template <int TYPE, int M, bool FUSED>
+template <int TYPE, int M, bool FUSED, bool NORM = false, int EPI = kEpiPlain>
 __global__ __launch_bounds__(512) void gemv_narrow_kernel(const uint8_t* __restrict__ w, int nb, uint64_t rows,
                                                           const int8_t* __restrict__ xv, const float* __restrict__ xs,
                                                           const int32_t* __restrict__ xsum,
                                                           const float* __restrict__ xf, float* __restrict__ y,
-                                                          const float* __restrict__ addend, uint64_t addend_stride) {
+                                                          const float* __restrict__ addend, uint64_t addend_stride,
+                                                          Fusion fu) {
+  static_assert(!NORM || (FUSED && M == 1), "the rmsnorm staging takes one f32 activation row");
+  static_assert(EPI != kEpiSiluPairs, "the silu pairs span 64-row blocks");
   constexpr int kTile = TYPE == kTypeQ4K ? kQ4kTileBytes : kIq4xsTileBytes;
   constexpr int D = kNarrowDepth;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -1527,15 +1552,15 @@ __global__ __launch_bounds__(512) void gemv_narrow_kernel(const uint8_t* __restr
   // Wave s multiplies blocks s, s + S, ...: with at most two per wave (and
   // up to 4 activation rows) it stages their activations itself, with no
   // work-group barrier; otherwise the work-group stages all of K.
-  constexpr bool kWaveFit = M <= 4;
+  constexpr bool kWaveFit = M <= 4 && !NORM;
   const bool wave_staged = kWaveFit && nb <= 2 * S;  // work-group uniform
-  FusedStage<TYPE, M, false> fs;
+  FusedStage<TYPE, M, NORM> fs;
   QuantizedStage<TYPE, M> qs;
   WaveStage<TYPE, kWaveFit ? M : 1, FUSED> ws;
   if (wave_staged) {
     if constexpr (kWaveFit) ws.load(xf, xv, xs, xsum, K, s, s + S, nb, lane);
   } else if (FUSED) {
-    fs.load(xf, K, 0, kn, kn);
+    fs.load(xf, K, 0, kn, kn, fu.norm_w);
   } else {
     qs.load(xv, xs, xsum, K, 0, kn, kn);
   }
@@ -1548,8 +1573,10 @@ __global__ __launch_bounds__(512) void gemv_narrow_kernel(const uint8_t* __restr
   if (wave_staged) {
     if constexpr (kWaveFit) ws.put(lds, kn, kruns, 0, s, s + S, nb, lane);
   } else {
+    float nscale = 1.0f;  // rmsnorm'd first under NORM
+    if constexpr (NORM) nscale = fs.norm_scale(xf, K, kn, fu.norm_eps);
     if (FUSED)
-      fs.store(xf, K, 0, kn, kn, lds, 1.0f, nullptr);
+      fs.store(xf, K, 0, kn, kn, lds, nscale, fu.norm_w);
     else
       qs.store(xv, xs, xsum, K, 0, kn, kn, lds);
     __syncthreads();
@@ -1591,20 +1618,24 @@ __global__ __launch_bounds__(512) void gemv_narrow_kernel(const uint8_t* __restr
     }
   }
   __syncthreads();
-  if (s != 0 || lane >= kNarrowRows) return;
-  const uint64_t row = static_cast<uint64_t>(blockIdx.x) * kNarrowRows + lane;
-  if (row >= rows) return;
+  if (s != 0) return;
+  // wave 0 stays whole for the epilogue's lane pairs; lanes 16..63 repeat
+  // lanes 0..15 and store nothing
+  const int i16 = lane & (kNarrowRows - 1);
+  const uint64_t row = static_cast<uint64_t>(blockIdx.x) * kNarrowRows + i16;
+  const bool valid = lane < kNarrowRows && row < rows;
+  float v[M];
 #pragma unroll
   for (int m = 0; m < M; ++m) {
-    float a = red[(m * 2 + 0) * kNarrowRows + lane], mn = red[(m * 2 + 1) * kNarrowRows + lane];
+    float a = red[(m * 2 + 0) * kNarrowRows + i16], mn = red[(m * 2 + 1) * kNarrowRows + i16];
     for (int i = 1; i < S; ++i) {
-      a += red[((i * M + m) * 2 + 0) * kNarrowRows + lane];
-      mn += red[((i * M + m) * 2 + 1) * kNarrowRows + lane];
+      a += red[((i * M + m) * 2 + 0) * kNarrowRows + i16];
+      mn += red[((i * M + m) * 2 + 1) * kNarrowRows + i16];
     }
-    float v = a - mn;
-    if (addend) v = v + addend[m * addend_stride + row];
-    y[m * rows + row] = v;
+    v[m] = a - mn;
+    if (addend && valid) v[m] = v[m] + addend[m * addend_stride + row];
   }
+  store_out<M, EPI>(v, row, valid, lane, rows, y, fu);
 }
 
 // ---------------------------------------------------------------------------
@@ -3494,18 +3525,19 @@ size_t gemv_lds_bytes(int type, uint64_t nbk, uint64_t m, int splits) {
 int lds_form_max_splits(uint64_t) { return 8; }  // launch bound 512
 
 // The 16-row form, when asked or by default where the 64-row form would
-// split K and the 16-row grid is 128..256 work-groups (one round over the
-// CUs; measured at 4096 rows: 4096 x 4096 6.2 us against 6.8, IQ4_XS
-// 4096 x 14336 pre-quantized 10.2 us against 12.8; at 6144 rows, 384
-// work-groups, 9.8 against 7.1). Fused quantization only up to 16 blocks of
-// K: each work-group quantizes all of K, which at 4096 x 14336 costs more
-// (12.3 us) than the K split saves (10.4). Its LDS (all of K staged) must
-// fit.
+// split K and the 16-row grid is 128..384 work-groups (measured: IQ4_XS
+// 4096 x 14336 pre-quantized 8.8 us against 12.8 split four ways; Q4_K
+// 4096 x 4096 4.7 against 6.8; 6144 x 4096 5.8 against 7.0; at 14336 rows,
+// 896 work-groups, slower: 10.5 against 8.4). Fused quantization only up
+// to 16 blocks of K: each
+// work-group quantizes all of K, which at Q4_K 4096 x 14336 costs more than
+// the K split saves (the decoder step 1 us slower). Its LDS (all of K
+// staged) must fit.
 bool narrow_form(int type, uint64_t rows, uint64_t nb, uint64_t m, bool fused, const GemvSplitK& sk, size_t& lds) {
   if (sk.narrow == 0) return false;
   if (sk.narrow < 0) {
     const uint64_t wgs = (rows + kNarrowRows - 1) / kNarrowRows;
-    if (sk.ks <= 1 || wgs < 128 || wgs > 256 || (fused && nb > 16)) return false;
+    if (sk.ks <= 1 || wgs < 128 || wgs > 384 || (fused && nb > 16)) return false;
   }
   lds = gemv_lds_bytes(type, nb, m, 8);
   return lds <= 65536;
@@ -3522,7 +3554,7 @@ void launch_gemv_narrow(int type, const uint8_t* tiled, uint64_t rows, uint64_t 
 #define X(MM)                                                                                                  \
   case MM:                                                                                                     \
     hipLaunchKernelGGL((gemv_narrow_kernel<kTypeQ4K, MM, FUSED>), grid, block, lds, stream, tiled, inb, rows,   \
-                       values, scales, sums, x, y, addend, addend_stride);                                     \
+                       values, scales, sums, x, y, addend, addend_stride, Fusion{});                           \
     break;
       MQ_GEMV_CASES(X)
 #undef X
@@ -3534,7 +3566,7 @@ void launch_gemv_narrow(int type, const uint8_t* tiled, uint64_t rows, uint64_t 
 #define X(MM)                                                                                                    \
   case MM:                                                                                                       \
     hipLaunchKernelGGL((gemv_narrow_kernel<kTypeIq4Xs, MM, FUSED>), grid, block, lds, stream, tiled, inb, rows,   \
-                       values, scales, nullptr, x, y, addend, addend_stride);                                    \
+                       values, scales, nullptr, x, y, addend, addend_stride, Fusion{});                          \
     break;
       MQ_GEMV_CASES(X)
 #undef X
@@ -3690,13 +3722,30 @@ bool launch_gemv_fused(int type, const uint8_t* tiled, uint64_t rows, uint64_t n
 bool launch_gemv_decode_fused(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, const float* x, float* y,
                               bool norm, int epilogue, const GemvFusion& fu, const GemvSplitK& sk,
                               hipStream_t stream) {
+  const int inb = static_cast<int>(nb);
+  const int key = (type == kTypeQ4K ? 0 : 8) + (norm ? 4 : 0) + epilogue;
+  size_t narrow_lds = 0;
+  if (epilogue != kEpiSiluPairs && narrow_form(type, rows, nb, 1, true, sk, narrow_lds)) {
+    // the same form as the plain fused GEMV of this shape takes
+    dim3 grid(static_cast<unsigned>((rows + kNarrowRows - 1) / kNarrowRows)), block(512);
+    switch (key) {
+#define X(T, KEY, N, E)                                                                                        \
+  case KEY:                                                                                                    \
+    hipLaunchKernelGGL((gemv_narrow_kernel<T, 1, true, N, E>), grid, block, narrow_lds, stream, tiled, inb,     \
+                       rows, nullptr, nullptr, nullptr, x, y, nullptr, 0, fu);                                 \
+    return true;
+      X(kTypeQ4K, 1, false, kEpiRope) X(kTypeQ4K, 4, true, kEpiPlain) X(kTypeQ4K, 5, true, kEpiRope)
+      X(kTypeIq4Xs, 9, false, kEpiRope) X(kTypeIq4Xs, 12, true, kEpiPlain) X(kTypeIq4Xs, 13, true, kEpiRope)
+#undef X
+      default:
+        return false;
+    }
+  }
   int splits = 0;
   size_t lds = 0;
   if (!lds_form_shape(type, rows, nb, 1, 0, sk.ks, splits, lds)) return false;
   dim3 grid(static_cast<unsigned>((rows + 63) / 64), static_cast<unsigned>(sk.ks)), block(64 * splits);
-  const int inb = static_cast<int>(nb);
   const SplitK k{sk.partials, sk.counters, sk.ks};
-  const int key = (type == kTypeQ4K ? 0 : 8) + (norm ? 4 : 0) + epilogue;
   switch (key) {
 #define X(T, KEY, N, E)                                                                                              \
   case KEY:                                                                                                          \

@@ -190,9 +190,32 @@ def _q4k(seed, n, k):
     return mg.quantize(mg.Q4_K, mg.gaussian(seed, 0.02, n * k).reshape(n, k))
 
 
-def test_rope_kv_epilogue_equals_the_unfused_chain(ctx):
+@pytest.fixture(params=["default", "narrow"])
+def form_ctx(request, ctx):
+    """The session context (this test's shapes take the 64-row GEMV form),
+    and one whose GEMVs all take the 16-row form."""
+    if request.param == "default":
+        yield ctx
+        return
+    import os
+    old = os.environ.get("MQ_GEMV_NARROW")
+    os.environ["MQ_GEMV_NARROW"] = "1"
+    try:
+        c = mg.Context(0)
+    finally:
+        if old is None:
+            del os.environ["MQ_GEMV_NARROW"]
+        else:
+            os.environ["MQ_GEMV_NARROW"] = old
+    yield c
+    c.close()
+
+
+def test_rope_kv_epilogue_equals_the_unfused_chain(form_ctx):
     """GEMV + rope + kv-write in one launch equals matmul_dev, rope_dev and
-    kv_write_dev bit for bit (same kernel results, same rotation)."""
+    kv_write_dev bit for bit (same kernel results, same rotation), in
+    either GEMV form."""
+    ctx = form_ctx
     n, k, dim, pos = 768, 1024, 64, 37
     w = _q4k(5, n, k)
     h = ctx.upload(mg.Q4_K, n, k, w)
@@ -240,11 +263,13 @@ def test_silu_pairs_epilogue_equals_silu_mul(ctx):
         h.release()
 
 
-def test_norm_staging_matches_rmsnorm_then_matmul(ctx):
+@pytest.mark.parametrize("n", [4096, 6144, 14336])
+def test_norm_staging_matches_rmsnorm_then_matmul(ctx, n):
     """rmsnorm folded into the GEMV's staging: within the matmul bar of the
     rmsnorm_dev + matmul_dev chain (the sum of squares adds in another
-    order, so an int8 rounding may differ), and of the oracle."""
-    n, k = 4096, 4096
+    order, so an int8 rounding may differ), and of the oracle; at row
+    counts that take the 16-row form (4096, 6144) and the 64-row form."""
+    k = 4096
     w = _q4k(8, n, k)
     h = ctx.upload(mg.Q4_K, n, k, w)
     xh = (rng(5).standard_normal((1, k)) * 3).astype(np.float32)
