@@ -483,7 +483,7 @@ def emit(args, value, steps, warmup, ms_per_step, n, k, weight_bytes, use_graph,
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": recorded_traffic("gemv_q4k_m1_fused"),
             "traffic_unit": "HBM bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
             "algorithmic_bytes": weight_bytes + 4 * k + 4 * n, "kernel_us": round(kernel_us, 3),
-            "kernel": "gemv_lds_q4k_int8_kernel<1, fused>: int8 quantization of x in LDS + Q4_K GEMV, one launch",
+            "kernel": "gemv_lds_int8_kernel<Q4_K, 1, fused> (64-row form): int8 quantization of x in LDS + Q4_K GEMV, one launch",
         },
         "cpu_baseline": cpu,
         "gemm": gemm,
