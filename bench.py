@@ -352,7 +352,7 @@ def formats_part(ctx, torch, per_graph, use_graph, extra):
         for h in copies:
             h.release()
     # the IQ2 / IQ3 grid formats (stand-in grid tables of the real shapes): the
-    # decode GEMV, and M = 512 as the 8-row GEMVs these formats' prefill runs
+    # decode GEMV and the M = 512 prefill GEMM (raw blocks decoded per lane)
     ctx.set_iq_grids(workloads.synthetic_iq_grids(1))
     for fmt in mg.GRID_FORMATS:
         name = mg.FORMAT_NAMES[fmt]
@@ -372,12 +372,14 @@ def formats_part(ctx, torch, per_graph, use_graph, extra):
         def gm(i, stream, copies=copies):
             ctx.matmul_dev(copies[i % len(copies)], xm.data_ptr(), 512, k, ym.data_ptr(), int8=True, stream=stream)
 
-        rg = GraphRunner(torch, gm, 2, use_graph)
-        rg.time(2)
-        tg = rg.time(4) / 4
-        extra[f"{name}_prefill512_us"] = round(tg * 1e6, 1)
+        rg = GraphRunner(torch, gm, 5, use_graph)
+        rg.time(5)
+        tg = rg.time(20) / 20
+        tflops = 2 * 512 * n * k / tg / 1e12
+        extra[f"{name}_gemm512_us"] = round(tg * 1e6, 2)
+        extra[f"{name}_gemm512_TFLOPs"] = round(tflops, 1)
         log(f"{name}: gemv {t * 1e6:.2f} us, {w.size / t / 1e9:.1f} GB/s ({w.size} B); "
-            f"M=512 as 8-row GEMVs {tg * 1e6:.0f} us")
+            f"M=512 gemm {tg * 1e6:.1f} us, {tflops:.1f} TFLOP/s")
         for h in copies:
             h.release()
 

@@ -78,7 +78,10 @@ const char *mq_last_error(mq_ctx *ctx);
  * device shares them. The reference reads these statics from the external
  * magnetar-provider-api crate (src/native/quant.rs:14, 1057-1061): a Rust
  * binding passes them once at start-up. Waits for this context's queued
- * work first; work queued on other streams must not be running. */
+ * work first; work queued on other streams must not be running. When every
+ * table byte is below 128 (true of the GGUF grids), prefill matmuls of the
+ * grid formats run on the MFMA GEMM; otherwise as 8-row decode GEMVs, and
+ * mq_matmul_f16_dev declines them. */
 int mq_set_iq_grids(mq_ctx *ctx, const uint64_t *iq2xxs, const uint64_t *iq2xs, const uint64_t *iq2s,
                     const uint32_t *iq3xxs, const uint32_t *iq3s);
 

@@ -105,13 +105,22 @@ bool known_type(uint32_t type) {
 bool plane_type(uint32_t type) { return mq::is_plane_format(static_cast<int>(type)); }
 bool grid_type(uint32_t type) { return mq::is_grid_format(static_cast<int>(type)); }
 
-// Devices whose copy of the IQ2 / IQ3 grid tables has been filled.
+// Devices whose copy of the IQ2 / IQ3 grid tables has been filled, and
+// those whose tables hold only magnitude bytes below 128 (every GGUF grid
+// does): the MFMA prefill reads the magnitudes as unsigned bytes, so other
+// tables keep the 8-row GEMV prefill.
 std::mutex g_grid_mu;
 std::set<int> g_grid_devices;
+std::set<int> g_grid_gemm_devices;
 
 bool grids_ready(int device) {
   std::lock_guard<std::mutex> lock(g_grid_mu);
   return g_grid_devices.count(device) != 0;
+}
+
+bool grid_gemm_ready(int device) {
+  std::lock_guard<std::mutex> lock(g_grid_mu);
+  return g_grid_gemm_devices.count(device) != 0;
 }
 
 class DeviceGuard {
@@ -329,8 +338,7 @@ int matmul_locked(mq_ctx* ctx, const Weight& w, const float* x, uint64_t m, uint
     if (rc) return rc;
     mq::launch_axpy(static_cast<int>(w.type), w.dev, w.nb, k, n, x, m, y, addend, addend_stride,
                     static_cast<float*>(ctx->ws), ks, stream);
-  } else if (m <= kGemvChunkRows || k < kGemmMinK || grid_type(w.type)) {
-    // (the grid formats have no MFMA form: their prefill is 8-row GEMVs)
+  } else if (m <= kGemvChunkRows || k < kGemmMinK || (grid_type(w.type) && !grid_gemm_ready(ctx->device))) {
     for (uint64_t r0 = 0; r0 < m; r0 += kGemvMaxRows) {
       const uint64_t mc = m - r0 < kGemvMaxRows ? m - r0 : kGemvMaxRows;
       const float* ad = addend ? addend + (addend_stride ? r0 * w.rows : 0) : nullptr;
@@ -488,8 +496,14 @@ int mq_set_iq_grids(mq_ctx* ctx, const uint64_t* iq2xxs, const uint64_t* iq2xs, 
   // queued work of this context may still read the previous tables
   MQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
   MQ_HIP(ctx, mq::grid_tables_upload(tables.data(), ctx->stream));
+  bool small = true;
+  for (uint8_t b : tables) small = small && b < 128;
   std::lock_guard<std::mutex> glock(g_grid_mu);
   g_grid_devices.insert(ctx->device);
+  if (small)
+    g_grid_gemm_devices.insert(ctx->device);
+  else
+    g_grid_gemm_devices.erase(ctx->device);
   return MQ_OK;
 }
 
@@ -750,7 +764,8 @@ int mq_matmul_f16_dev(mq_ctx* ctx, uint64_t handle, const uint16_t* a16_dev, uin
   if (rc) return rc;
   if (m == 0) return MQ_OK;
   if (!a16_dev || !y_dev) return fail(ctx, MQ_ERR_ARGUMENT, "mq_matmul_f16_dev: null pointer");
-  if (grid_type(w->type)) return fail(ctx, MQ_DECLINED, "the IQ2 / IQ3 grid formats have no f16 MFMA GEMM");
+  if (grid_type(w->type) && !grid_gemm_ready(ctx->device))
+    return fail(ctx, MQ_DECLINED, "the f16 MFMA GEMM of the IQ2 / IQ3 grid formats needs grid magnitudes below 128");
   DeviceGuard guard(ctx->device);
   hipStream_t s = static_cast<hipStream_t>(stream);
   mq::launch_gemm(static_cast<int>(w->type), w->dev, w->rows, w->nb, w->cols, a16_dev, m, y_dev, nullptr, 0,

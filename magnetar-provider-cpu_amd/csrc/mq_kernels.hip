@@ -3452,6 +3452,281 @@ __global__ __launch_bounds__(kKsThreads) void gemm_ks_kernel(const uint8_t* __re
   }
 }
 
+// ---------------------------------------------------------------------------
+// Grid-format prefill GEMM, `gemm_grid_kernel<F, MF, NF>` (IQ2_XXS, IQ2_XS,
+// IQ2_S, IQ3_XXS, IQ3_S; src/native/quant.rs:207-277 decode).
+//
+// The register-B structure of gemm_rb_kernel: a 16 MF x 64 NF output tile
+// per work-group (4 waves side by side in N), A (f16 activations)
+// double-buffered through LDS, B decoded per lane. Lane (li, kq) of a
+// v_mfma_f32_16x16x32_f16 holds column li and K values 8 kq .. 8 kq + 7 of a
+// 32-value run: exactly grid group kq of that run (one 8-magnitude IQ2
+// entry, or two 4-magnitude IQ3 entries), its sign byte and the scale of
+// half kq >> 1. So each lane reads only its group's block fields (16-bit
+// loads of the raw blocks, one super-block ahead). The format's grid table
+// and a sign-byte -> f16 sign-mask table are copied to LDS at start.
+//
+// B = +-(scale * magnitude) rounded once to f16: the magnitude byte becomes
+// the f16 1024 + m by a byte permute, v_fma_mix forms s (1024 + m) - 1024 s
+// = s m in f32 (exact before its one rounding, 1024 s being exact) and
+// rounds it to f16, and the sign is an xor of the f16 sign bit. This reads
+// the magnitudes as unsigned bytes; the host routes a weight here only when
+// every byte of its grid table is below 128, where that equals the i8
+// reading of `grid_value`.
+// ---------------------------------------------------------------------------
+
+__host__ __device__ constexpr int grid_table_offset(int type) {
+  return type == kTypeIq2Xxs ? kGridIq2Xxs
+         : type == kTypeIq2Xs ? kGridIq2Xs
+         : type == kTypeIq2S  ? kGridIq2S
+         : type == kTypeIq3Xxs ? kGridIq3Xxs
+                               : kGridIq3S;
+}
+__host__ __device__ constexpr int grid_table_size(int type) {
+  return type == kTypeIq2Xxs ? 2048 : type == kTypeIq2Xs ? 4096 : type == kTypeIq2S ? 8192 : type == kTypeIq3Xxs ? 1024 : 2048;
+}
+
+// Raw block fields of one lane's group for the 8 runs of a super-block, per
+// fragment: a = index bytes, b = sign / aux word, c = per-run-pair bytes
+// (qh, scales; at the pair's even run). The block's f16 d is kept apart.
+template <int NF>
+struct RawG {
+  uint32_t a[NF][8], b[NF][8], c[NF][8];
+};
+
+template <int TYPE, int NF>
+__device__ inline void load_d_g(uint32_t (&d)[NF], const uint8_t* const (&blk0)[NF], uint64_t b) {
+#pragma unroll
+  for (int f = 0; f < NF; ++f) d[f] = ld_u16(blk0[f] + b * block_bytes_of(TYPE));
+}
+
+// Runs 2C and 2C + 1 of super-block b (K-step C of the block).
+template <int TYPE, int NF, int C>
+__device__ inline void load_raw_g(RawG<NF>& r, const uint8_t* const (&blk0)[NF], uint64_t b, int l) {
+  constexpr int BB = block_bytes_of(TYPE);
+#pragma unroll
+  for (int f = 0; f < NF; ++f) {
+    const uint8_t* p = blk0[f] + b * BB;
+#pragma unroll
+    for (int j = 2 * C; j < 2 * C + 2; ++j) {
+      if constexpr (TYPE == kTypeIq2Xxs) {
+        r.a[f][j] = ld_u16(p + 2 + 8 * j + 2 * (l >> 1));
+        r.b[f][j] = ld_u32_a2(p + 6 + 8 * j);
+      } else if constexpr (TYPE == kTypeIq2Xs) {
+        r.a[f][j] = ld_u16(p + 2 + 2 * (4 * j + l));
+        if ((j & 1) == 0) r.c[f][j] = ld_u16(p + 66 + j);
+      } else if constexpr (TYPE == kTypeIq2S) {
+        r.a[f][j] = ld_u16(p + 2 + 4 * j + 2 * (l >> 1));
+        r.b[f][j] = ld_u16(p + 34 + 4 * j + 2 * (l >> 1));
+        if ((j & 1) == 0) r.c[f][j] = ld_u16(p + 66 + j) | (ld_u16(p + 74 + j) << 16);
+      } else if constexpr (TYPE == kTypeIq3Xxs) {
+        r.a[f][j] = ld_u16(p + 2 + 8 * j + 2 * l);
+        r.b[f][j] = ld_u32_a2(p + 66 + 4 * j);
+      } else {
+        static_assert(TYPE == kTypeIq3S, "grid format");
+        r.a[f][j] = ld_u16(p + 2 + 8 * j + 2 * l);
+        r.b[f][j] = ld_u16(p + 74 + 4 * j + 2 * (l >> 1));
+        if ((j & 1) == 0) r.c[f][j] = ld_u16(p + 66 + j) | (ld_u16(p + 106 + 2 * (j >> 2)) << 16);
+      }
+    }
+  }
+}
+
+// Run j, group l of every fragment as an f16 B operand (the same fields
+// and scale arithmetic as grid_run).
+template <int TYPE, int NF>
+__device__ inline void dequant_g(const RawG<NF>& r, const uint32_t (&dbits)[NF], int j, int l, const uint8_t* glds,
+                                 const uint4* smask, half8 (&bop)[NF]) {
+  const uint2* g64 = reinterpret_cast<const uint2*>(glds);
+  const uint32_t* g32 = reinterpret_cast<const uint32_t*>(glds);
+#pragma unroll
+  for (int f = 0; f < NF; ++f) {
+    const float d = half_bits(dbits[f]);
+    uint32_t m0, m1, sg;
+    float s;
+    if constexpr (TYPE == kTypeIq2Xxs) {
+      const uint32_t aux = r.b[f][j];
+      const uint2 e = g64[(r.a[f][j] >> (8 * (l & 1))) & 0xFFu];
+      m0 = e.x;
+      m1 = e.y;
+      sg = iq_sign_byte(aux >> (7 * l));
+      s = d * (0.5f + static_cast<float>(aux >> 28)) * 0.25f;
+    } else if constexpr (TYPE == kTypeIq2Xs) {
+      const uint32_t code = r.a[f][j];
+      const uint2 e = g64[code & 511u];
+      m0 = e.x;
+      m1 = e.y;
+      sg = iq_sign_byte(code >> 9);
+      const uint32_t sc = (r.c[f][j & ~1] >> (8 * (j & 1))) & 0xFFu;
+      s = d * (0.5f + static_cast<float>((sc >> (4 * (l >> 1))) & 0xFu)) * 0.25f;
+    } else if constexpr (TYPE == kTypeIq2S) {
+      const uint32_t cc = r.c[f][j & ~1];
+      const uint32_t qh = (cc >> (8 * (j & 1))) & 0xFFu;
+      const uint2 e = g64[((r.a[f][j] >> (8 * (l & 1))) & 0xFFu) | (((qh >> (2 * l)) & 3u) << 8)];
+      m0 = e.x;
+      m1 = e.y;
+      sg = (r.b[f][j] >> (8 * (l & 1))) & 0xFFu;
+      const uint32_t sc = (cc >> (16 + 8 * (j & 1))) & 0xFFu;
+      s = d * (0.5f + static_cast<float>((sc >> (4 * (l >> 1))) & 0xFu)) * 0.25f;
+    } else if constexpr (TYPE == kTypeIq3Xxs) {
+      const uint32_t a = r.a[f][j], aux = r.b[f][j];
+      m0 = g32[a & 0xFFu];
+      m1 = g32[(a >> 8) & 0xFFu];
+      sg = iq_sign_byte(aux >> (7 * l));
+      s = d * (0.5f + static_cast<float>(aux >> 28)) * 0.5f;
+    } else {
+      const uint32_t a = r.a[f][j], cc = r.c[f][j & ~1];
+      const uint32_t qh = (cc >> (8 * (j & 1))) & 0xFFu;
+      m0 = g32[(a & 0xFFu) | (((qh >> (2 * l)) & 1u) << 8)];
+      m1 = g32[((a >> 8) & 0xFFu) | (((qh >> (2 * l + 1)) & 1u) << 8)];
+      sg = (r.b[f][j] >> (8 * (l & 1))) & 0xFFu;
+      const uint32_t sc = (cc >> (16 + 8 * ((j >> 1) & 1) + 4 * (j & 1))) & 0xFu;
+      s = d * static_cast<float>(1 + 2 * sc);
+    }
+    const float c = -1024.0f * s;
+    const uint4 sm = smask[sg];
+    uint32_t p[4];
+    p[0] = fma_mix_pair(s, __builtin_amdgcn_perm(0x64646464u, m0, 0x04010400u), c) ^ sm.x;
+    p[1] = fma_mix_pair(s, __builtin_amdgcn_perm(0x64646464u, m0, 0x04030402u), c) ^ sm.y;
+    p[2] = fma_mix_pair(s, __builtin_amdgcn_perm(0x64646464u, m1, 0x04010400u), c) ^ sm.z;
+    p[3] = fma_mix_pair(s, __builtin_amdgcn_perm(0x64646464u, m1, 0x04030402u), c) ^ sm.w;
+    bop[f] = *reinterpret_cast<half8*>(p);
+  }
+}
+
+template <int TYPE, int MF, int NF>
+__global__ __launch_bounds__(256) void gemm_grid_kernel(const uint8_t* __restrict__ w, int nb, uint64_t rows,
+                                                        const uint16_t* __restrict__ a16, uint64_t m_rows,
+                                                        float* __restrict__ y, const float* __restrict__ addend,
+                                                        uint64_t addend_stride) {
+  constexpr int BM = MF * 16;
+  constexpr int LDK = kBK + 8;                  // halves per LDS row (16-byte pad)
+  constexpr int A_CHUNKS = BM * kBK / 8 / 256;  // 16-byte chunks per thread per K-step
+  constexpr int GBYTES = grid_table_size(TYPE);
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM][LDK];
+  __shared__ __attribute__((aligned(16))) uint8_t glds[GBYTES];
+  __shared__ uint4 smask[256];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int li = lane & 15, kq = lane >> 4;
+  const uint64_t m0 = static_cast<uint64_t>(blockIdx.y) * BM;
+  const uint64_t n0 = static_cast<uint64_t>(blockIdx.x) * (4 * NF * 16) + static_cast<uint64_t>(wave) * NF * 16;
+  const uint64_t K = static_cast<uint64_t>(nb) * 256;
+  const int ksteps = nb * 4;
+
+  floatx4 acc[MF][NF];
+#pragma unroll
+  for (int i = 0; i < MF; ++i)
+#pragma unroll
+    for (int f = 0; f < NF; ++f) acc[i][f] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  // this lane's stored row per fragment (columns past the last row read the
+  // last row; their outputs are not stored)
+  const uint8_t* blk0[NF];
+#pragma unroll
+  for (int f = 0; f < NF; ++f) {
+    const uint64_t n = n0 + 16 * f + li;
+    blk0[f] = w + (n < rows ? n : rows - 1) * static_cast<uint64_t>(nb) * block_bytes_of(TYPE);
+  }
+
+  // the format's grid table, and per sign byte the xor masks of its four
+  // f16 pairs (bit 2p -> bit 15 of word p, bit 2p + 1 -> bit 31)
+  for (int i = tid; i < GBYTES / 16; i += 256)
+    reinterpret_cast<uint4*>(glds)[i] = reinterpret_cast<const uint4*>(g_iq_grids + grid_table_offset(TYPE))[i];
+  {
+    uint32_t v[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) v[p] = (((tid >> (2 * p)) & 1u) << 15) | (((tid >> (2 * p + 1)) & 1u) << 31);
+    smask[tid] = make_uint4(v[0], v[1], v[2], v[3]);
+  }
+
+  auto load_a = [&](int kb, uint4 (&regs)[A_CHUNKS]) {
+#pragma unroll
+    for (int i = 0; i < A_CHUNKS; ++i) {
+      const int idx = tid + 256 * i, row = idx >> 3, ch = idx & 7;
+      regs[i] = make_uint4(0, 0, 0, 0);
+      if (m0 + row < m_rows)
+        regs[i] = *reinterpret_cast<const uint4*>(a16 + (m0 + row) * K + static_cast<uint64_t>(kb) * kBK + ch * 8);
+    }
+  };
+  auto store_a = [&](int buf, const uint4 (&regs)[A_CHUNKS]) {
+#pragma unroll
+    for (int i = 0; i < A_CHUNKS; ++i) {
+      const int idx = tid + 256 * i, row = idx >> 3, ch = idx & 7;
+      *reinterpret_cast<uint4*>(&As[buf][row][ch * 8]) = regs[i];
+    }
+  };
+
+  // raw fields: K-step slot C of the block in use is refilled with the next
+  // block's as soon as it is decoded (a super-block ahead, one copy)
+  RawG<NF> raw;
+  uint32_t dcur[NF], dnxt[NF];
+  load_d_g<TYPE, NF>(dcur, blk0, 0);
+  load_raw_g<TYPE, NF, 0>(raw, blk0, 0, kq);
+  load_raw_g<TYPE, NF, 1>(raw, blk0, 0, kq);
+  load_raw_g<TYPE, NF, 2>(raw, blk0, 0, kq);
+  load_raw_g<TYPE, NF, 3>(raw, blk0, 0, kq);
+  uint4 areg[A_CHUNKS];
+  load_a(0, areg);
+  store_a(0, areg);
+  __syncthreads();
+
+  auto kstep = [&](int kb, const half8 (&bop)[2][NF]) {
+    const int buf = kb & 1;
+    const bool more = kb + 1 < ksteps;
+    if (more) load_a(kb + 1, areg);
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+#pragma unroll
+      for (int i = 0; i < MF; ++i) {
+        const half8 af = *reinterpret_cast<const half8*>(&As[buf][16 * i + li][32 * r + 8 * kq]);
+#pragma unroll
+        for (int f = 0; f < NF; ++f)
+          acc[i][f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bop[r][f], acc[i][f], 0, 0, 0);
+      }
+    }
+    if (more) store_a(buf ^ 1, areg);
+    __syncthreads();
+  };
+
+  auto step = [&](int b, auto cc) {
+    constexpr int C = decltype(cc)::value;
+    half8 bop[2][NF];
+    dequant_g<TYPE, NF>(raw, dcur, 2 * C, kq, glds, smask, bop[0]);
+    dequant_g<TYPE, NF>(raw, dcur, 2 * C + 1, kq, glds, smask, bop[1]);
+    if (b + 1 < nb) load_raw_g<TYPE, NF, C>(raw, blk0, static_cast<uint64_t>(b + 1), kq);
+    kstep(4 * b + C, bop);
+  };
+  for (int b = 0; b < nb; ++b) {
+    const bool more = b + 1 < nb;
+    if (more) load_d_g<TYPE, NF>(dnxt, blk0, static_cast<uint64_t>(b + 1));
+    step(b, std::integral_constant<int, 0>{});
+    step(b, std::integral_constant<int, 1>{});
+    step(b, std::integral_constant<int, 2>{});
+    step(b, std::integral_constant<int, 3>{});
+    if (more) {
+#pragma unroll
+      for (int f = 0; f < NF; ++f) dcur[f] = dnxt[f];
+    }
+  }
+
+#pragma unroll
+  for (int i = 0; i < MF; ++i) {
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+      const uint64_t col = n0 + 16 * f + li;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint64_t row = m0 + 16 * i + 4 * kq + e;
+        if (row < m_rows && col < rows) {
+          float v = acc[i][f][e];
+          if (addend) v = v + addend[row * addend_stride + col];
+          y[row * rows + col] = v;
+        }
+      }
+    }
+  }
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -4057,6 +4332,24 @@ void launch_gemm_rb(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, 
   }
 }
 
+template <int MF, int NF>
+void launch_gemm_grid(int type, const uint8_t* w, uint64_t rows, uint64_t nb, const uint16_t* a16, uint64_t m,
+                      float* y, const float* addend, uint64_t addend_stride, hipStream_t stream) {
+  const uint64_t bn = 4 * NF * 16, bm = MF * 16;
+  dim3 grid(static_cast<unsigned>((rows + bn - 1) / bn), static_cast<unsigned>((m + bm - 1) / bm));
+  switch (type) {
+#define X(T)                                                                                                    \
+  case T:                                                                                                       \
+    hipLaunchKernelGGL((gemm_grid_kernel<T, MF, NF>), grid, dim3(256), 0, stream, w, static_cast<int>(nb), rows, \
+                       a16, m, y, addend, addend_stride);                                                      \
+    break;
+    MQ_GRID_TYPES(X)
+#undef X
+    default:
+      break;
+  }
+}
+
 uint64_t tiles(uint64_t rows, uint64_t m, uint64_t bn, uint64_t bm) {
   return ((rows + bn - 1) / bn) * ((m + bm - 1) / bm);
 }
@@ -4078,6 +4371,15 @@ void launch_gemm(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, uin
                  hipStream_t stream) {
   const uint64_t rows_padded = (rows + 7) / 8 * 8;
   dim3 grid(static_cast<unsigned>((rows + kBN - 1) / kBN), static_cast<unsigned>((m + kBM - 1) / kBM));
+  if (is_grid_format(type)) {
+    // grid formats: raw blocks, whole super-blocks (k % 256 == 0)
+    if (variant == 0) variant = tiles(rows, m, 256, 128) >= 1024 ? 2 : 3;
+    if (variant == 2)
+      launch_gemm_grid<8, 4>(type, tiled, rows, nb, a16, m, y, addend, addend_stride, stream);
+    else
+      launch_gemm_grid<8, 2>(type, tiled, rows, nb, a16, m, y, addend, addend_stride, stream);
+    return;
+  }
   // plane formats whose rows end inside a group take the LDS-B form
   if (is_plane_format(type) && k % 256 != 0) variant = 1;
   if (variant == 1 && is_plane_format(type)) {

@@ -92,7 +92,9 @@ void launch_gemv_f32(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb,
 // registers with 128 x 256, 128 x 128 and 64 x 256 tiles; 5 (Q4_K): the
 // K-split form, 128 x 256 tiles of 8 waves; 0: choose.
 // k = the logical row length; plane formats whose rows end inside a group
-// take variant 1.
+// take variant 1. The IQ2 / IQ3 grid formats (raw blocks, the grid tables
+// in the device copy) take the register-B form: 128 x 256 tiles for
+// variant 2, else 128 x 128.
 void launch_gemm(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, uint64_t k,
                  const uint16_t* a16, uint64_t m, float* y, const float* addend, uint64_t addend_stride,
                  int variant, hipStream_t stream);

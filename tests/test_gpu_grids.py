@@ -75,9 +75,9 @@ def test_gemv_every_m(gctx, fmt, int8):
         h.release()
 
 
-@pytest.mark.parametrize("fmt", [IQ2_XXS, IQ3_S])
+@pytest.mark.parametrize("fmt", GRID_FORMATS)
 def test_prefill_rows_and_residual(gctx, fmt):
-    """M = 40 (the grid formats' prefill is 8-row GEMVs) and the residual
+    """M = 40 (past 16 rows: the MFMA prefill GEMM) and the residual
     epilogue with one broadcast row and with M rows."""
     m, n, k = 40, 136, 768
     w = packed(fmt, n, k, 51)
@@ -156,14 +156,83 @@ def test_full_size_gemv_sampled_columns(gctx):
     assert np.isfinite(got).all()
 
 
+def _context_with(env):
+    """A Context whose launch choices are forced through the environment
+    (read once, at creation)."""
+    import os
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update({k: str(v) for k, v in env.items()})
+    try:
+        return mg.Context(0)
+    finally:
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+
+
+@pytest.mark.parametrize("fmt", GRID_FORMATS)
+@pytest.mark.parametrize("variant", [0, 2, 3])
+def test_prefill_gemm_tiles_and_ragged_edges(gctx, fmt, variant):
+    """The MFMA prefill (register-B form decoding the raw blocks per lane)
+    with 128 x 128 (variant 3) and 128 x 256 (variant 2) tiles: M and N
+    ragged against both tile sizes, both activation modes, and the f16
+    operand entry point against the same dense product."""
+    c = _context_with({"MQ_GEMM_VARIANT": variant})
+    try:
+        for m, n, k in ((130, 300, 1024), (17, 257, 512), (64, 40, 2304)):
+            w = packed(fmt, n, k, 61 + n)
+            x = activations(m, k, 62 + m)
+            h = c.upload(fmt, n, k, w)
+            try:
+                for int8 in (True, False):
+                    assert_row_tolerance(c.matmul(h, x, int8=int8), dense(fmt, w, n, k, x, int8),
+                                         f"m {m} n {n} k {k} int8 {int8}")
+                a16 = dev(x.astype(np.float16))
+                y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+                c.matmul_f16_dev(h, a16.data_ptr(), m, k, y.data_ptr())
+                torch.cuda.synchronize()
+                exp = dense(fmt, w, n, k, x.astype(np.float16).astype(np.float32), False)
+                assert_row_tolerance(y.cpu().numpy(), exp, f"f16 entry m {m} n {n} k {k}")
+            finally:
+                h.release()
+    finally:
+        c.close()
+
+
+def test_prefill_falls_back_for_wide_grid_bytes(gctx):
+    """Grid tables holding a magnitude byte of 128 or more: the MFMA
+    prefill (unsigned magnitudes) is not used; the prefill runs as 8-row
+    GEMVs (i8 magnitudes, as the reference) and the f16 entry point
+    declines. The stand-in tables are restored afterwards."""
+    wide = [t.copy() for t in GRIDS]
+    wide[0][5] |= np.uint64(0x90)  # one IQ2_XXS entry's byte 0 -> 0x90 | b
+    gctx.set_iq_grids(tuple(wide))
+    oracle.set_iq_grids(tuple(wide))
+    try:
+        m, n, k = 40, 72, 512
+        w = packed(IQ2_XXS, n, k, 71)
+        x = activations(m, k, 72)
+        h = gctx.upload(IQ2_XXS, n, k, w)
+        try:
+            assert_row_tolerance(gctx.matmul(h, x), dense(IQ2_XXS, w, n, k, x, True), "prefill, wide bytes")
+            a16 = torch.zeros((m, k), dtype=torch.float16, device="cuda")
+            y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+            with pytest.raises(mg.Declined):
+                gctx.matmul_f16_dev(h, a16.data_ptr(), m, k, y.data_ptr())
+        finally:
+            h.release()
+    finally:
+        gctx.set_iq_grids(GRIDS)
+        oracle.set_iq_grids(GRIDS)
+
+
 def test_declines(gctx):
     w = packed(IQ2_XXS, 8, 256, 91)
     h = gctx.upload(IQ2_XXS, 8, 256, w)
     try:
-        a16 = torch.zeros((4, 256), dtype=torch.float16, device="cuda")
         y = torch.empty((4, 8), dtype=torch.float32, device="cuda")
-        with pytest.raises(mg.Declined):
-            gctx.matmul_f16_dev(h, a16.data_ptr(), 4, 256, y.data_ptr())
         x = torch.zeros((1, 256), dtype=torch.float32, device="cuda")
         with pytest.raises(mg.Declined):
             gctx.decode_matmul_dev(h, x.data_ptr(), 256, y.data_ptr())
