@@ -2126,6 +2126,19 @@ __global__ __launch_bounds__(512) void gemv_planes_f32_kernel(const uint8_t* __r
 
 __device__ __attribute__((aligned(16))) uint8_t g_iq_grids[kGridTableBytes];
 
+// The format's table within the device copy: byte offset and size.
+__host__ __device__ constexpr int grid_table_offset(int type) {
+  return type == kTypeIq2Xxs ? kGridIq2Xxs
+         : type == kTypeIq2Xs ? kGridIq2Xs
+         : type == kTypeIq2S  ? kGridIq2S
+         : type == kTypeIq3Xxs ? kGridIq3Xxs
+                               : kGridIq3S;
+}
+__host__ __device__ constexpr int grid_table_size(int type) {
+  return type == kTypeIq2Xxs ? 2048 : type == kTypeIq2Xs ? 4096 : type == kTypeIq2S ? 8192 : type == kTypeIq3Xxs ? 1024 : 2048;
+}
+
+
 __device__ inline uint32_t ld_u16(const uint8_t* p) { return *reinterpret_cast<const uint16_t*>(p); }
 __device__ inline uint32_t ld_u32_a2(const uint8_t* p) { return ld_u16(p) | (ld_u16(p + 2) << 16); }
 
@@ -2145,68 +2158,106 @@ struct GridRun {
   float scale[2];
 };
 
+// A run's raw block fields, loaded apart from the decode so that several
+// runs' loads can be in flight before any of them is decoded: w = the
+// format's words (below), d = the block's f16 d.
+struct GridRaw {
+  uint32_t w[4];
+  uint32_t d;
+};
+
 template <int TYPE>
-__device__ inline void grid_run(const uint8_t* __restrict__ blk, int run, GridRun& g) {
-  const float d = half_bits(ld_u16(blk));
-  const uint8_t* grids = g_iq_grids;
+__device__ inline void grid_raw(const uint8_t* __restrict__ blk, int run, GridRaw& r) {
+  r.d = ld_u16(blk);
+  if constexpr (TYPE == kTypeIq2Xxs) {
+    r.w[0] = ld_u32_a2(blk + 2 + 8 * run);  // 4 grid indices
+    r.w[1] = ld_u32_a2(blk + 6 + 8 * run);  // 4 x 7 sign bits, 4-bit scale
+  } else if constexpr (TYPE == kTypeIq2Xs) {
+    r.w[0] = ld_u32_a2(blk + 2 + 8 * run);  // codes 0, 1 (9-bit index, 7 sign bits)
+    r.w[1] = ld_u32_a2(blk + 6 + 8 * run);  // codes 2, 3
+    r.w[2] = ld_u16(blk + 66 + (run & ~1));  // scale bytes of runs (run & ~1), (run | 1)
+  } else if constexpr (TYPE == kTypeIq2S) {
+    r.w[0] = ld_u32_a2(blk + 2 + 4 * run);   // 4 low index bytes
+    r.w[1] = ld_u32_a2(blk + 34 + 4 * run);  // 4 sign bytes
+    r.w[2] = ld_u16(blk + 66 + (run & ~1)) | (ld_u16(blk + 74 + (run & ~1)) << 16);  // qh, scale bytes
+  } else if constexpr (TYPE == kTypeIq3Xxs) {
+    r.w[0] = ld_u32_a2(blk + 2 + 8 * run);  // grid indices 0..3
+    r.w[1] = ld_u32_a2(blk + 6 + 8 * run);  // grid indices 4..7
+    r.w[2] = ld_u32_a2(blk + 66 + 4 * run);  // 4 x 7 sign bits, 4-bit scale
+  } else {
+    static_assert(TYPE == kTypeIq3S, "grid format");
+    r.w[0] = ld_u32_a2(blk + 2 + 8 * run);
+    r.w[1] = ld_u32_a2(blk + 6 + 8 * run);
+    r.w[2] = ld_u32_a2(blk + 74 + 4 * run);  // 4 sign bytes
+    r.w[3] = ld_u16(blk + 66 + (run & ~1)) | (ld_u16(blk + 106 + 2 * (run >> 2)) << 16);  // qh, scale nibbles
+  }
+}
+
+// `table` = the format's grid table (the device copy, or an LDS copy).
+template <int TYPE>
+__device__ inline void grid_decode(const GridRaw& r, int run, const uint8_t* table, GridRun& g) {
+  const float d = half_bits(r.d);
   g.signs = 0;
   if constexpr (TYPE == kTypeIq2Xxs) {
-    const uint32_t idx = ld_u32_a2(blk + 2 + 8 * run), aux = ld_u32_a2(blk + 6 + 8 * run);
 #pragma unroll
     for (int l = 0; l < 4; ++l) {
-      const uint2 e = *reinterpret_cast<const uint2*>(grids + kGridIq2Xxs + 8 * ((idx >> (8 * l)) & 0xFFu));
+      const uint2 e = *reinterpret_cast<const uint2*>(table + 8 * ((r.w[0] >> (8 * l)) & 0xFFu));
       g.mag[2 * l] = e.x;
       g.mag[2 * l + 1] = e.y;
-      g.signs |= iq_sign_byte(aux >> (7 * l)) << (8 * l);
+      g.signs |= iq_sign_byte(r.w[1] >> (7 * l)) << (8 * l);
     }
-    g.scale[0] = g.scale[1] = d * (0.5f + static_cast<float>(aux >> 28)) * 0.25f;
+    g.scale[0] = g.scale[1] = d * (0.5f + static_cast<float>(r.w[1] >> 28)) * 0.25f;
   } else if constexpr (TYPE == kTypeIq2Xs) {
 #pragma unroll
     for (int l = 0; l < 4; ++l) {
-      const uint32_t code = ld_u16(blk + 2 + 2 * (4 * run + l));
-      const uint2 e = *reinterpret_cast<const uint2*>(grids + kGridIq2Xs + 8 * (code & 511u));
+      const uint32_t code = (r.w[l >> 1] >> (16 * (l & 1))) & 0xFFFFu;
+      const uint2 e = *reinterpret_cast<const uint2*>(table + 8 * (code & 511u));
       g.mag[2 * l] = e.x;
       g.mag[2 * l + 1] = e.y;
       g.signs |= iq_sign_byte(code >> 9) << (8 * l);
     }
-    const uint32_t sc = blk[66 + run];
+    const uint32_t sc = (r.w[2] >> (8 * (run & 1))) & 0xFFu;
     g.scale[0] = d * (0.5f + static_cast<float>(sc & 0xFu)) * 0.25f;
     g.scale[1] = d * (0.5f + static_cast<float>(sc >> 4)) * 0.25f;
   } else if constexpr (TYPE == kTypeIq2S) {
-    const uint32_t qh = blk[66 + run];
+    const uint32_t qh = (r.w[2] >> (8 * (run & 1))) & 0xFFu;
 #pragma unroll
     for (int l = 0; l < 4; ++l) {
-      const uint32_t index = blk[2 + 4 * run + l] | (((qh >> (2 * l)) & 3u) << 8);
-      const uint2 e = *reinterpret_cast<const uint2*>(grids + kGridIq2S + 8 * index);
+      const uint32_t index = ((r.w[0] >> (8 * l)) & 0xFFu) | (((qh >> (2 * l)) & 3u) << 8);
+      const uint2 e = *reinterpret_cast<const uint2*>(table + 8 * index);
       g.mag[2 * l] = e.x;
       g.mag[2 * l + 1] = e.y;
-      g.signs |= static_cast<uint32_t>(blk[34 + 4 * run + l]) << (8 * l);
     }
-    const uint32_t sc = blk[74 + run];
+    g.signs = r.w[1];
+    const uint32_t sc = (r.w[2] >> (16 + 8 * (run & 1))) & 0xFFu;
     g.scale[0] = d * (0.5f + static_cast<float>(sc & 0xFu)) * 0.25f;
     g.scale[1] = d * (0.5f + static_cast<float>(sc >> 4)) * 0.25f;
   } else if constexpr (TYPE == kTypeIq3Xxs) {
-    const uint32_t aux = ld_u32_a2(blk + 66 + 4 * run);
 #pragma unroll
-    for (int l = 0; l < 4; ++l) {
-      g.mag[2 * l] = *reinterpret_cast<const uint32_t*>(grids + kGridIq3Xxs + 4 * blk[2 + 8 * run + 2 * l]);
-      g.mag[2 * l + 1] = *reinterpret_cast<const uint32_t*>(grids + kGridIq3Xxs + 4 * blk[3 + 8 * run + 2 * l]);
-      g.signs |= iq_sign_byte(aux >> (7 * l)) << (8 * l);
-    }
-    g.scale[0] = g.scale[1] = d * (0.5f + static_cast<float>(aux >> 28)) * 0.5f;
+    for (int i = 0; i < 8; ++i)
+      g.mag[i] = *reinterpret_cast<const uint32_t*>(table + 4 * ((r.w[i >> 2] >> (8 * (i & 3))) & 0xFFu));
+#pragma unroll
+    for (int l = 0; l < 4; ++l) g.signs |= iq_sign_byte(r.w[2] >> (7 * l)) << (8 * l);
+    g.scale[0] = g.scale[1] = d * (0.5f + static_cast<float>(r.w[2] >> 28)) * 0.5f;
   } else {
-    static_assert(TYPE == kTypeIq3S, "grid format");
-    const uint32_t qh = blk[66 + run];
+    const uint32_t qh = (r.w[3] >> (8 * (run & 1))) & 0xFFu;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const uint32_t index = blk[2 + 8 * run + i] | (((qh >> i) & 1u) << 8);
-      g.mag[i] = *reinterpret_cast<const uint32_t*>(grids + kGridIq3S + 4 * index);
+      const uint32_t index = ((r.w[i >> 2] >> (8 * (i & 3))) & 0xFFu) | (((qh >> i) & 1u) << 8);
+      g.mag[i] = *reinterpret_cast<const uint32_t*>(table + 4 * index);
     }
-#pragma unroll
-    for (int l = 0; l < 4; ++l) g.signs |= static_cast<uint32_t>(blk[74 + 4 * run + l]) << (8 * l);
-    const uint32_t sc = (blk[106 + run / 2] >> (4 * (run % 2))) & 0xFu;
+    g.signs = r.w[2];
+    const uint32_t sc = (r.w[3] >> (16 + 8 * ((run >> 1) & 1) + 4 * (run & 1))) & 0xFu;
     g.scale[0] = g.scale[1] = d * static_cast<float>(1 + 2 * sc);
   }
+}
+
+// One run of a grid format as `decode` produces it (src/native/quant.rs:207-277).
+template <int TYPE>
+__device__ inline void grid_run(const uint8_t* __restrict__ blk, int run, GridRun& g) {
+  GridRaw r;
+  grid_raw<TYPE>(blk, run, r);
+  grid_decode<TYPE>(r, run, g_iq_grids + grid_table_offset(TYPE), g);
 }
 
 // Value i of a decoded run: the magnitude as i8, negated (as i8) where its
@@ -2257,49 +2308,90 @@ __global__ void dequantize_grid_kernel(const uint8_t* __restrict__ w, uint64_t r
   }
 }
 
-// Decode GEMV of a grid format (m <= 8): one wave per stored row, lanes
-// over its runs, a fixed-order shuffle reduction. INT8: the reference's
-// int8 path (per half: scale * integer dot, times d_act per run); else its
-// f32 column loop (w = scale * q, acc += w * x per value).
+// Decode GEMV of a grid format (m <= 8): one wave per stored row at a time
+// (8 waves per work-group, rows strided over the grid), lanes over the
+// row's runs, a fixed-order shuffle reduction. The format's grid table is
+// copied to LDS once per work-group, so the four gathers per run leave the
+// vector-memory path to the activation and block loads. INT8: the
+// reference's int8 path (per half: scale * integer dot, times d_act per
+// run); else its f32 column loop (w = scale * q, acc += w * x per value).
+constexpr int kGridGemvWaves = 8;
 template <int TYPE, int M, bool INT8>
-__global__ __launch_bounds__(256) void gemv_grid_kernel(const uint8_t* __restrict__ w, uint64_t nb, uint64_t rows,
-                                                        const int8_t* __restrict__ xv, const float* __restrict__ xs,
-                                                        const float* __restrict__ xf, float* __restrict__ y,
-                                                        const float* __restrict__ addend, uint64_t addend_stride) {
+__global__ __launch_bounds__(64 * kGridGemvWaves) void gemv_grid_kernel(
+    const uint8_t* __restrict__ w, uint64_t nb, uint64_t rows, const int8_t* __restrict__ xv,
+    const float* __restrict__ xs, const float* __restrict__ xf, float* __restrict__ y,
+    const float* __restrict__ addend, uint64_t addend_stride) {
   constexpr int BB = block_bytes_of(TYPE);
+  constexpr int GBYTES = grid_table_size(TYPE);
+  __shared__ __attribute__((aligned(16))) uint8_t glds[GBYTES];
+  for (int i = threadIdx.x; i < GBYTES / 16; i += 64 * kGridGemvWaves)
+    reinterpret_cast<uint4*>(glds)[i] = reinterpret_cast<const uint4*>(g_iq_grids + grid_table_offset(TYPE))[i];
+  __syncthreads();
   const int lane = threadIdx.x & 63;
-  const uint64_t row = static_cast<uint64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;  // the whole wave
   const uint64_t runs = nb * 8, K = nb * 256;
+  for (uint64_t row = static_cast<uint64_t>(blockIdx.x) * kGridGemvWaves + (threadIdx.x >> 6); row < rows;
+       row += static_cast<uint64_t>(gridDim.x) * kGridGemvWaves) {
   const uint8_t* base = w + row * nb * BB;
   float acc[M];
 #pragma unroll
   for (int m = 0; m < M; ++m) acc[m] = 0.0f;
-  for (uint64_t u = lane; u < runs; u += 64) {
-    GridRun g;
-    grid_run<TYPE>(base + (u >> 3) * BB, static_cast<int>(u & 7), g);
+  // Two runs per lane per pass (u0 and u0 + 64, the order of the one-run
+  // loop): both runs' block fields and int8 activations are requested
+  // before either is decoded. A second run past the row's end re-reads the
+  // first and adds nothing.
+  for (uint64_t u0 = lane; u0 < runs; u0 += 128) {
+    const bool two = u0 + 64 < runs;
+    const uint64_t us[2] = {u0, two ? u0 + 64 : u0};
+    GridRaw raw[2];
 #pragma unroll
-    for (int m = 0; m < M; ++m) {
-      if constexpr (INT8) {
-        const uint4* ap = reinterpret_cast<const uint4*>(xv + m * K + 32 * u);
-        const uint4 a0 = ap[0], a1 = ap[1];
-        const uint32_t a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-        int dot[2];
-        grid_dots(g, a, dot);
-        float t = g.scale[0] * static_cast<float>(dot[0]);
-        t = t + g.scale[1] * static_cast<float>(dot[1]);
-        acc[m] += xs[m * runs + u] * t;
-      } else {
-        const float4* xp = reinterpret_cast<const float4*>(xf + m * K + 32 * u);
+    for (int q = 0; q < 2; ++q) grid_raw<TYPE>(base + (us[q] >> 3) * BB, static_cast<int>(us[q] & 7), raw[q]);
+    if constexpr (INT8) {
+      uint4 av[2][M][2];
+      float as[2][M];
 #pragma unroll
-        for (int q4 = 0; q4 < 8; ++q4) {
-          const float4 xq = xp[q4];
-          const float xv4[4] = {xq.x, xq.y, xq.z, xq.w};
+      for (int q = 0; q < 2; ++q)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int i = 4 * q4 + e;
-            const float wv = g.scale[i >> 4] * static_cast<float>(grid_value(g, i));
-            acc[m] += wv * xv4[e];
+        for (int m = 0; m < M; ++m) {
+          const uint4* ap = reinterpret_cast<const uint4*>(xv + m * K + 32 * us[q]);
+          av[q][m][0] = ap[0];
+          av[q][m][1] = ap[1];
+          as[q][m] = xs[m * runs + us[q]];
+        }
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        GridRun g;
+        grid_decode<TYPE>(raw[q], static_cast<int>(us[q] & 7), glds, g);
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+          const uint32_t a[8] = {av[q][m][0].x, av[q][m][0].y, av[q][m][0].z, av[q][m][0].w,
+                                 av[q][m][1].x, av[q][m][1].y, av[q][m][1].z, av[q][m][1].w};
+          int dot[2];
+          grid_dots(g, a, dot);
+          float t = g.scale[0] * static_cast<float>(dot[0]);
+          t = t + g.scale[1] * static_cast<float>(dot[1]);
+          if (q == 0 || two) acc[m] += as[q][m] * t;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        if (q == 1 && !two) break;
+        const uint64_t u = us[q];
+        GridRun g;
+        grid_decode<TYPE>(raw[q], static_cast<int>(u & 7), glds, g);
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+          const float4* xp = reinterpret_cast<const float4*>(xf + m * K + 32 * u);
+#pragma unroll
+          for (int q4 = 0; q4 < 8; ++q4) {
+            const float4 xq = xp[q4];
+            const float xv4[4] = {xq.x, xq.y, xq.z, xq.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int i = 4 * q4 + e;
+              const float wv = g.scale[i >> 4] * static_cast<float>(grid_value(g, i));
+              acc[m] += wv * xv4[e];
+            }
           }
         }
       }
@@ -2316,6 +2408,7 @@ __global__ __launch_bounds__(256) void gemv_grid_kernel(const uint8_t* __restric
       if (addend) v = v + addend[m * addend_stride + row];
       y[m * rows + row] = v;
     }
+  }
   }
 }
 
@@ -3475,24 +3568,20 @@ __global__ __launch_bounds__(kKsThreads) void gemm_ks_kernel(const uint8_t* __re
 // reading of `grid_value`.
 // ---------------------------------------------------------------------------
 
-__host__ __device__ constexpr int grid_table_offset(int type) {
-  return type == kTypeIq2Xxs ? kGridIq2Xxs
-         : type == kTypeIq2Xs ? kGridIq2Xs
-         : type == kTypeIq2S  ? kGridIq2S
-         : type == kTypeIq3Xxs ? kGridIq3Xxs
-                               : kGridIq3S;
-}
-__host__ __device__ constexpr int grid_table_size(int type) {
-  return type == kTypeIq2Xxs ? 2048 : type == kTypeIq2Xs ? 4096 : type == kTypeIq2S ? 8192 : type == kTypeIq3Xxs ? 1024 : 2048;
-}
-
-// Raw block fields of one lane's group for the 8 runs of a super-block, per
-// fragment: a = index bytes, b = sign / aux word, c = per-run-pair bytes
-// (qh, scales; at the pair's even run). The block's f16 d is kept apart.
-template <int NF>
+// Raw block fields of one lane's group for DEPTH K-steps (2 DEPTH runs),
+// per fragment: a = index bytes, b = sign / aux word, c = per-run-pair
+// bytes (qh, scales; at the pair's even slot). K-step C of a super-block
+// sits in ring slot C % DEPTH. The block's f16 d is kept apart.
+template <int NF, int DEPTH>
 struct RawG {
-  uint32_t a[NF][8], b[NF][8], c[NF][8];
+  uint32_t a[NF][2 * DEPTH], b[NF][2 * DEPTH], c[NF][2 * DEPTH];
 };
+
+// Ring depth in K-steps: a whole super-block where the registers allow two
+// waves per SIMD, half of one for the formats with three fields per run.
+__host__ __device__ constexpr int grid_ring_depth(int type) {
+  return type == kTypeIq2S || type == kTypeIq3S ? 2 : 4;
+}
 
 template <int TYPE, int NF>
 __device__ inline void load_d_g(uint32_t (&d)[NF], const uint8_t* const (&blk0)[NF], uint64_t b) {
@@ -3500,33 +3589,35 @@ __device__ inline void load_d_g(uint32_t (&d)[NF], const uint8_t* const (&blk0)[
   for (int f = 0; f < NF; ++f) d[f] = ld_u16(blk0[f] + b * block_bytes_of(TYPE));
 }
 
-// Runs 2C and 2C + 1 of super-block b (K-step C of the block).
-template <int TYPE, int NF, int C>
-__device__ inline void load_raw_g(RawG<NF>& r, const uint8_t* const (&blk0)[NF], uint64_t b, int l) {
+// Runs 2C and 2C + 1 of super-block b (K-step C of the block), into ring
+// slot C % DEPTH.
+template <int TYPE, int NF, int DEPTH, int C>
+__device__ inline void load_raw_g(RawG<NF, DEPTH>& r, const uint8_t* const (&blk0)[NF], uint64_t b, int l) {
   constexpr int BB = block_bytes_of(TYPE);
 #pragma unroll
   for (int f = 0; f < NF; ++f) {
     const uint8_t* p = blk0[f] + b * BB;
 #pragma unroll
-    for (int j = 2 * C; j < 2 * C + 2; ++j) {
+    for (int h = 0; h < 2; ++h) {
+      const int j = 2 * C + h, q = 2 * (C % DEPTH) + h;
       if constexpr (TYPE == kTypeIq2Xxs) {
-        r.a[f][j] = ld_u16(p + 2 + 8 * j + 2 * (l >> 1));
-        r.b[f][j] = ld_u32_a2(p + 6 + 8 * j);
+        r.a[f][q] = ld_u16(p + 2 + 8 * j + 2 * (l >> 1));
+        r.b[f][q] = ld_u32_a2(p + 6 + 8 * j);
       } else if constexpr (TYPE == kTypeIq2Xs) {
-        r.a[f][j] = ld_u16(p + 2 + 2 * (4 * j + l));
-        if ((j & 1) == 0) r.c[f][j] = ld_u16(p + 66 + j);
+        r.a[f][q] = ld_u16(p + 2 + 2 * (4 * j + l));
+        if ((j & 1) == 0) r.c[f][q] = ld_u16(p + 66 + j);
       } else if constexpr (TYPE == kTypeIq2S) {
-        r.a[f][j] = ld_u16(p + 2 + 4 * j + 2 * (l >> 1));
-        r.b[f][j] = ld_u16(p + 34 + 4 * j + 2 * (l >> 1));
-        if ((j & 1) == 0) r.c[f][j] = ld_u16(p + 66 + j) | (ld_u16(p + 74 + j) << 16);
+        r.a[f][q] = ld_u16(p + 2 + 4 * j + 2 * (l >> 1));
+        r.b[f][q] = ld_u16(p + 34 + 4 * j + 2 * (l >> 1));
+        if ((j & 1) == 0) r.c[f][q] = ld_u16(p + 66 + j) | (ld_u16(p + 74 + j) << 16);
       } else if constexpr (TYPE == kTypeIq3Xxs) {
-        r.a[f][j] = ld_u16(p + 2 + 8 * j + 2 * l);
-        r.b[f][j] = ld_u32_a2(p + 66 + 4 * j);
+        r.a[f][q] = ld_u16(p + 2 + 8 * j + 2 * l);
+        r.b[f][q] = ld_u32_a2(p + 66 + 4 * j);
       } else {
         static_assert(TYPE == kTypeIq3S, "grid format");
-        r.a[f][j] = ld_u16(p + 2 + 8 * j + 2 * l);
-        r.b[f][j] = ld_u16(p + 74 + 4 * j + 2 * (l >> 1));
-        if ((j & 1) == 0) r.c[f][j] = ld_u16(p + 66 + j) | (ld_u16(p + 106 + 2 * (j >> 2)) << 16);
+        r.a[f][q] = ld_u16(p + 2 + 8 * j + 2 * l);
+        r.b[f][q] = ld_u16(p + 74 + 4 * j + 2 * (l >> 1));
+        if ((j & 1) == 0) r.c[f][q] = ld_u16(p + 66 + j) | (ld_u16(p + 106 + 2 * (j >> 2)) << 16);
       }
     }
   }
@@ -3534,9 +3625,9 @@ __device__ inline void load_raw_g(RawG<NF>& r, const uint8_t* const (&blk0)[NF],
 
 // Run j, group l of every fragment as an f16 B operand (the same fields
 // and scale arithmetic as grid_run).
-template <int TYPE, int NF>
-__device__ inline void dequant_g(const RawG<NF>& r, const uint32_t (&dbits)[NF], int j, int l, const uint8_t* glds,
-                                 const uint4* smask, half8 (&bop)[NF]) {
+template <int TYPE, int NF, int DEPTH>
+__device__ inline void dequant_g(const RawG<NF, DEPTH>& r, const uint32_t (&dbits)[NF], int j, int q, int l,
+                                 const uint8_t* glds, const uint4* smask, half8 (&bop)[NF]) {
   const uint2* g64 = reinterpret_cast<const uint2*>(glds);
   const uint32_t* g32 = reinterpret_cast<const uint32_t*>(glds);
 #pragma unroll
@@ -3545,41 +3636,41 @@ __device__ inline void dequant_g(const RawG<NF>& r, const uint32_t (&dbits)[NF],
     uint32_t m0, m1, sg;
     float s;
     if constexpr (TYPE == kTypeIq2Xxs) {
-      const uint32_t aux = r.b[f][j];
-      const uint2 e = g64[(r.a[f][j] >> (8 * (l & 1))) & 0xFFu];
+      const uint32_t aux = r.b[f][q];
+      const uint2 e = g64[(r.a[f][q] >> (8 * (l & 1))) & 0xFFu];
       m0 = e.x;
       m1 = e.y;
       sg = iq_sign_byte(aux >> (7 * l));
       s = d * (0.5f + static_cast<float>(aux >> 28)) * 0.25f;
     } else if constexpr (TYPE == kTypeIq2Xs) {
-      const uint32_t code = r.a[f][j];
+      const uint32_t code = r.a[f][q];
       const uint2 e = g64[code & 511u];
       m0 = e.x;
       m1 = e.y;
       sg = iq_sign_byte(code >> 9);
-      const uint32_t sc = (r.c[f][j & ~1] >> (8 * (j & 1))) & 0xFFu;
+      const uint32_t sc = (r.c[f][q & ~1] >> (8 * (j & 1))) & 0xFFu;
       s = d * (0.5f + static_cast<float>((sc >> (4 * (l >> 1))) & 0xFu)) * 0.25f;
     } else if constexpr (TYPE == kTypeIq2S) {
-      const uint32_t cc = r.c[f][j & ~1];
+      const uint32_t cc = r.c[f][q & ~1];
       const uint32_t qh = (cc >> (8 * (j & 1))) & 0xFFu;
-      const uint2 e = g64[((r.a[f][j] >> (8 * (l & 1))) & 0xFFu) | (((qh >> (2 * l)) & 3u) << 8)];
+      const uint2 e = g64[((r.a[f][q] >> (8 * (l & 1))) & 0xFFu) | (((qh >> (2 * l)) & 3u) << 8)];
       m0 = e.x;
       m1 = e.y;
-      sg = (r.b[f][j] >> (8 * (l & 1))) & 0xFFu;
+      sg = (r.b[f][q] >> (8 * (l & 1))) & 0xFFu;
       const uint32_t sc = (cc >> (16 + 8 * (j & 1))) & 0xFFu;
       s = d * (0.5f + static_cast<float>((sc >> (4 * (l >> 1))) & 0xFu)) * 0.25f;
     } else if constexpr (TYPE == kTypeIq3Xxs) {
-      const uint32_t a = r.a[f][j], aux = r.b[f][j];
+      const uint32_t a = r.a[f][q], aux = r.b[f][q];
       m0 = g32[a & 0xFFu];
       m1 = g32[(a >> 8) & 0xFFu];
       sg = iq_sign_byte(aux >> (7 * l));
       s = d * (0.5f + static_cast<float>(aux >> 28)) * 0.5f;
     } else {
-      const uint32_t a = r.a[f][j], cc = r.c[f][j & ~1];
+      const uint32_t a = r.a[f][q], cc = r.c[f][q & ~1];
       const uint32_t qh = (cc >> (8 * (j & 1))) & 0xFFu;
       m0 = g32[(a & 0xFFu) | (((qh >> (2 * l)) & 1u) << 8)];
       m1 = g32[((a >> 8) & 0xFFu) | (((qh >> (2 * l + 1)) & 1u) << 8)];
-      sg = (r.b[f][j] >> (8 * (l & 1))) & 0xFFu;
+      sg = (r.b[f][q] >> (8 * (l & 1))) & 0xFFu;
       const uint32_t sc = (cc >> (16 + 8 * ((j >> 1) & 1) + 4 * (j & 1))) & 0xFu;
       s = d * static_cast<float>(1 + 2 * sc);
     }
@@ -3594,8 +3685,10 @@ __device__ inline void dequant_g(const RawG<NF>& r, const uint32_t (&dbits)[NF],
   }
 }
 
+// (128 x 128 tiles: held to two waves per SIMD, so that one work-group's
+// decode overlaps the other's MFMAs)
 template <int TYPE, int MF, int NF>
-__global__ __launch_bounds__(256) void gemm_grid_kernel(const uint8_t* __restrict__ w, int nb, uint64_t rows,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NF == 2 ? 2 : 1))) void gemm_grid_kernel(const uint8_t* __restrict__ w, int nb, uint64_t rows,
                                                         const uint16_t* __restrict__ a16, uint64_t m_rows,
                                                         float* __restrict__ y, const float* __restrict__ addend,
                                                         uint64_t addend_stride) {
@@ -3658,13 +3751,16 @@ __global__ __launch_bounds__(256) void gemm_grid_kernel(const uint8_t* __restric
 
   // raw fields: K-step slot C of the block in use is refilled with the next
   // block's as soon as it is decoded (a super-block ahead, one copy)
-  RawG<NF> raw;
+  constexpr int DEPTH = grid_ring_depth(TYPE);
+  RawG<NF, DEPTH> raw;
   uint32_t dcur[NF], dnxt[NF];
   load_d_g<TYPE, NF>(dcur, blk0, 0);
-  load_raw_g<TYPE, NF, 0>(raw, blk0, 0, kq);
-  load_raw_g<TYPE, NF, 1>(raw, blk0, 0, kq);
-  load_raw_g<TYPE, NF, 2>(raw, blk0, 0, kq);
-  load_raw_g<TYPE, NF, 3>(raw, blk0, 0, kq);
+  load_raw_g<TYPE, NF, DEPTH, 0>(raw, blk0, 0, kq);
+  load_raw_g<TYPE, NF, DEPTH, 1>(raw, blk0, 0, kq);
+  if constexpr (DEPTH == 4) {
+    load_raw_g<TYPE, NF, DEPTH, 2>(raw, blk0, 0, kq);
+    load_raw_g<TYPE, NF, DEPTH, 3>(raw, blk0, 0, kq);
+  }
   uint4 areg[A_CHUNKS];
   load_a(0, areg);
   store_a(0, areg);
@@ -3689,11 +3785,14 @@ __global__ __launch_bounds__(256) void gemm_grid_kernel(const uint8_t* __restric
   };
 
   auto step = [&](int b, auto cc) {
-    constexpr int C = decltype(cc)::value;
+    constexpr int C = decltype(cc)::value, Q = 2 * (C % DEPTH);
     half8 bop[2][NF];
-    dequant_g<TYPE, NF>(raw, dcur, 2 * C, kq, glds, smask, bop[0]);
-    dequant_g<TYPE, NF>(raw, dcur, 2 * C + 1, kq, glds, smask, bop[1]);
-    if (b + 1 < nb) load_raw_g<TYPE, NF, C>(raw, blk0, static_cast<uint64_t>(b + 1), kq);
+    dequant_g<TYPE, NF, DEPTH>(raw, dcur, 2 * C, Q, kq, glds, smask, bop[0]);
+    dequant_g<TYPE, NF, DEPTH>(raw, dcur, 2 * C + 1, Q + 1, kq, glds, smask, bop[1]);
+    // refill the slot with K-step C + DEPTH (this block's, or the next's)
+    constexpr int CN = (C + DEPTH) % 4;
+    const int bn = b + (C + DEPTH) / 4;
+    if (bn < nb) load_raw_g<TYPE, NF, DEPTH, CN>(raw, blk0, static_cast<uint64_t>(bn), kq);
     kstep(4 * b + C, bop);
   };
   for (int b = 0; b < nb; ++b) {
@@ -4124,7 +4223,9 @@ void launch_dequantize_grid(int type, const uint8_t* w, uint64_t rows, uint64_t 
 void launch_gemv_grid(int type, const uint8_t* w, uint64_t nb, uint64_t rows, const int8_t* xv, const float* xs,
                       const float* xf, uint64_t m, int int8, float* y, const float* addend, uint64_t addend_stride,
                       hipStream_t stream) {
-  const dim3 grid(static_cast<unsigned>((rows + 3) / 4)), block(256);
+  // at most 4 work-groups per CU: each copies the format's grid table once
+  const uint64_t wgs = (rows + kGridGemvWaves - 1) / kGridGemvWaves;
+  const dim3 grid(static_cast<unsigned>(wgs < 1024 ? wgs : 1024)), block(64 * kGridGemvWaves);
   switch (type) {
 #define MQ_GRID_M(T, MM)                                                                                            \
   case MM:                                                                                                          \
