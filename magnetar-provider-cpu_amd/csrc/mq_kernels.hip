@@ -2315,20 +2315,37 @@ __global__ void dequantize_grid_kernel(const uint8_t* __restrict__ w, uint64_t r
 // vector-memory path to the activation and block loads. INT8: the
 // reference's int8 path (per half: scale * integer dot, times d_act per
 // run); else its f32 column loop (w = scale * q, acc += w * x per value).
+// STAGE (int8 mode, when they fit): the int8 activations and their run
+// scales are copied to LDS too (m K + 4 m K / 32 bytes), so each row's pass
+// reads them from LDS instead of re-reading them through vector memory.
 constexpr int kGridGemvWaves = 8;
-template <int TYPE, int M, bool INT8>
+template <int TYPE, int M, bool INT8, bool STAGE>
 __global__ __launch_bounds__(64 * kGridGemvWaves) void gemv_grid_kernel(
     const uint8_t* __restrict__ w, uint64_t nb, uint64_t rows, const int8_t* __restrict__ xv,
     const float* __restrict__ xs, const float* __restrict__ xf, float* __restrict__ y,
     const float* __restrict__ addend, uint64_t addend_stride) {
+  static_assert(INT8 || !STAGE, "staging is for the int8 activations");
   constexpr int BB = block_bytes_of(TYPE);
   constexpr int GBYTES = grid_table_size(TYPE);
-  __shared__ __attribute__((aligned(16))) uint8_t glds[GBYTES];
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  uint8_t* glds = lds;
+  const uint64_t runs = nb * 8, K = nb * 256;
   for (int i = threadIdx.x; i < GBYTES / 16; i += 64 * kGridGemvWaves)
     reinterpret_cast<uint4*>(glds)[i] = reinterpret_cast<const uint4*>(g_iq_grids + grid_table_offset(TYPE))[i];
+  const int8_t* xsrc = xv;
+  const float* ssrc = xs;
+  if constexpr (STAGE) {
+    int8_t* xl = reinterpret_cast<int8_t*>(lds + GBYTES);
+    float* sl = reinterpret_cast<float*>(lds + GBYTES + M * K);
+    for (uint64_t i = threadIdx.x; i < M * K / 16; i += 64 * kGridGemvWaves)
+      reinterpret_cast<uint4*>(xl)[i] = reinterpret_cast<const uint4*>(xv)[i];
+    for (uint64_t i = threadIdx.x; i < M * runs / 4; i += 64 * kGridGemvWaves)
+      reinterpret_cast<uint4*>(sl)[i] = reinterpret_cast<const uint4*>(xs)[i];
+    xsrc = xl;
+    ssrc = sl;
+  }
   __syncthreads();
   const int lane = threadIdx.x & 63;
-  const uint64_t runs = nb * 8, K = nb * 256;
   for (uint64_t row = static_cast<uint64_t>(blockIdx.x) * kGridGemvWaves + (threadIdx.x >> 6); row < rows;
        row += static_cast<uint64_t>(gridDim.x) * kGridGemvWaves) {
   const uint8_t* base = w + row * nb * BB;
@@ -2352,10 +2369,10 @@ __global__ __launch_bounds__(64 * kGridGemvWaves) void gemv_grid_kernel(
       for (int q = 0; q < 2; ++q)
 #pragma unroll
         for (int m = 0; m < M; ++m) {
-          const uint4* ap = reinterpret_cast<const uint4*>(xv + m * K + 32 * us[q]);
+          const uint4* ap = reinterpret_cast<const uint4*>(xsrc + m * K + 32 * us[q]);
           av[q][m][0] = ap[0];
           av[q][m][1] = ap[1];
-          as[q][m] = xs[m * runs + us[q]];
+          as[q][m] = ssrc[m * runs + us[q]];
         }
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
@@ -4224,17 +4241,24 @@ void launch_gemv_grid(int type, const uint8_t* w, uint64_t nb, uint64_t rows, co
                       const float* xf, uint64_t m, int int8, float* y, const float* addend, uint64_t addend_stride,
                       hipStream_t stream) {
   // at most 4 work-groups per CU: each copies the format's grid table once
+  // (and the int8 activations, when table and activations fit 64 KiB)
   const uint64_t wgs = (rows + kGridGemvWaves - 1) / kGridGemvWaves;
   const dim3 grid(static_cast<unsigned>(wgs < 1024 ? wgs : 1024)), block(64 * kGridGemvWaves);
+  const uint64_t table = static_cast<uint64_t>(grid_table_size(type));
+  const uint64_t staged = table + m * nb * 256 + 4 * m * nb * 8;
+  const bool stage = int8 && staged <= 65536;
   switch (type) {
-#define MQ_GRID_M(T, MM)                                                                                            \
-  case MM:                                                                                                          \
-    if (int8)                                                                                                       \
-      hipLaunchKernelGGL((gemv_grid_kernel<T, MM, true>), grid, block, 0, stream, w, nb, rows, xv, xs, xf, y, addend, \
-                         addend_stride);                                                                            \
-    else                                                                                                            \
-      hipLaunchKernelGGL((gemv_grid_kernel<T, MM, false>), grid, block, 0, stream, w, nb, rows, xv, xs, xf, y,      \
-                         addend, addend_stride);                                                                    \
+#define MQ_GRID_M(T, MM)                                                                                             \
+  case MM:                                                                                                           \
+    if (stage)                                                                                                       \
+      hipLaunchKernelGGL((gemv_grid_kernel<T, MM, true, true>), grid, block, staged, stream, w, nb, rows, xv, xs, xf, \
+                         y, addend, addend_stride);                                                                  \
+    else if (int8)                                                                                                   \
+      hipLaunchKernelGGL((gemv_grid_kernel<T, MM, true, false>), grid, block, table, stream, w, nb, rows, xv, xs, xf, \
+                         y, addend, addend_stride);                                                                  \
+    else                                                                                                             \
+      hipLaunchKernelGGL((gemv_grid_kernel<T, MM, false, false>), grid, block, table, stream, w, nb, rows, xv, xs,   \
+                         xf, y, addend, addend_stride);                                                              \
     break;
 #define X(T)                                                                                                 \
   case T:                                                                                                    \

@@ -134,6 +134,25 @@ def test_input_major_product_and_embedding(gctx, fmt):
         h.release()
 
 
+@pytest.mark.parametrize("fmt", GRID_FORMATS)
+def test_gemv_long_rows_staged_and_unstaged(gctx, fmt):
+    """K = 14336 (the FFN down rows): the int8 activations are staged in LDS
+    with the grid table while m K (1 + 4 / 32) bytes and the table fit 64 KiB
+    (m <= 3), and read from memory beyond (m >= 4); both against the
+    reference's int8 column loop."""
+    n, k = 40, 14336
+    w = packed(fmt, n, k, 37 + fmt)
+    h = gctx.upload(fmt, n, k, w)
+    try:
+        for m in (1, 3, 4, 8):
+            x = activations(m, k, 140 + m)
+            got = gctx.matmul(h, x)
+            assert_row_tolerance(got, dense(fmt, w, n, k, x, True), f"m {m}")
+            assert_close_reference(got, oracle.columns_scalar(fmt, w, n, k, x, True), f"m {m} column loop")
+    finally:
+        h.release()
+
+
 def test_full_size_gemv_sampled_columns(gctx):
     """IQ2_XXS at the Llama FFN up shape, m = 1: 8 sampled output columns
     against the reference's column loop."""
