@@ -228,7 +228,8 @@ __global__ __launch_bounds__(256) void attention_partial_kernel(
 // One work-group of 4 waves per (head, query row). Every wave finds the
 // maximum over the chunks; wave 0 writes the weights e^(m_c - M) to LDS and
 // forms the denominator; wave w then adds chunks w, w + 4, ... for all HD
-// dimensions (2 per lane), and the 4 sums meet in LDS in wave order.
+// dimensions (2 per lane), and the 4 sums meet in LDS in wave order. The
+// first 16 chunks of each wave are loaded before the maximum is known.
 template <int HD>
 __global__ __launch_bounds__(256) void attention_combine_kernel(const float* __restrict__ part, uint64_t heads,
                                                               uint64_t chunks, float* __restrict__ out) {
@@ -238,6 +239,16 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(const float* __r
   const uint64_t h = blockIdx.x, t = blockIdx.y;
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const float* base = part + (t * heads + h) * chunks * (2 + HD);
+  // the wave's first 16 chunks' partial outputs are requested with the
+  // chunk maxima (one memory round trip for up to 64 chunks = 4096 keys)
+  constexpr int kPre = 16;
+  const float* col = base + 2 + 2 * lane;
+  float2 opre[kPre];
+#pragma unroll
+  for (int i = 0; i < kPre; ++i) {
+    const uint64_t c = static_cast<uint64_t>(w) + 4 * i;
+    opre[i] = *reinterpret_cast<const float2*>(col + (c < chunks ? c : 0) * (2 + HD));
+  }
   float mx = -INFINITY;
   for (uint64_t c = lane; c < chunks; c += 64) mx = fmaxf(mx, base[c * (2 + HD)]);
   mx = wave_max(mx);
@@ -254,9 +265,17 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(const float* __r
   }
   __syncthreads();
   float n0 = 0.0f, n1 = 0.0f;
-  const float* col = base + 2 + 2 * lane;
+#pragma unroll
+  for (int i = 0; i < kPre; ++i) {
+    const uint64_t c = static_cast<uint64_t>(w) + 4 * i;
+    if (c < chunks) {
+      const float e = w_lds[c];
+      n0 += e * opre[i].x;
+      n1 += e * opre[i].y;
+    }
+  }
 #pragma unroll 8
-  for (uint64_t c = w; c < chunks; c += 4) {
+  for (uint64_t c = static_cast<uint64_t>(w) + 4 * kPre; c < chunks; c += 4) {
     const float2 o = *reinterpret_cast<const float2*>(col + c * (2 + HD));
     const float e = w_lds[c];
     n0 += e * o.x;

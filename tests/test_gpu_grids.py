@@ -99,8 +99,13 @@ def test_prefill_rows_and_residual(gctx, fmt):
 
 
 @pytest.mark.parametrize("fmt", GRID_FORMATS)
-def test_prequantized_entry_point(gctx, fmt):
-    n, k, m = 64, 512, 3
+@pytest.mark.parametrize("m,k", [(3, 512), (1, 4096), (8, 4096), (3, 14336), (4, 14336)])
+def test_prequantized_entry_point(gctx, fmt, m, k):
+    """The pre-quantized entry point equals the f32 entry point (quantized
+    by the quantization kernel) bit for bit, with the quantized rows
+    staged in LDS (they fit with the grid table) and read from memory (the
+    4 x 14336 case does not fit)."""
+    n = 64
     w = packed(fmt, n, k, 61)
     x = activations(m, k, 62)
     values, scales, sums = oracle.quantize_rows(x)

@@ -82,6 +82,7 @@ def test_kv_write_is_exact_and_bounded(ctx):
 
 @pytest.mark.parametrize("seq,key_count,kv_rows,heads,kv_heads,causal", [
     (1, 4096, 4096, 32, 8, True),   # the Llama-3-8B decode step
+    (1, 5000, 5000, 32, 8, True),   # 79 chunks: past the combine's 16 prefetched chunks per wave
     (1, 100, 4096, 32, 8, True),    # key_count below the store's rows
     (5, 300, 512, 8, 8, True),      # multi-row, causal
     (3, 65, 65, 16, 2, False),      # bidirectional
