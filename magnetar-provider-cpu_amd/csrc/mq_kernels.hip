@@ -2035,29 +2035,51 @@ __global__ __launch_bounds__(512) void gemv_planes_int8_kernel(
   const uint32_t lane_off = static_cast<uint32_t>((lane >> 3) * group_bytes);
   auto block_off = [&](int b) { return b < b1 ? lane_off + static_cast<uint32_t>(b) * kTile : kBufferNone; };
 
-  FusedStage<TYPE, M> fs;
-  QuantizedStage<TYPE, M> qs;
-  if (FUSED)
-    fs.load(xf, K, k0, kn, kv);
-  else
-    qs.load(xv, xs, xsum, K, k0, kn, kv);
-  PlaneBlock<TYPE> A;
-  const int bA = b0 + s;
-  load_planes<TYPE>(A, rsrc, block_off(bA), r);
-  if (FUSED)
-    fs.store(xf, K, k0, kn, kv, lds);
-  else
-    qs.store(xv, xs, xsum, K, k0, kn, kv, lds);
-  __syncthreads();
-
   float acc[M], mins[M];
 #pragma unroll
   for (int m = 0; m < M; ++m) acc[m] = mins[m] = 0.0f;
-  for (int b = bA; b < b1; b += S) {
-    const PlaneBlock<TYPE> cur = A;
-    load_planes<TYPE>(A, rsrc, block_off(b + S), r);
-    __builtin_amdgcn_sched_barrier(0);
-    plane_block_int8<TYPE, M>(cur, lds, kn, kruns, b - b0, acc, mins);
+  const int bA = b0 + s;
+  bool done = false;
+  if constexpr (FUSED && M == 1) {
+    // Wave-local staging, as in the Q4_K form (WaveStage; one row here: with
+    // two rows the two plane blocks in flight spill): when the rows are
+    // whole groups and every wave has at most two blocks (both bounds are
+    // work-group uniform), each wave quantizes its own blocks' activations
+    // into their LDS slots, with both weight blocks in flight from the
+    // start and no work-group barrier before the math.
+    if (b1 - b0 <= 2 * S && static_cast<uint64_t>(nb) * 256 == K) {
+      const int bB = bA + S;
+      WaveStage<TYPE, M, true> ws;
+      ws.load(xf, xv, xs, xsum, K, bA, bB, b1, lane);
+      PlaneBlock<TYPE> A0, A1;
+      load_planes<TYPE>(A0, rsrc, block_off(bA), r);
+      load_planes<TYPE>(A1, rsrc, block_off(bB), r);
+      ws.put(lds, kn, kruns, b0, bA, bB, b1, lane);
+      if (bA < b1) plane_block_int8<TYPE, M>(A0, lds, kn, kruns, bA - b0, acc, mins);
+      if (bB < b1) plane_block_int8<TYPE, M>(A1, lds, kn, kruns, bB - b0, acc, mins);
+      done = true;
+    }
+  }
+  if (!done) {
+    FusedStage<TYPE, M> fs;
+    QuantizedStage<TYPE, M> qs;
+    if (FUSED)
+      fs.load(xf, K, k0, kn, kv);
+    else
+      qs.load(xv, xs, xsum, K, k0, kn, kv);
+    PlaneBlock<TYPE> A;
+    load_planes<TYPE>(A, rsrc, block_off(bA), r);
+    if (FUSED)
+      fs.store(xf, K, k0, kn, kv, lds);
+    else
+      qs.store(xv, xs, xsum, K, k0, kn, kv, lds);
+    __syncthreads();
+    for (int b = bA; b < b1; b += S) {
+      const PlaneBlock<TYPE> cur = A;
+      load_planes<TYPE>(A, rsrc, block_off(b + S), r);
+      __builtin_amdgcn_sched_barrier(0);
+      plane_block_int8<TYPE, M>(cur, lds, kn, kruns, b - b0, acc, mins);
+    }
   }
   finish_rows<M>(acc, mins, rows, y, addend, addend_stride, reinterpret_cast<float*>(lds), sk.partials,
                  sk.counters, sk.ks);

@@ -109,6 +109,35 @@ def test_gemv_every_row_count_and_k_split(ctx, fmt):
 
 
 @pytest.mark.parametrize("fmt", PLANE_FORMATS)
+def test_fused_m1_equals_prequantized(ctx, fmt):
+    """m = 1 with fused quantization equals the pre-quantized GEMV bit for
+    bit, whichever staging the shape takes: wave-local where the rows are
+    whole 256-value groups and each wave has at most two blocks of its K
+    split (K = 1024, 4096), work-group staging where rows end inside a group
+    (K = 800, the 32-value formats) or a split holds more blocks."""
+    ks = (1024, 4096, 8192) + ((800,) if BLOCK_ELEMENTS[fmt] == 32 else ())
+    for k in ks:
+        n = 200
+        w = packed(fmt, n, k, 33 + k)
+        h = ctx.upload(fmt, n, k, w)
+        try:
+            a1 = mg.gaussian(9 + k, 1.0, k).reshape(1, k)
+            x = torch.from_numpy(a1).cuda()
+            xq = torch.empty(k, dtype=torch.int8, device="cuda")
+            xs = torch.empty(k // 32, dtype=torch.float32, device="cuda")
+            xh = torch.empty(k // 16, dtype=torch.int32, device="cuda")
+            y = torch.empty((1, n), dtype=torch.float32, device="cuda")
+            s = torch.cuda.current_stream().cuda_stream
+            ctx.quantize_activations_dev(x.data_ptr(), 1, k, xq.data_ptr(), xs.data_ptr(), xh.data_ptr(), s)
+            ctx.matmul_prequantized_dev(h, xq.data_ptr(), xs.data_ptr(), xh.data_ptr(), 1, k, y.data_ptr(),
+                                        stream=s)
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(y.cpu().numpy(), ctx.matmul(h, a1), f"k {k}")
+        finally:
+            h.release()
+
+
+@pytest.mark.parametrize("fmt", PLANE_FORMATS)
 def test_prequantized_and_f16_entry_points(ctx, fmt):
     """The prequantized GEMV agrees with mq_matmul on the same weight, and
     the GEMM (m = 40) meets the bar; the 32-value formats take K = 800,
