@@ -178,7 +178,9 @@ int mq_prepare_activations_f16_dev(mq_ctx *ctx, const float *x_dev, uint64_t m,
 /* The prefill GEMM on prepared f16 activations (any m): y[m][stored_rows]
  * = a16 . dequantize(W)^T with f32 accumulation, the MFMA replacement of
  * the column kernels for many activation rows
- * (src/native/quant.rs:666-744, 1386-1433 via src/native/mod.rs:110-152). */
+ * (src/native/quant.rs:666-744, 1386-1433 via src/native/mod.rs:110-152).
+ * MQ_DECLINED for an IQ2 / IQ3 grid weight whose device grid tables hold a
+ * byte of 128 or more (mq_set_iq_grids). */
 int mq_matmul_f16_dev(mq_ctx *ctx, uint64_t handle, const uint16_t *a16_dev,
                       uint64_t m, uint64_t k, float *y_dev, void *stream);
 
