@@ -422,6 +422,34 @@ def gemm_part(ctx, torch, workloads, use_graph, args):
     }
     log(f"gemm m=512: step {t_gstep * 1e6:.1f} us ({flops / t_gstep / 1e12:.1f} TFLOP/s), "
         f"kernel {t_gkern * 1e6:.1f} us ({flops / t_gkern / 1e12:.1f} TFLOP/s)")
+    # the prefill shapes around it (kernel time on prepared f16 activations):
+    # M in {128, 512, 2048} over W[4096, 4096] and W[14336, 4096], and the
+    # IQ4_XS W[4096, 14336] at M = 512
+    shapes = {}
+    stream = torch.cuda.current_stream().cuda_stream
+    for wname, mm in (("q4k_14336x4096_s2", 128), ("q4k_14336x4096_s2", 2048), ("q4k_4096x4096_s2", 128),
+                      ("q4k_4096x4096_s2", 512), ("q4k_4096x4096_s2", 2048), ("iq4xs_4096x14336_s3", 512)):
+        sfmt, sn, sk, sseed, _ = workloads.WEIGHTS[wname]
+        sw = gw if wname == gname else ctx.upload(sfmt, sn, sk, workloads.weight_bytes(wname))
+        sx = torch.from_numpy(workloads.activations(sseed, mm, sk)).cuda()
+        sa = torch.empty(mm * sk, dtype=torch.float16, device="cuda")
+        sy = torch.empty((mm, sn), dtype=torch.float32, device="cuda")
+        ctx.prepare_activations_f16_dev(sx.data_ptr(), mm, sk, sa.data_ptr(), int8=True, stream=stream)
+
+        def skern(i, stream, sw=sw, sa=sa, sy=sy, mm=mm, sk=sk):
+            ctx.matmul_f16_dev(sw, sa.data_ptr(), mm, sk, sy.data_ptr(), stream=stream)
+
+        r = GraphRunner(torch, skern, gper, use_graph)
+        r.time(gper)
+        t = r.time(gsteps) / gsteps
+        sflops = 2.0 * mm * sn * sk
+        key = f"{wname.rsplit('_', 1)[0]}_m{mm}"
+        shapes[key] = {"kernel_us": round(t * 1e6, 2), "tflops": round(sflops / t / 1e12, 1),
+                       "frac": round(sflops / t / 1e12 / F16_MFMA_PEAK_TFLOPS, 4)}
+        log(f"gemm {key}: kernel {t * 1e6:.1f} us ({sflops / t / 1e12:.1f} TFLOP/s)")
+        if sw is not gw:
+            sw.release()
+    gemm["shapes"] = shapes
     gw.release()
     return gemm
 

@@ -346,15 +346,21 @@ int matmul_locked(mq_ctx* ctx, const Weight& w, const float* x, uint64_t m, uint
       if (rc) return rc;
     }
   } else {
-    rc = acquire_workspace(ctx, stream, align256(m * k * 2));
+    // workspace: the f16 activations, then (under-filled GEMMs) the split-K
+    // partials
+    const int ks = mq::gemm_splits(static_cast<int>(w.type), w.rows, m, w.nb, k, ctx->gemm_variant);
+    const size_t abytes = align256(m * k * 2);
+    const size_t pbytes = ks > 1 ? align256(static_cast<size_t>(ks) * m * w.rows * sizeof(float)) : 0;
+    rc = acquire_workspace(ctx, stream, abytes + pbytes);
     if (rc) return rc;
     auto* a16 = static_cast<uint16_t*>(ctx->ws);
+    float* part = ks > 1 ? reinterpret_cast<float*>(static_cast<uint8_t*>(ctx->ws) + abytes) : nullptr;
     if (int8)
       mq::launch_quantize_activations(x, m, k, nullptr, nullptr, nullptr, a16, 1, stream);
     else
       mq::launch_activations_f16(x, m, k, a16, stream);
     mq::launch_gemm(static_cast<int>(w.type), w.dev, w.rows, w.nb, k, a16, m, y, addend, addend_stride,
-                    ctx->gemm_variant, stream);
+                    ctx->gemm_variant, stream, part);
   }
   MQ_HIP(ctx, hipGetLastError());
   return MQ_OK;
@@ -768,8 +774,15 @@ int mq_matmul_f16_dev(mq_ctx* ctx, uint64_t handle, const uint16_t* a16_dev, uin
     return fail(ctx, MQ_DECLINED, "the f16 MFMA GEMM of the IQ2 / IQ3 grid formats needs grid magnitudes below 128");
   DeviceGuard guard(ctx->device);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const int ks = mq::gemm_splits(static_cast<int>(w->type), w->rows, m, w->nb, w->cols, ctx->gemm_variant);
+  float* part = nullptr;
+  if (ks > 1) {
+    rc = acquire_workspace(ctx, s, align256(static_cast<size_t>(ks) * m * w->rows * sizeof(float)));
+    if (rc) return rc;
+    part = static_cast<float*>(ctx->ws);
+  }
   mq::launch_gemm(static_cast<int>(w->type), w->dev, w->rows, w->nb, w->cols, a16_dev, m, y_dev, nullptr, 0,
-                  ctx->gemm_variant, s);
+                  ctx->gemm_variant, s, part);
   MQ_HIP(ctx, hipGetLastError());
   return MQ_OK;
 }

@@ -3178,7 +3178,13 @@ __global__ __launch_bounds__(256) void gemm_rb_kernel(const uint8_t* __restrict_
   const uint64_t m0 = static_cast<uint64_t>(blockIdx.y) * BM;
   const uint64_t n0 = static_cast<uint64_t>(blockIdx.x) * (4 * NF * 16) + static_cast<uint64_t>(wave) * NF * 16;
   const uint64_t K = static_cast<uint64_t>(nb) * 256;
-  const int ksteps = nb * 4;
+  // split-K over gridDim.z work-groups: super-blocks [bl, bh) of the row,
+  // results to the split's own [m_rows][rows] slice of y (the partials,
+  // which the host sums in split order)
+  const int bl = static_cast<int>(blockIdx.z * static_cast<uint64_t>(nb) / gridDim.z);
+  const int bh = static_cast<int>((blockIdx.z + 1) * static_cast<uint64_t>(nb) / gridDim.z);
+  const int ksteps = bh * 4;  // K-step indices are absolute
+  y += static_cast<uint64_t>(blockIdx.z) * m_rows * rows;
 
   floatx4 acc[MF][NF];
 #pragma unroll
@@ -3231,10 +3237,10 @@ __global__ __launch_bounds__(256) void gemm_rb_kernel(const uint8_t* __restrict_
     }
   };
   Raw cur, nxt;
-  load_b(nxt, 0);
+  load_b(nxt, static_cast<uint64_t>(bl));
   uint4 areg[A_CHUNKS];
-  load_a(0, areg);
-  store_a(0, areg);
+  load_a(4 * bl, areg);
+  store_a(0, areg);  // K-step 4 bl is even: buffer 0
   __syncthreads();
 
   auto kstep = [&](int kb, const half8 (&bop)[2][NF]) {
@@ -3255,9 +3261,9 @@ __global__ __launch_bounds__(256) void gemm_rb_kernel(const uint8_t* __restrict_
     __syncthreads();
   };
 
-  for (int b = 0; b < nb; ++b) {
+  for (int b = bl; b < bh; ++b) {
     cur = nxt;
-    if (b + 1 < nb) load_b(nxt, static_cast<uint64_t>(b + 1));
+    if (b + 1 < bh) load_b(nxt, static_cast<uint64_t>(b + 1));
     half8 bop[2][NF];
     if constexpr (is_plane_format(TYPE)) {
       dequant_pb<TYPE, NF, 0>(cur, kq, bop);
@@ -4494,10 +4500,11 @@ namespace {
 
 template <int MF, int NF>
 void launch_gemm_rb(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, const uint16_t* a16, uint64_t m,
-                    float* y, const float* addend, uint64_t addend_stride, hipStream_t stream) {
+                    float* y, const float* addend, uint64_t addend_stride, hipStream_t stream, int ks = 1) {
   const uint64_t rows_padded = (rows + 7) / 8 * 8;
   const uint64_t bn = 4 * NF * 16, bm = MF * 16;
-  dim3 grid(static_cast<unsigned>((rows + bn - 1) / bn), static_cast<unsigned>((m + bm - 1) / bm));
+  dim3 grid(static_cast<unsigned>((rows + bn - 1) / bn), static_cast<unsigned>((m + bm - 1) / bm),
+            static_cast<unsigned>(ks));
   switch (type) {
 #define X(T)                                                                                                     \
   case T:                                                                                                        \
@@ -4533,6 +4540,20 @@ uint64_t tiles(uint64_t rows, uint64_t m, uint64_t bn, uint64_t bm) {
   return ((rows + bn - 1) / bn) * ((m + bm - 1) / bm);
 }
 
+// Split-K sum of the register-B GEMM: y = partials of split 0 + split 1 +
+// ... in split order, then + addend (the epilogue's order).
+__global__ void gemm_split_reduce_kernel(const float* __restrict__ part, int ks, uint64_t m_rows, uint64_t rows,
+                                         float* __restrict__ y, const float* __restrict__ addend,
+                                         uint64_t addend_stride) {
+  const uint64_t count = m_rows * rows;
+  const uint64_t i = blockIdx.x * static_cast<uint64_t>(blockDim.x) + threadIdx.x;
+  if (i >= count) return;
+  float v = part[i];
+  for (int z = 1; z < ks; ++z) v = v + part[static_cast<uint64_t>(z) * count + i];
+  if (addend) v = v + addend[(i / rows) * addend_stride + i % rows];
+  y[i] = v;
+}
+
 }  // namespace
 
 int gemm_default_variant(int type, uint64_t rows, uint64_t m) {
@@ -4545,9 +4566,39 @@ int gemm_default_variant(int type, uint64_t rows, uint64_t m) {
   return 3;
 }
 
+// The register-B form's split-K factor: 1 unless its tiles leave most CUs
+// idle (fewer than 192 work-groups); then enough splits for about 224
+// work-groups, at most 8 and at most one per super-block.
+int gemm_splits(int type, uint64_t rows, uint64_t m, uint64_t nb, uint64_t k, int variant) {
+  if (is_grid_format(type) || (is_plane_format(type) && k % 256 != 0)) return 1;
+  if (variant == 0) variant = gemm_default_variant(type, rows, m);
+  if (variant == 5 && type != kTypeQ4K) variant = 3;
+  if (variant != 2 && variant != 3 && variant != 4) return 1;
+  const uint64_t t = tiles(rows, m, variant == 3 ? 128 : 256, variant == 4 ? 64 : 128);
+  if (t >= 192) return 1;
+  uint64_t ks = (224 + t - 1) / t;
+  if (ks > 8) ks = 8;
+  if (ks > nb) ks = nb;
+  return static_cast<int>(ks);
+}
+
 void launch_gemm(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, uint64_t k, const uint16_t* a16,
                  uint64_t m, float* y, const float* addend, uint64_t addend_stride, int variant,
-                 hipStream_t stream) {
+                 hipStream_t stream, float* part) {
+  const int ks = part ? gemm_splits(type, rows, m, nb, k, variant) : 1;
+  if (ks > 1) {
+    // the register-B form over ks K ranges into `part`, then their sum
+    const int v = variant == 0 ? gemm_default_variant(type, rows, m) : (variant == 5 ? 3 : variant);
+    if (v == 2)
+      launch_gemm_rb<8, 4>(type, tiled, rows, nb, a16, m, part, nullptr, 0, stream, ks);
+    else if (v == 4)
+      launch_gemm_rb<4, 4>(type, tiled, rows, nb, a16, m, part, nullptr, 0, stream, ks);
+    else
+      launch_gemm_rb<8, 2>(type, tiled, rows, nb, a16, m, part, nullptr, 0, stream, ks);
+    hipLaunchKernelGGL(gemm_split_reduce_kernel, dim3(grid_for(m * rows, 256)), dim3(256), 0, stream, part, ks, m,
+                       rows, y, addend, addend_stride);
+    return;
+  }
   const uint64_t rows_padded = (rows + 7) / 8 * 8;
   dim3 grid(static_cast<unsigned>((rows + kBN - 1) / kBN), static_cast<unsigned>((m + kBM - 1) / kBM));
   if (is_grid_format(type)) {
