@@ -11,7 +11,7 @@ import pytest
 
 import magnetar_gpu as mg
 import oracle
-from helpers import (IQ4_XS, Q4_K, activations, assert_close_reference, assert_row_tolerance, packed,
+from helpers import (IQ4_XS, Q4_K, Q6_K, activations, assert_close_reference, assert_row_tolerance, packed,
                      row_tolerance_violation)
 from magnetar_gpu import workloads
 
@@ -270,6 +270,33 @@ def test_gemm_k_split_form_residual(ks_ctx):
             assert_row_tolerance(y.cpu().numpy(), (base + r).astype(np.float32), f"residual rows {r_rows}")
     finally:
         h.release()
+
+
+@pytest.mark.parametrize("fmt", [Q4_K, IQ4_XS, Q6_K])
+def test_gemm_split_k_register_b_form(ctx, fmt):
+    """Under-filled register-B GEMMs split K over work-groups and sum the
+    partials in split order (splits 4, 2 and 8 here, the second capped by
+    the row's two super-blocks): within the bar of the dense oracle,
+    deterministic, and the residual added after the sum (equal to the
+    product plus r bit for bit)."""
+    for m, n, k in ((160, 384, 1024), (40, 300, 512), (130, 1024, 4096)):
+        w = packed(fmt, n, k, 90 + m)
+        a = activations(m, k, 91 + m)
+        h = ctx.upload(fmt, n, k, w)
+        try:
+            got = ctx.matmul(h, a)
+            assert_row_tolerance(got, expected(fmt, w, n, k, a, True), f"m {m} n {n} k {k}")
+            np.testing.assert_array_equal(got.view(np.uint32), ctx.matmul(h, a).view(np.uint32))
+            x = dev(a)
+            for r_rows in (1, m):
+                r = activations(r_rows, n, 92 + r_rows)
+                y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+                ctx.matmul_add_dev(h, x.data_ptr(), m, k, dev(r).data_ptr(), r_rows, y.data_ptr())
+                torch.cuda.synchronize()
+                np.testing.assert_array_equal(y.cpu().numpy(), (got + r).astype(np.float32),
+                                              err_msg=f"residual rows {r_rows}, m {m} n {n}")
+        finally:
+            h.release()
 
 
 # ---- properties at full size -------------------------------------------------------
