@@ -3781,7 +3781,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NF == 2 ? 2
   const uint64_t m0 = static_cast<uint64_t>(blockIdx.y) * BM;
   const uint64_t n0 = static_cast<uint64_t>(blockIdx.x) * (4 * NF * 16) + static_cast<uint64_t>(wave) * NF * 16;
   const uint64_t K = static_cast<uint64_t>(nb) * 256;
-  const int ksteps = nb * 4;
+  // split-K over gridDim.z: super-blocks [bl, bh), results to the split's
+  // own [m_rows][rows] slice of y (partials summed by the host)
+  const int bl = static_cast<int>(blockIdx.z * static_cast<uint64_t>(nb) / gridDim.z);
+  const int bh = static_cast<int>((blockIdx.z + 1) * static_cast<uint64_t>(nb) / gridDim.z);
+  const int ksteps = bh * 4;  // K-step indices are absolute
+  y += static_cast<uint64_t>(blockIdx.z) * m_rows * rows;
 
   floatx4 acc[MF][NF];
 #pragma unroll
@@ -3831,16 +3836,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NF == 2 ? 2
   constexpr int DEPTH = grid_ring_depth(TYPE);
   RawG<NF, DEPTH> raw;
   uint32_t dcur[NF], dnxt[NF];
-  load_d_g<TYPE, NF>(dcur, blk0, 0);
-  load_raw_g<TYPE, NF, DEPTH, 0>(raw, blk0, 0, kq);
-  load_raw_g<TYPE, NF, DEPTH, 1>(raw, blk0, 0, kq);
+  const uint64_t b0 = static_cast<uint64_t>(bl);
+  load_d_g<TYPE, NF>(dcur, blk0, b0);
+  load_raw_g<TYPE, NF, DEPTH, 0>(raw, blk0, b0, kq);
+  load_raw_g<TYPE, NF, DEPTH, 1>(raw, blk0, b0, kq);
   if constexpr (DEPTH == 4) {
-    load_raw_g<TYPE, NF, DEPTH, 2>(raw, blk0, 0, kq);
-    load_raw_g<TYPE, NF, DEPTH, 3>(raw, blk0, 0, kq);
+    load_raw_g<TYPE, NF, DEPTH, 2>(raw, blk0, b0, kq);
+    load_raw_g<TYPE, NF, DEPTH, 3>(raw, blk0, b0, kq);
   }
   uint4 areg[A_CHUNKS];
-  load_a(0, areg);
-  store_a(0, areg);
+  load_a(4 * bl, areg);
+  store_a(0, areg);  // K-step 4 bl is even: buffer 0
   __syncthreads();
 
   auto kstep = [&](int kb, const half8 (&bop)[2][NF]) {
@@ -3869,11 +3875,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NF == 2 ? 2
     // refill the slot with K-step C + DEPTH (this block's, or the next's)
     constexpr int CN = (C + DEPTH) % 4;
     const int bn = b + (C + DEPTH) / 4;
-    if (bn < nb) load_raw_g<TYPE, NF, DEPTH, CN>(raw, blk0, static_cast<uint64_t>(bn), kq);
+    if (bn < bh) load_raw_g<TYPE, NF, DEPTH, CN>(raw, blk0, static_cast<uint64_t>(bn), kq);
     kstep(4 * b + C, bop);
   };
-  for (int b = 0; b < nb; ++b) {
-    const bool more = b + 1 < nb;
+  for (int b = bl; b < bh; ++b) {
+    const bool more = b + 1 < bh;
     if (more) load_d_g<TYPE, NF>(dnxt, blk0, static_cast<uint64_t>(b + 1));
     step(b, std::integral_constant<int, 0>{});
     step(b, std::integral_constant<int, 1>{});
@@ -4520,9 +4526,10 @@ void launch_gemm_rb(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, 
 
 template <int MF, int NF>
 void launch_gemm_grid(int type, const uint8_t* w, uint64_t rows, uint64_t nb, const uint16_t* a16, uint64_t m,
-                      float* y, const float* addend, uint64_t addend_stride, hipStream_t stream) {
+                      float* y, const float* addend, uint64_t addend_stride, hipStream_t stream, int ks = 1) {
   const uint64_t bn = 4 * NF * 16, bm = MF * 16;
-  dim3 grid(static_cast<unsigned>((rows + bn - 1) / bn), static_cast<unsigned>((m + bm - 1) / bm));
+  dim3 grid(static_cast<unsigned>((rows + bn - 1) / bn), static_cast<unsigned>((m + bm - 1) / bm),
+            static_cast<unsigned>(ks));
   switch (type) {
 #define X(T)                                                                                                    \
   case T:                                                                                                       \
@@ -4570,8 +4577,11 @@ int gemm_default_variant(int type, uint64_t rows, uint64_t m) {
 // idle (fewer than 192 work-groups); then enough splits for about 224
 // work-groups, at most 8 and at most one per super-block.
 int gemm_splits(int type, uint64_t rows, uint64_t m, uint64_t nb, uint64_t k, int variant) {
-  if (is_grid_format(type) || (is_plane_format(type) && k % 256 != 0)) return 1;
-  if (variant == 0) variant = gemm_default_variant(type, rows, m);
+  if (is_plane_format(type) && k % 256 != 0) return 1;
+  if (is_grid_format(type))
+    variant = variant == 2 || (variant == 0 && tiles(rows, m, 256, 128) >= 1024) ? 2 : 3;
+  else if (variant == 0)
+    variant = gemm_default_variant(type, rows, m);
   if (variant == 5 && type != kTypeQ4K) variant = 3;
   if (variant != 2 && variant != 3 && variant != 4) return 1;
   const uint64_t t = tiles(rows, m, variant == 3 ? 128 : 256, variant == 4 ? 64 : 128);
@@ -4586,6 +4596,15 @@ void launch_gemm(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, uin
                  uint64_t m, float* y, const float* addend, uint64_t addend_stride, int variant,
                  hipStream_t stream, float* part) {
   const int ks = part ? gemm_splits(type, rows, m, nb, k, variant) : 1;
+  if (ks > 1 && is_grid_format(type)) {
+    if (variant == 2)
+      launch_gemm_grid<8, 4>(type, tiled, rows, nb, a16, m, part, nullptr, 0, stream, ks);
+    else
+      launch_gemm_grid<8, 2>(type, tiled, rows, nb, a16, m, part, nullptr, 0, stream, ks);
+    hipLaunchKernelGGL(gemm_split_reduce_kernel, dim3(grid_for(m * rows, 256)), dim3(256), 0, stream, part, ks, m,
+                       rows, y, addend, addend_stride);
+    return;
+  }
   if (ks > 1) {
     // the register-B form over ks K ranges into `part`, then their sum
     const int v = variant == 0 ? gemm_default_variant(type, rows, m) : (variant == 5 ? 3 : variant);

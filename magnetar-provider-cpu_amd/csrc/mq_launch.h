@@ -96,11 +96,12 @@ void launch_gemv_f32(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb,
 // in the device copy) take the register-B form: 128 x 256 tiles for
 // variant 2, else 128 x 128.
 // part: gemm_splits(...) * m * rows floats of workspace for the split-K
-// partials of an under-filled register-B GEMM (nullptr: no split).
+// partials of an under-filled register-B or grid-format GEMM (nullptr: no
+// split).
 void launch_gemm(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, uint64_t k,
                  const uint16_t* a16, uint64_t m, float* y, const float* addend, uint64_t addend_stride,
                  int variant, hipStream_t stream, float* part = nullptr);
-// Split-K factor of that GEMM (1: none).
+// Split-K factor of that GEMM (register-B and grid-format forms; 1: none).
 int gemm_splits(int type, uint64_t rows, uint64_t m, uint64_t nb, uint64_t k, int variant);
 int gemm_default_variant(int type, uint64_t rows, uint64_t m);
 
