@@ -3654,10 +3654,11 @@ struct RawG {
   uint32_t a[NF][2 * DEPTH], b[NF][2 * DEPTH], c[NF][2 * DEPTH];
 };
 
-// Ring depth in K-steps: a whole super-block where the registers allow two
-// waves per SIMD, half of one for the formats with three fields per run.
+// Ring depth in K-steps: half a super-block for the formats with three
+// fields per run (registers) and for IQ2_XXS (measured: M = 512 GEMM 181 ->
+// 166 us), a whole one for the others.
 __host__ __device__ constexpr int grid_ring_depth(int type) {
-  return type == kTypeIq2S || type == kTypeIq3S ? 2 : 4;
+  return type == kTypeIq2S || type == kTypeIq3S || type == kTypeIq2Xxs ? 2 : 4;
 }
 
 template <int TYPE, int NF>
