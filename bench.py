@@ -38,13 +38,39 @@ def log(*a):
 
 
 def cpu_model():
+    """The host CPU as /proc/cpuinfo names it, with its family / model /
+    stepping numbers (a virtualised host may print only the vendor line)."""
+    fields = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            if ":" in line:
+                key, val = (t.strip() for t in line.split(":", 1))
+                fields.setdefault(key, val)
+            elif fields:
+                break  # the first processor's block is enough
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    name = fields.get("model name", "unknown")
+    ident = ", ".join(f"{k} {fields[k]}" for k in ("cpu family", "model", "stepping") if k in fields)
+    return f"{name} ({ident})" if ident else name
+
+
+def affinity_threads():
+    """T: the logical CPUs this process may run on (the reference sizes its
+    pool by available_parallelism, which reads the same mask)."""
+    try:
+        return len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        return os.cpu_count() or 1
+
+
+def graph_size(steps, cap):
+    """Calls per captured graph: the largest divisor of `steps` not above
+    `cap`, so that exactly `steps` calls are timed."""
+    for d in range(max(1, min(cap, steps)), 0, -1):
+        if steps % d == 0:
+            return d
+    return 1
 
 
 class GraphRunner:
@@ -75,12 +101,15 @@ class GraphRunner:
         torch.cuda.synchronize()
 
     def run(self, calls):
-        """Enqueues `calls` calls (a multiple of per_graph) on the current stream."""
+        """Enqueues `calls` calls on the current stream: whole graph replays,
+        then the remainder (calls % per_graph) as eager launches."""
         torch = self.torch
         cur = torch.cuda.current_stream()
         if self.graph is not None:
             for _ in range(calls // self.per_graph):
                 self.graph.replay()
+            for i in range(calls % self.per_graph):
+                self.fn(i, cur.cuda_stream)
         else:
             for i in range(calls):
                 self.fn(i, cur.cuda_stream)
@@ -129,8 +158,10 @@ def main():
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=8.0, help="bound on CPU-baseline timing")
-    ap.add_argument("--parts", default="gemv,shapes,iq4xs,layer,formats,gemm,cpu",
+    ap.add_argument("--parts", default="gemv,stream,shapes,iq4xs,layer,formats,gemm,cpu",
                     help="comma list of parts to run (the headline line needs gemv)")
+    ap.add_argument("--layer-copies", type=int, default=3,
+                    help="decoder-layer copies the decode step rotates through (> 256 MB in all)")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="also run a plain device copy of this size (counter calibration under rocprofv3)")
     args = ap.parse_args()
@@ -151,9 +182,12 @@ def main():
 
     torch.cuda.set_device(0)
     ctx = mg.Context(0)
-    per_graph = args.per_graph
-    steps = round_up(max(args.steps, per_graph), per_graph)
-    warmup = round_up(max(args.warmup, per_graph), per_graph)
+    if args.steps < 1 or args.warmup < 0:
+        print("--steps must be at least 1 and --warmup at least 0", file=sys.stderr)
+        sys.exit(2)
+    # exactly --steps timed calls and --warmup untimed ones for the headline
+    steps, warmup = args.steps, args.warmup
+    per_graph = graph_size(steps, args.per_graph)
 
     # ---- decode GEMV: Q4_K x[1, 4096] . W[14336, 4096]^T -------------------------
     name = "q4k_14336x4096_s1"
@@ -181,7 +215,7 @@ def main():
                                  torch.cuda.current_stream().cuda_stream)
     use_graph = not args.no_graph
     step_runner = GraphRunner(torch, step, per_graph, use_graph)
-    step_runner.time(warmup)
+    step_runner.run(warmup)
     t_step = step_runner.time(steps)
     ms_per_step = t_step / steps * 1e3
     value = weight_bytes * steps / t_step / 1e9
@@ -194,7 +228,7 @@ def main():
     log(f"gemv kernel (fused quantize + GEMV): {kernel_us:.2f} us, {achieved:.1f} GB/s = "
         f"{achieved / HBM_PEAK_GBS:.3f} of HBM peak")
     kernel_runner = GraphRunner(torch, gemv_only, per_graph, use_graph)
-    kernel_runner.time(warmup)
+    kernel_runner.run(max(warmup, per_graph))
     t_pre = kernel_runner.time(steps) / steps
     log(f"gemv on pre-quantized activations: {t_pre * 1e6:.2f} us, {weight_bytes / t_pre / 1e9:.1f} GB/s")
 
@@ -236,20 +270,58 @@ def main():
         extra[f"q4k_gemv_m{m}_GBps"] = round(weight_bytes / t / 1e9, 1)
         log(f"gemv m={m} kernel: {t * 1e6:.2f} us, {weight_bytes / t / 1e9:.1f} GB/s")
 
+    if "stream" in parts:
+        stream_part(torch, weight_bytes, args.copies, kernel_us, extra)
     if "iq4xs" in parts:
         iq4xs_part(ctx, torch, workloads, args, per_graph, use_graph, extra)
     if "layer" in parts:
-        layer_part(ctx, torch, per_graph, use_graph, extra)
+        layer_part(ctx, torch, per_graph, use_graph, extra, args.layer_copies)
     if "formats" in parts:
         formats_part(ctx, torch, per_graph, use_graph, extra)
     gemm = gemm_part(ctx, torch, workloads, use_graph, args) if "gemm" in parts else None
-    cpu = cpu_part(fmt, wbytes, n, k, x_host, y_gpu, weight_bytes, args) if "cpu" in parts else None
+    cpu = cpu_part(fmt, wbytes, n, k, x_host, y_gpu, weight_bytes, args, kernel_us, gemm, extra) \
+        if "cpu" in parts else None
 
     for h in copies:
         h.release()
     ctx.close()
     emit(args, value, steps, warmup, ms_per_step, n, k, weight_bytes, use_graph, step_runner, achieved, kernel_us,
          cpu, gemm, extra)
+
+
+def stream_part(torch, nbytes, copies, gemv_us, extra):
+    """The practical read ceiling at the GEMV's size: a kernel that only
+    reads `nbytes` (the headline weight's bytes) with 16-byte loads, rotated
+    over as many distinct buffers as the GEMV's weight copies (so the MALL
+    cannot serve it), best over a small sweep of launch shapes."""
+    import magnetar_gpu as mg
+
+    L = mg.probe_lib()
+    bufs = [torch.randint(-2**31, 2**31 - 1, (nbytes // 4,), dtype=torch.int32, device="cuda") for _ in range(copies)]
+    best = None
+    for loads in (1, 2, 4, 8):
+        for block in (256, 512):
+            sink = torch.zeros(int(L.mqp_stream_groups(nbytes, loads, block)), dtype=torch.int32, device="cuda")
+
+            def read(i, stream, loads=loads, block=block, sink=sink):
+                rc = L.mqp_stream_read(bufs[i % len(bufs)].data_ptr(), nbytes, loads, block, sink.data_ptr(), stream)
+                if rc:
+                    raise RuntimeError("stream-read probe launch failed")
+
+            r = GraphRunner(torch, read, 100, True)
+            r.run(100)
+            t = r.time(500) / 500
+            if best is None or t < best[0]:
+                best = (t, loads, block)
+    t, loads, block = best
+    extra["stream_read_ceiling_us"] = round(t * 1e6, 3)
+    extra["stream_read_ceiling_GBps"] = round(nbytes / t / 1e9, 1)
+    extra["stream_read_ceiling_frac_hbm"] = round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)
+    extra["stream_read_ceiling_shape"] = f"{nbytes} B x {copies} buffers, {loads} x 16 B per lane, {block} threads"
+    extra["gemv_frac_of_stream_ceiling"] = round(t * 1e6 / gemv_us, 4)
+    log(f"streaming-read ceiling at {nbytes} B: {t * 1e6:.2f} us, {nbytes / t / 1e9:.1f} GB/s "
+        f"({loads} loads/lane, {block} threads); the GEMV step reaches {t * 1e6 / gemv_us:.3f} of it")
+    del bufs
 
 
 def iq4xs_part(ctx, torch, workloads, args, per_graph, use_graph, extra):
@@ -282,23 +354,26 @@ def iq4xs_part(ctx, torch, workloads, args, per_graph, use_graph, extra):
         h.release()
 
 
-def layer_part(ctx, torch, per_graph, use_graph, extra):
+def layer_part(ctx, torch, per_graph, use_graph, extra, copies):
     # ---- one Llama-3-8B-shaped decoder layer decode step (seed 4) ----------------
     # fused: 6 launches (mq_decode_matmul_dev); unfused: each operator's own
-    # entry point, 12 launches
+    # entry point, 12 launches. The step rotates through `copies` uploads of
+    # the layer (weights and KV cache: 156 MB each), so successive steps
+    # read distinct bytes and the 256 MB MALL cannot hold the working set.
     from magnetar_gpu import decoder
 
     data = decoder.LayerData(seed=4)
     position = data.prefilled  # the token after the 4095 cached ones
     kv_bytes = 2 * (position + 1) * decoder.KV_HEADS * decoder.HEAD_DIM * 4
     hbm = data.weight_bytes() + kv_bytes
+    copies = max(2, copies)
     for fused, key in ((True, "layer_decode_step"), (False, "layer_decode_step_unfused")):
-        layer = decoder.DecoderLayer(ctx, torch, data, fused=fused)
+        layers = [decoder.DecoderLayer(ctx, torch, data, fused=fused) for _ in range(copies)]
 
-        def step(i, stream, layer=layer):
-            layer.step(position, stream=stream)
+        def step(i, stream, layers=layers):
+            layers[i % len(layers)].step(position, stream=stream)
 
-        per = max(10, per_graph // 10)
+        per = 10 * copies
         r = GraphRunner(torch, step, per, use_graph)
         r.time(per)
         calls = 10 * per
@@ -307,9 +382,14 @@ def layer_part(ctx, torch, per_graph, use_graph, extra):
         extra[f"{key}_GBps"] = round(hbm / t / 1e9, 1)
         extra[f"{key}_frac_hbm"] = round(hbm / t / 1e9 / HBM_PEAK_GBS, 4)
         log(f"decoder layer decode step ({'fused, 6' if fused else 'unfused, 12'} launches): {t * 1e6:.1f} us, "
-            f"{hbm} HBM bytes (Q4_K weights {data.weight_bytes()} + f32 K/V {kv_bytes}), {hbm / t / 1e9:.1f} GB/s")
-        layer.release()
+            f"{hbm} HBM bytes (Q4_K weights {data.weight_bytes()} + f32 K/V {kv_bytes}), {hbm / t / 1e9:.1f} GB/s, "
+            f"rotated over {copies} layer copies ({copies * hbm / 2**20:.0f} MiB)")
+        for layer in layers:
+            layer.release()
+        del layers
+        torch.cuda.empty_cache()
     extra["layer_decode_step_bytes"] = hbm
+    extra["layer_decode_step_copies"] = copies
 
 
 def formats_part(ctx, torch, per_graph, use_graph, extra):
@@ -413,6 +493,7 @@ def gemm_part(ctx, torch, workloads, use_graph, args):
     t_gkern = r.time(gsteps) / gsteps
     gemm = {
         "workload": "Q4_K prefill GEMM x[512,4096] . W[14336,4096]^T, seed 2",
+        "dtype": "f16 MFMA operands (f16(q*d) int8-rounded activations, f16(s*q-m) weights), f32 accumulate",
         "step_tflops": round(flops / t_gstep / 1e12, 2),
         "ms_per_step": round(t_gstep * 1e3, 4),
         "roofline": {"bound": "mfma", "achieved": round(flops / t_gkern / 1e12, 2), "peak": F16_MFMA_PEAK_TFLOPS,
@@ -454,37 +535,100 @@ def gemm_part(ctx, torch, workloads, use_graph, args):
     return gemm
 
 
-def cpu_part(fmt, wbytes, n, k, x_host, y_gpu, weight_bytes, args):
+def cpu_time(fn, seconds, min_reps=3, max_reps=1000):
+    """Mean seconds per call of fn() after one warm-up call: at least
+    `min_reps` calls, more while under `seconds`."""
+    fn()
+    reps = 0
+    t0 = time.perf_counter()
+    while reps < min_reps or (time.perf_counter() - t0 < seconds and reps < max_reps):
+        fn()
+        reps += 1
+    return (time.perf_counter() - t0) / reps, reps
+
+
+def cpu_part(fmt, wbytes, n, k, x_host, y_gpu, weight_bytes, args, gemv_us, gemm, extra):
     # ---- CPU baseline: the reference's AVX2 path on this host ------------------------
+    # The oracle's restatement of columns_q4k_avx2 / columns_iq4xs_avx2 with the
+    # reference's column chunking over a pool (src/native/quant.rs:666-744,
+    # 1386-1433; src/native/mod.rs:110-152; src/native/pool.rs), at
+    # T = the affinity mask's CPU count capped at 16 (the box's CPU share),
+    # and at 1 thread; the dense f32 oracle (src/lib.rs:262-318) at the
+    # CPU-only matvec.
     import numpy as np
 
     import oracle
+    from magnetar_gpu import workloads
 
-    threads = min(16, os.cpu_count() or 1)
-    got = oracle.baseline_packed_matmul(fmt, wbytes, n, k, x_host, threads)  # warm-up
+    avail = affinity_threads()
+    threads = min(16, avail)
+    budget = args.cpu_seconds
+    legs = {}
+
+    # config 2 (the headline shape): Q4_K x[1,4096] . W[14336,4096]^T
+    got = oracle.baseline_packed_matmul(fmt, wbytes, n, k, x_host, threads)
     err = float(np.max(np.abs(got - y_gpu)))
-    reps = 0
-    t0 = time.perf_counter()
-    while reps < 10 or (time.perf_counter() - t0 < args.cpu_seconds and reps < 1000):
-        oracle.baseline_packed_matmul(fmt, wbytes, n, k, x_host, threads)
-        reps += 1
-    t_cpu = (time.perf_counter() - t0) / reps
-    t1_reps = 0
-    t0 = time.perf_counter()
-    while t1_reps < 3 or (time.perf_counter() - t0 < args.cpu_seconds / 4 and t1_reps < 50):
-        oracle.baseline_packed_matmul(fmt, wbytes, n, k, x_host, 1)
-        t1_reps += 1
-    t_cpu1 = (time.perf_counter() - t0) / t1_reps
+    t_cpu, reps = cpu_time(lambda: oracle.baseline_packed_matmul(fmt, wbytes, n, k, x_host, threads), budget, 10)
+    t_cpu1, _ = cpu_time(lambda: oracle.baseline_packed_matmul(fmt, wbytes, n, k, x_host, 1), budget / 4, 3, 50)
     cpu = {
         "value": round(weight_bytes / t_cpu / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
         "sample": (f"Q4_K x[1,4096] . W[14336,4096]^T, int8 activations, AVX2 column kernels + "
-                   f"pool chunking; 1 warm-up + {reps} timed calls ({t_cpu * 1e3:.2f} ms/call)"),
+                   f"pool chunking; 1 warm-up + {reps} timed calls ({t_cpu * 1e3:.3f} ms/call)"),
         "single_thread_GBps": round(weight_bytes / t_cpu1 / 1e9, 2),
+        "threads_available": avail,
         "cpu_model": cpu_model(),
         "max_abs_diff_vs_gpu": err,
+        "gpu_over_cpu": round(t_cpu / (gemv_us * 1e-6), 1),
     }
-    log(f"cpu baseline ({threads} threads, {cpu_model()}): {t_cpu * 1e3:.2f} ms/call, "
+    log(f"cpu baseline, config 2 ({threads} of {avail} threads, {cpu_model()}): {t_cpu * 1e3:.3f} ms/call, "
         f"{cpu['value']} GB/s; 1 thread {cpu['single_thread_GBps']} GB/s; max|gpu-cpu| {err:.2e}")
+
+    # config 1: the CPU-only Q4_K matvec x[1,4096] . W[4096,4096]^T, plus the
+    # dense f32 oracle on the dequantized weight (ReferenceCpuExecutor's path)
+    name1 = "q4k_4096x4096_s0"
+    f1, n1, k1, s1, _ = workloads.WEIGHTS[name1]
+    w1 = workloads.weight_bytes(name1)
+    x1 = workloads.activations(s1, 1, k1)
+    b1 = workloads.weight_bytes_per_call(name1)
+    t1, r1 = cpu_time(lambda: oracle.baseline_packed_matmul(f1, w1, n1, k1, x1, threads), budget / 4, 10)
+    t1s, _ = cpu_time(lambda: oracle.baseline_packed_matmul(f1, w1, n1, k1, x1, 1), budget / 8, 3, 100)
+    dense_w = oracle.dequantize(f1, w1, n1, k1)
+    td, rd = cpu_time(lambda: oracle.matmul_dense(x1, dense_w, False, True), budget / 4, 2, 20)
+    legs["config1_q4k_1x4096x4096"] = {
+        "ms_per_call": round(t1 * 1e3, 4), "GBps": round(b1 / t1 / 1e9, 2), "threads": threads,
+        "single_thread_ms": round(t1s * 1e3, 4), "dense_f32_oracle_ms": round(td * 1e3, 2),
+        "sample": f"{r1} timed calls (AVX2 port), {rd} dense-oracle calls (1 thread, f32 W of 64 MiB)"}
+    log(f"cpu baseline, config 1: {t1 * 1e3:.3f} ms/call ({b1 / t1 / 1e9:.2f} GB/s) at {threads} threads, "
+        f"{t1s * 1e3:.3f} ms at 1; dense f32 oracle {td * 1e3:.1f} ms")
+
+    # config 3: the prefill GEMM x[512,4096] . W[14336,4096]^T on the CPU path
+    name3 = "q4k_14336x4096_s2"
+    f3, n3, k3, s3, _ = workloads.WEIGHTS[name3]
+    w3 = workloads.weight_bytes(name3)
+    x3 = workloads.activations(s3, 512, k3)
+    t3, r3 = cpu_time(lambda: oracle.baseline_packed_matmul(f3, w3, n3, k3, x3, threads), budget, 2, 10)
+    flops3 = 2.0 * 512 * n3 * k3
+    leg3 = {"ms_per_call": round(t3 * 1e3, 2), "TOPs": round(flops3 / t3 / 1e12, 3), "threads": threads,
+            "sample": f"the full M=512 call, 1 warm-up + {r3} timed calls"}
+    if gemm:
+        leg3["gpu_over_cpu"] = round(t3 / (gemm["roofline"]["kernel_us"] * 1e-6), 1)
+    legs["config3_q4k_512x14336x4096"] = leg3
+    log(f"cpu baseline, config 3 (M=512): {t3 * 1e3:.1f} ms/call, {flops3 / t3 / 1e12:.3f} TOP/s")
+
+    # config 4: IQ4_XS x[1,14336] . W[4096,14336]^T
+    name4 = "iq4xs_4096x14336_s3"
+    f4, n4, k4, s4, _ = workloads.WEIGHTS[name4]
+    w4 = workloads.weight_bytes(name4)
+    x4 = workloads.activations(s4, 1, k4)
+    b4 = workloads.weight_bytes_per_call(name4)
+    t4, r4 = cpu_time(lambda: oracle.baseline_packed_matmul(f4, w4, n4, k4, x4, threads), budget / 2, 10)
+    leg4 = {"ms_per_call": round(t4 * 1e3, 4), "GBps": round(b4 / t4 / 1e9, 2), "threads": threads,
+            "sample": f"1 warm-up + {r4} timed calls"}
+    if "iq4xs_gemv_kernel_us" in extra:
+        leg4["gpu_over_cpu"] = round(t4 / (extra["iq4xs_gemv_kernel_us"] * 1e-6), 1)
+    legs["config4_iq4xs_1x14336x4096"] = leg4
+    log(f"cpu baseline, config 4 (IQ4_XS): {t4 * 1e3:.3f} ms/call, {b4 / t4 / 1e9:.2f} GB/s")
+    cpu["legs"] = legs
     return cpu
 
 

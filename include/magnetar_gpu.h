@@ -77,8 +77,8 @@ const char *mq_last_error(mq_ctx *ctx);
  * `IQ3S_GRID` 512 u32 entries of 4), synchronously; every context on the
  * device shares them. The reference reads these statics from the external
  * magnetar-provider-api crate (src/native/quant.rs:14, 1057-1061): a Rust
- * binding passes them once at start-up. Waits for this context's queued
- * work first; work queued on other streams must not be running. When every
+ * binding passes them once at start-up. Waits for all work queued on the
+ * device first (every context and stream shares the tables). When every
  * table byte is below 128 (true of the GGUF grids), prefill matmuls of the
  * grid formats run on the MFMA GEMM; otherwise as 8-row decode GEMVs, and
  * mq_matmul_f16_dev declines them. */
@@ -307,6 +307,30 @@ typedef struct {
  * staging, return MQ_DECLINED. */
 int mq_decode_matmul_dev(mq_ctx *ctx, uint64_t handle, const float *x_dev, uint64_t k,
                          const mq_decode_fusion *fusion, float *y_dev, void *stream);
+
+/* ---- Launch-shape query --------------------------------------------------------
+ * No counterpart in the reference (its pool has no launch shape): the launch
+ * the pre-quantized int8 decode GEMV (mq_matmul_prequantized_dev) takes for
+ * a Q4_K or IQ4_XS weight, computed on the host without a device, for tests
+ * and tuning. waves (waves per work-group, < 1: the default), variant (0:
+ * the default; 1, 2, 3: the MQ_GEMV_VARIANT forms) and ksplit (< 1: the
+ * default K split) are the overrides a context reads from MQ_GEMV_SPLITS,
+ * MQ_GEMV_VARIANT and MQ_GEMV_KSPLIT; every form clamps waves to its
+ * kernel's launch bound (8 waves, 512 threads). */
+#define MQ_GEMV_FORM_LANES8 1u /* 8 lanes per row */
+#define MQ_GEMV_FORM_ROWS 2u   /* one row per lane, scalar activation reads (m <= 4) */
+#define MQ_GEMV_FORM_LDS 3u    /* 64 rows per work-group, activations in LDS, split-K over grid_y */
+#define MQ_GEMV_FORM_NARROW 4u /* 16 rows per work-group, activations in LDS */
+
+typedef struct {
+  uint32_t form;
+  uint32_t waves;  /* work-group = 64 * waves threads */
+  uint32_t grid_x, grid_y;
+  uint64_t lds_bytes;  /* dynamic LDS per work-group */
+} mq_gemv_shape;
+
+int mq_gemv_launch_shape(uint32_t gguf_type, uint64_t stored_rows, uint64_t stored_cols, uint64_t m,
+                         int waves, int variant, int ksplit, mq_gemv_shape *out);
 
 /* Library version string. */
 const char *mq_version(void);

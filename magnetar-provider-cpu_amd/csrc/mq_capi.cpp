@@ -9,6 +9,8 @@
 #include <cstdlib>
 #include <cstring>
 #include <map>
+#include <new>
+#include <stdexcept>
 #include <mutex>
 #include <set>
 #include <vector>
@@ -96,6 +98,33 @@ int hip_fail(mq_ctx* ctx, hipError_t e, const char* where) {
     hipError_t e_ = (call);                               \
     if (e_ != hipSuccess) return hip_fail(ctx, e_, #call); \
   } while (0)
+
+// Records an error without letting a second exception escape (a failure
+// to record the text still returns the code).
+int fail_quietly(mq_ctx* ctx, int code, const char* what) noexcept {
+  try {
+    return fail(ctx, code, what);
+  } catch (...) {
+    return code;
+  }
+}
+
+// The handlers of every entry point's function-try-block: nothing thrown
+// inside the library (a host allocation sized by the caller, a container
+// insert) crosses the C ABI.
+#define MQ_CATCH(ctx)                                                                         \
+  catch (const std::bad_alloc&) {                                                             \
+    return fail_quietly(ctx, MQ_ERR_OOM, "out of host memory");                               \
+  }                                                                                           \
+  catch (const std::length_error&) {                                                          \
+    return fail_quietly(ctx, MQ_ERR_OOM, "a host buffer of that size cannot be allocated");   \
+  }                                                                                           \
+  catch (const std::exception& e_) {                                                          \
+    return fail_quietly(ctx, MQ_ERR_ARGUMENT, e_.what());                                     \
+  }                                                                                           \
+  catch (...) {                                                                               \
+    return fail_quietly(ctx, MQ_ERR_ARGUMENT, "unexpected exception");                        \
+  }
 
 bool known_type(uint32_t type) {
   return type == MQ_TYPE_Q4_K || type == MQ_TYPE_IQ4_XS || mq::is_plane_format(static_cast<int>(type)) ||
@@ -437,7 +466,7 @@ extern "C" {
 
 const char* mq_version(void) { return "magnetar_gpu 0.1.0 (gfx950)"; }
 
-int mq_create(int device, mq_ctx** out) {
+int mq_create(int device, mq_ctx** out) try {
   if (!out) return fail(nullptr, MQ_ERR_ARGUMENT, "mq_create: null out pointer");
   *out = nullptr;
   int count = 0;
@@ -463,7 +492,7 @@ int mq_create(int device, mq_ctx** out) {
   if (const char* s = std::getenv("MQ_GEMM_VARIANT")) ctx->gemm_variant = std::atoi(s);
   *out = ctx;
   return MQ_OK;
-}
+} MQ_CATCH(nullptr)
 
 void mq_destroy(mq_ctx* ctx) {
   if (!ctx) return;
@@ -484,11 +513,15 @@ void mq_destroy(mq_ctx* ctx) {
 const char* mq_last_error(mq_ctx* ctx) {
   if (!ctx) return g_create_error.c_str();
   std::lock_guard<std::mutex> lock(ctx->err_mu);
-  return ctx->errors[std::this_thread::get_id()].c_str();
+  try {
+    return ctx->errors[std::this_thread::get_id()].c_str();
+  } catch (...) {
+    return "out of host memory";
+  }
 }
 
 int mq_set_iq_grids(mq_ctx* ctx, const uint64_t* iq2xxs, const uint64_t* iq2xs, const uint64_t* iq2s,
-                    const uint32_t* iq3xxs, const uint32_t* iq3s) {
+                    const uint32_t* iq3xxs, const uint32_t* iq3s) try {
   if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_set_iq_grids: null context");
   if (!iq2xxs || !iq2xs || !iq2s || !iq3xxs || !iq3s) return fail(ctx, MQ_ERR_ARGUMENT, "mq_set_iq_grids: null table");
   std::vector<uint8_t> tables(mq::kGridTableBytes);
@@ -499,8 +532,9 @@ int mq_set_iq_grids(mq_ctx* ctx, const uint64_t* iq2xxs, const uint64_t* iq2xs, 
   std::memcpy(tables.data() + mq::kGridIq3S, iq3s, 512 * sizeof(uint32_t));
   std::lock_guard<std::mutex> lock(ctx->mu);
   DeviceGuard guard(ctx->device);
-  // queued work of this context may still read the previous tables
-  MQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  // every context's work on the device (any stream) may still read the
+  // previous tables: the device copy is shared
+  MQ_HIP(ctx, hipDeviceSynchronize());
   MQ_HIP(ctx, mq::grid_tables_upload(tables.data(), ctx->stream));
   bool small = true;
   for (uint8_t b : tables) small = small && b < 128;
@@ -511,10 +545,10 @@ int mq_set_iq_grids(mq_ctx* ctx, const uint64_t* iq2xxs, const uint64_t* iq2xs, 
   else
     g_grid_gemm_devices.erase(ctx->device);
   return MQ_OK;
-}
+} MQ_CATCH(ctx)
 
 int mq_weight_upload(mq_ctx* ctx, uint32_t gguf_type, uint64_t stored_rows, uint64_t stored_cols, int transposed,
-                     const uint8_t* bytes, size_t len, uint64_t* handle) {
+                     const uint8_t* bytes, size_t len, uint64_t* handle) try {
   if (!ctx || !handle) return fail(ctx, MQ_ERR_ARGUMENT, "mq_weight_upload: null argument");
   *handle = 0;
   if (!known_type(gguf_type))
@@ -583,9 +617,31 @@ int mq_weight_upload(mq_ctx* ctx, uint32_t gguf_type, uint64_t stored_rows, uint
   *handle = ctx->next_handle++;
   ctx->weights.emplace(*handle, w);
   return MQ_OK;
-}
+} MQ_CATCH(ctx)
 
-int mq_weight_release(mq_ctx* ctx, uint64_t handle) {
+int mq_gemv_launch_shape(uint32_t gguf_type, uint64_t stored_rows, uint64_t stored_cols, uint64_t m, int waves,
+                         int variant, int ksplit, mq_gemv_shape* out) try {
+  if (!out) return fail(nullptr, MQ_ERR_ARGUMENT, "mq_gemv_launch_shape: null out pointer");
+  if (gguf_type != MQ_TYPE_Q4_K && gguf_type != MQ_TYPE_IQ4_XS)
+    return fail(nullptr, MQ_DECLINED, "mq_gemv_launch_shape: Q4_K and IQ4_XS only");
+  if (stored_rows == 0 || stored_cols == 0 || stored_cols % 256 || m < 1 || m > 8 || variant < 0 || variant > 3)
+    return fail(nullptr, MQ_ERR_SHAPE, "mq_gemv_launch_shape: no decode GEMV of this shape");
+  const uint64_t nb = stored_cols / 256;
+  mq::GemvSplitK sk;
+  sk.ks = ksplit > 0 ? ksplit : mq::gemv_default_ksplit(stored_rows, nb);
+  if (sk.ks > 16) sk.ks = 16;  // the context's bounds (acquire_splitk)
+  if (static_cast<uint64_t>(sk.ks) > nb) sk.ks = static_cast<int>(nb);
+  const mq::GemvShape g =
+      mq::gemv_int8_shape(static_cast<int>(gguf_type), stored_rows, nb, m, waves, variant, sk);
+  out->form = static_cast<uint32_t>(g.form);
+  out->waves = static_cast<uint32_t>(g.waves);
+  out->grid_x = g.grid_x;
+  out->grid_y = g.grid_y;
+  out->lds_bytes = g.lds;
+  return MQ_OK;
+} MQ_CATCH(nullptr)
+
+int mq_weight_release(mq_ctx* ctx, uint64_t handle) try {
   if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_weight_release: null context");
   std::lock_guard<std::mutex> lock(ctx->mu);
   auto it = ctx->weights.find(handle);
@@ -596,10 +652,10 @@ int mq_weight_release(mq_ctx* ctx, uint64_t handle) {
   MQ_HIP(ctx, hipFree(it->second.dev));
   ctx->weights.erase(it);
   return MQ_OK;
-}
+} MQ_CATCH(ctx)
 
 int mq_weight_info(mq_ctx* ctx, uint64_t handle, uint32_t* gguf_type, uint64_t* stored_rows, uint64_t* stored_cols,
-                   int* transposed, uint64_t* device_bytes) {
+                   int* transposed, uint64_t* device_bytes) try {
   if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_weight_info: null context");
   std::lock_guard<std::mutex> lock(ctx->mu);
   const Weight* w = find_weight(ctx, handle);
@@ -610,10 +666,10 @@ int mq_weight_info(mq_ctx* ctx, uint64_t handle, uint32_t* gguf_type, uint64_t* 
   if (transposed) *transposed = w->transposed;
   if (device_bytes) *device_bytes = w->dev_bytes;
   return MQ_OK;
-}
+} MQ_CATCH(ctx)
 
 int mq_matmul_dev(mq_ctx* ctx, uint64_t handle, const float* x_dev, uint64_t m, uint64_t k, uint32_t flags,
-                  float* y_dev, void* stream) {
+                  float* y_dev, void* stream) try {
   if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_matmul_dev: null context");
   std::lock_guard<std::mutex> lock(ctx->mu);
   const Weight* w = find_weight(ctx, handle);
@@ -621,7 +677,7 @@ int mq_matmul_dev(mq_ctx* ctx, uint64_t handle, const float* x_dev, uint64_t m, 
   DeviceGuard guard(ctx->device);
   hipStream_t s = static_cast<hipStream_t>(stream);
   return matmul_locked(ctx, *w, x_dev, m, k, flags, y_dev, s);
-}
+} MQ_CATCH(ctx)
 
 namespace {
 
@@ -664,17 +720,17 @@ int matmul_host_locked(mq_ctx* ctx, const Weight& w, const float* x, uint64_t m,
 
 }  // namespace
 
-int mq_matmul(mq_ctx* ctx, uint64_t handle, const float* x, uint64_t m, uint64_t k, uint32_t flags, float* y) {
+int mq_matmul(mq_ctx* ctx, uint64_t handle, const float* x, uint64_t m, uint64_t k, uint32_t flags, float* y) try {
   if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_matmul: null context");
   std::lock_guard<std::mutex> lock(ctx->mu);
   const Weight* w = find_weight(ctx, handle);
   if (!w) return fail(ctx, MQ_ERR_ARGUMENT, "unknown weight handle " + std::to_string(handle));
   DeviceGuard guard(ctx->device);
   return matmul_host_locked(ctx, *w, x, m, k, flags, nullptr, 0, y);
-}
+} MQ_CATCH(ctx)
 
 int mq_matmul_add(mq_ctx* ctx, uint64_t handle, const float* x, uint64_t m, uint64_t k, uint32_t flags,
-                  const float* addend, uint64_t addend_rows, float* y) {
+                  const float* addend, uint64_t addend_rows, float* y) try {
   if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_matmul_add: null context");
   if (!addend) return fail(ctx, MQ_ERR_ARGUMENT, "mq_matmul_add: null addend");
   std::lock_guard<std::mutex> lock(ctx->mu);
@@ -682,10 +738,10 @@ int mq_matmul_add(mq_ctx* ctx, uint64_t handle, const float* x, uint64_t m, uint
   if (!w) return fail(ctx, MQ_ERR_ARGUMENT, "unknown weight handle " + std::to_string(handle));
   DeviceGuard guard(ctx->device);
   return matmul_host_locked(ctx, *w, x, m, k, flags, addend, addend_rows, y);
-}
+} MQ_CATCH(ctx)
 
 int mq_matmul_add_dev(mq_ctx* ctx, uint64_t handle, const float* x_dev, uint64_t m, uint64_t k, uint32_t flags,
-                      const float* addend_dev, uint64_t addend_rows, float* y_dev, void* stream) {
+                      const float* addend_dev, uint64_t addend_rows, float* y_dev, void* stream) try {
   if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_matmul_add_dev: null context");
   if (!addend_dev) return fail(ctx, MQ_ERR_ARGUMENT, "mq_matmul_add_dev: null addend");
   std::lock_guard<std::mutex> lock(ctx->mu);
@@ -693,10 +749,10 @@ int mq_matmul_add_dev(mq_ctx* ctx, uint64_t handle, const float* x_dev, uint64_t
   if (!w) return fail(ctx, MQ_ERR_ARGUMENT, "unknown weight handle " + std::to_string(handle));
   DeviceGuard guard(ctx->device);
   return matmul_locked(ctx, *w, x_dev, m, k, flags, y_dev, static_cast<hipStream_t>(stream), addend_dev, addend_rows);
-}
+} MQ_CATCH(ctx)
 
 int mq_quantize_activations_dev(mq_ctx* ctx, const float* x_dev, uint64_t m, uint64_t k, int8_t* values_dev,
-                                float* scales_dev, int32_t* sums_dev, void* stream) {
+                                float* scales_dev, int32_t* sums_dev, void* stream) try {
   if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_quantize_activations_dev: null context");
   if (k % 32 != 0) return fail(ctx, MQ_ERR_SHAPE, "activation rows must hold whole 32-value blocks");
   if (m == 0) return MQ_OK;
@@ -707,10 +763,10 @@ int mq_quantize_activations_dev(mq_ctx* ctx, const float* x_dev, uint64_t m, uin
   mq::launch_quantize_activations(x_dev, m, k, values_dev, scales_dev, sums_dev, nullptr, 1, s);
   MQ_HIP(ctx, hipGetLastError());
   return MQ_OK;
-}
+} MQ_CATCH(ctx)
 
 int mq_matmul_prequantized_dev(mq_ctx* ctx, uint64_t handle, const int8_t* values_dev, const float* scales_dev,
-                               const int32_t* sums_dev, uint64_t m, uint64_t k, float* y_dev, void* stream) {
+                               const int32_t* sums_dev, uint64_t m, uint64_t k, float* y_dev, void* stream) try {
   if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_matmul_prequantized_dev: null context");
   std::lock_guard<std::mutex> lock(ctx->mu);
   const Weight* w = find_weight(ctx, handle);
@@ -741,10 +797,10 @@ int mq_matmul_prequantized_dev(mq_ctx* ctx, uint64_t handle, const int8_t* value
                          y_dev, nullptr, 0, ctx->gemv_splits_override, ctx->gemv_variant, sk, s);
   MQ_HIP(ctx, hipGetLastError());
   return MQ_OK;
-}
+} MQ_CATCH(ctx)
 
 int mq_prepare_activations_f16_dev(mq_ctx* ctx, const float* x_dev, uint64_t m, uint64_t k, uint32_t flags,
-                                   uint16_t* a16_dev, void* stream) {
+                                   uint16_t* a16_dev, void* stream) try {
   if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_prepare_activations_f16_dev: null context");
   if (flags & ~MQ_INT8_ACTIVATIONS) return fail(ctx, MQ_ERR_ARGUMENT, "unknown flag bits");
   if (k % 32 != 0) return fail(ctx, MQ_ERR_SHAPE, "activation rows must hold whole 32-value blocks");
@@ -758,10 +814,10 @@ int mq_prepare_activations_f16_dev(mq_ctx* ctx, const float* x_dev, uint64_t m, 
     mq::launch_activations_f16(x_dev, m, k, a16_dev, s);
   MQ_HIP(ctx, hipGetLastError());
   return MQ_OK;
-}
+} MQ_CATCH(ctx)
 
 int mq_matmul_f16_dev(mq_ctx* ctx, uint64_t handle, const uint16_t* a16_dev, uint64_t m, uint64_t k, float* y_dev,
-                      void* stream) {
+                      void* stream) try {
   if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_matmul_f16_dev: null context");
   std::lock_guard<std::mutex> lock(ctx->mu);
   const Weight* w = find_weight(ctx, handle);
@@ -785,9 +841,9 @@ int mq_matmul_f16_dev(mq_ctx* ctx, uint64_t handle, const uint16_t* a16_dev, uin
                   ctx->gemm_variant, s, part);
   MQ_HIP(ctx, hipGetLastError());
   return MQ_OK;
-}
+} MQ_CATCH(ctx)
 
-int mq_dequantize_dev(mq_ctx* ctx, uint64_t handle, int logical, float* out_dev, void* stream) {
+int mq_dequantize_dev(mq_ctx* ctx, uint64_t handle, int logical, float* out_dev, void* stream) try {
   if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_dequantize_dev: null context");
   std::lock_guard<std::mutex> lock(ctx->mu);
   const Weight* w = find_weight(ctx, handle);
@@ -803,9 +859,9 @@ int mq_dequantize_dev(mq_ctx* ctx, uint64_t handle, int logical, float* out_dev,
     mq::launch_dequantize(static_cast<int>(w->type), w->dev, w->rows, w->nb, logical, out_dev, s);
   MQ_HIP(ctx, hipGetLastError());
   return MQ_OK;
-}
+} MQ_CATCH(ctx)
 
-int mq_dequantize(mq_ctx* ctx, uint64_t handle, int logical, float* out) {
+int mq_dequantize(mq_ctx* ctx, uint64_t handle, int logical, float* out) try {
   if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_dequantize: null context");
   std::lock_guard<std::mutex> lock(ctx->mu);
   const Weight* w = find_weight(ctx, handle);
@@ -828,13 +884,13 @@ int mq_dequantize(mq_ctx* ctx, uint64_t handle, int logical, float* out) {
   (void)hipFree(dev);
   if (e != hipSuccess) return hip_fail(ctx, e, "mq_dequantize");
   return MQ_OK;
-}
+} MQ_CATCH(ctx)
 
 
 // ---- decode-step fusions ----------------------------------------------------------
 
 int mq_decode_matmul_dev(mq_ctx* ctx, uint64_t handle, const float* x_dev, uint64_t k, const mq_decode_fusion* f,
-                         float* y_dev, void* stream) {
+                         float* y_dev, void* stream) try {
   if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_decode_matmul_dev: null context");
   if (!f || !x_dev) return fail(ctx, MQ_ERR_ARGUMENT, "mq_decode_matmul_dev: null argument");
   std::lock_guard<std::mutex> lock(ctx->mu);
@@ -845,8 +901,9 @@ int mq_decode_matmul_dev(mq_ctx* ctx, uint64_t handle, const float* x_dev, uint6
   if (rc) return rc;
   if (plane_type(w->type) || grid_type(w->type))
     return fail(ctx, MQ_DECLINED, "decode-step fusions cover Q4_K and IQ4_XS weights");
-  if (f->norm_weight && !(f->norm_epsilon > 0.0f))
-    return fail(ctx, MQ_ERR_SHAPE, "rmsnorm epsilon must be positive");
+  // the reference's test (src/lib.rs:388): a NaN epsilon passes and gives NaN
+  if (f->norm_weight && f->norm_epsilon <= 0.0f)
+    return fail(ctx, MQ_ERR_SHAPE, "RMSNorm epsilon must be positive");
   mq::GemvFusion fu;
   fu.norm_w = f->norm_weight;
   fu.norm_eps = f->norm_epsilon;
@@ -893,12 +950,12 @@ int mq_decode_matmul_dev(mq_ctx* ctx, uint64_t handle, const float* x_dev, uint6
     return fail(ctx, MQ_DECLINED, "the row does not fit the fused decode GEMV's LDS staging");
   MQ_HIP(ctx, hipGetLastError());
   return MQ_OK;
-}
+} MQ_CATCH(ctx)
 
 // ---- embedding lookup ------------------------------------------------------------
 
 int mq_embedding_dev(mq_ctx* ctx, uint64_t handle, const float* ids, uint64_t count, float scale, float* out_dev,
-                     void* stream) {
+                     void* stream) try {
   if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_embedding_dev: null context");
   std::lock_guard<std::mutex> lock(ctx->mu);
   const Weight* w = find_weight(ctx, handle);
@@ -915,9 +972,9 @@ int mq_embedding_dev(mq_ctx* ctx, uint64_t handle, const float* ids, uint64_t co
                        std::isnan(scale) ? 0 : 1, out_dev, s);
   MQ_HIP(ctx, hipGetLastError());
   return MQ_OK;
-}
+} MQ_CATCH(ctx)
 
-int mq_embedding(mq_ctx* ctx, uint64_t handle, const float* ids, uint64_t count, float scale, float* out) {
+int mq_embedding(mq_ctx* ctx, uint64_t handle, const float* ids, uint64_t count, float scale, float* out) try {
   if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_embedding: null context");
   std::lock_guard<std::mutex> lock(ctx->mu);
   const Weight* w = find_weight(ctx, handle);
@@ -939,15 +996,16 @@ int mq_embedding(mq_ctx* ctx, uint64_t handle, const float* ids, uint64_t count,
   MQ_HIP(ctx, hipMemcpyAsync(out, dev, bytes, hipMemcpyDeviceToHost, ctx->stream));
   MQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
   return MQ_OK;
-}
+} MQ_CATCH(ctx)
 
 // ---- decoder-layer operators ----------------------------------------------------
 
 int mq_rmsnorm_dev(mq_ctx* ctx, const float* x_dev, uint64_t rows, uint64_t cols, const float* w_dev,
-                   uint64_t w_rows, float epsilon, float* out_dev, void* stream) {
+                   uint64_t w_rows, float epsilon, float* out_dev, void* stream) try {
   if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_rmsnorm_dev: null context");
   if (cols == 0) return fail(ctx, MQ_ERR_SHAPE, "RMSNorm hidden dimension must be non-zero");
-  if (!(epsilon > 0.0f)) return fail(ctx, MQ_ERR_SHAPE, "RMSNorm epsilon must be positive");
+  // the reference's test (src/lib.rs:388): a NaN epsilon passes and gives NaN
+  if (epsilon <= 0.0f) return fail(ctx, MQ_ERR_SHAPE, "RMSNorm epsilon must be positive");
   if (w_rows != 1 && w_rows != rows)
     return fail(ctx, MQ_ERR_SHAPE, "RMSNorm weight shape must be [" + std::to_string(cols) + "] or [" +
                                        std::to_string(rows) + ", " + std::to_string(cols) + "]");
@@ -958,11 +1016,11 @@ int mq_rmsnorm_dev(mq_ctx* ctx, const float* x_dev, uint64_t rows, uint64_t cols
                      static_cast<hipStream_t>(stream));
   MQ_HIP(ctx, hipGetLastError());
   return MQ_OK;
-}
+} MQ_CATCH(ctx)
 
 int mq_rope_dev(mq_ctx* ctx, const float* x_dev, uint64_t rows, uint64_t cols, float base, float scale,
                 uint64_t dimension, uint64_t position_offset, uint64_t head_count, int pairing, float* out_dev,
-                void* stream) {
+                void* stream) try {
   if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_rope_dev: null context");
   if (head_count == 0 || cols % head_count)
     return fail(ctx, MQ_ERR_SHAPE, "RoPE head_count " + std::to_string(head_count) +
@@ -988,10 +1046,10 @@ int mq_rope_dev(mq_ctx* ctx, const float* x_dev, uint64_t rows, uint64_t cols, f
                   static_cast<hipStream_t>(stream));
   MQ_HIP(ctx, hipGetLastError());
   return MQ_OK;
-}
+} MQ_CATCH(ctx)
 
 int mq_kv_write_dev(mq_ctx* ctx, float* store_dev, uint64_t capacity, uint64_t width, const float* rows_dev,
-                    uint64_t count, uint64_t row_offset, void* stream) {
+                    uint64_t count, uint64_t row_offset, void* stream) try {
   if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_kv_write_dev: null context");
   if (row_offset + count < row_offset || row_offset + count > capacity)
     return fail(ctx, MQ_ERR_SHAPE, "kv-write of " + std::to_string(count) + " rows at " +
@@ -1006,11 +1064,11 @@ int mq_kv_write_dev(mq_ctx* ctx, float* store_dev, uint64_t capacity, uint64_t w
   mq::launch_copy(rows_dev, count * width, dst, static_cast<hipStream_t>(stream));
   MQ_HIP(ctx, hipGetLastError());
   return MQ_OK;
-}
+} MQ_CATCH(ctx)
 
 int mq_attention_dev(mq_ctx* ctx, const float* q_dev, uint64_t seq, const float* k_dev, const float* v_dev,
                      uint64_t kv_rows, uint64_t key_count, uint64_t heads, uint64_t head_dim, uint64_t kv_heads,
-                     int causal, float score_scale, float* out_dev, void* stream) {
+                     int causal, float score_scale, float* out_dev, void* stream) try {
   if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_attention_dev: null context");
   if (heads == 0 || head_dim == 0 || kv_heads == 0)
     return fail(ctx, MQ_ERR_SHAPE, "head_count, kv_head_count, and head_dimension must all be positive");
@@ -1051,10 +1109,10 @@ int mq_attention_dev(mq_ctx* ctx, const float* q_dev, uint64_t seq, const float*
     return fail(ctx, MQ_DECLINED, "attention shape has no GPU path");
   MQ_HIP(ctx, hipGetLastError());
   return MQ_OK;
-}
+} MQ_CATCH(ctx)
 
 int mq_silu_mul_dev(mq_ctx* ctx, const float* gate_dev, const float* up_dev, uint64_t n, float* out_dev,
-                    void* stream) {
+                    void* stream) try {
   if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_silu_mul_dev: null context");
   if (n == 0) return MQ_OK;
   if (!gate_dev || !up_dev || !out_dev) return fail(ctx, MQ_ERR_ARGUMENT, "mq_silu_mul_dev: null pointer");
@@ -1062,10 +1120,10 @@ int mq_silu_mul_dev(mq_ctx* ctx, const float* gate_dev, const float* up_dev, uin
   mq::launch_silu_mul(gate_dev, up_dev, n, out_dev, static_cast<hipStream_t>(stream));
   MQ_HIP(ctx, hipGetLastError());
   return MQ_OK;
-}
+} MQ_CATCH(ctx)
 
 int mq_add_dev(mq_ctx* ctx, const float* a_dev, uint64_t n, const float* b_dev, uint64_t b_n, float* out_dev,
-               void* stream) {
+               void* stream) try {
   if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_add_dev: null context");
   if (b_n == 0 || n % b_n) return fail(ctx, MQ_ERR_SHAPE, "add: b must match a or be one row of a");
   if (n == 0) return MQ_OK;
@@ -1074,6 +1132,6 @@ int mq_add_dev(mq_ctx* ctx, const float* a_dev, uint64_t n, const float* b_dev, 
   mq::launch_add(a_dev, n, b_dev, b_n, out_dev, static_cast<hipStream_t>(stream));
   MQ_HIP(ctx, hipGetLastError());
   return MQ_OK;
-}
+} MQ_CATCH(ctx)
 
 }  // extern "C"

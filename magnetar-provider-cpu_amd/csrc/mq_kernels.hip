@@ -703,11 +703,19 @@ __device__ inline void splitk_finish(float (&acc)[M], float (&mins)[M], uint64_t
     __hip_atomic_store(&partials[((ks * M + m) * 2 + 1) * rows64 + row], mins[m], __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
   }
+  // The relaxed stores, the wait and the relaxed ticket are ordered for the
+  // hardware by the wait alone; the signal fences keep the compiler from
+  // moving any of these memory operations across it (a fence of no scope
+  // beyond the thread emits no instruction).
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
   uint32_t ticket = 0;
   if (lane == 0) ticket = __hip_atomic_fetch_add(&counters[rb], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   ticket = __shfl(ticket, 0);
   if (ticket != static_cast<uint32_t>(KS - 1)) return;
+  // the partial loads below stay after the ticket that admits them
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
   const bool valid = row < rows;
   float v[M];
 #pragma unroll
@@ -4092,25 +4100,60 @@ bool lds_form_shape(int type, uint64_t rows, uint64_t nb, uint64_t m, int splits
 
 }  // namespace
 
-void launch_gemv_int8(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, const int8_t* values,
-                      const float* scales, const int32_t* sums, uint64_t m, float* y, const float* addend,
-                      uint64_t addend_stride, int splits, int variant, const GemvSplitK& sk,
-                      hipStream_t stream) {
-  const int inb = static_cast<int>(nb);
-  // Waves per work-group never exceed what each kernel is built for.
+GemvShape gemv_int8_shape(int type, uint64_t rows, uint64_t nb, uint64_t m, int splits, int variant,
+                          const GemvSplitK& sk) {
+  GemvShape g;
   int lds_splits = 0;
   size_t lds = 0;
   const bool lds_fits = lds_form_shape(type, rows, nb, m, splits, sk.ks, lds_splits, lds);
   if (variant == 0) variant = lds_fits ? 3 : (m <= 4 ? 2 : 1);
   if (variant == 3 && lds_fits) {
+    size_t narrow_lds = 0;
+    if (narrow_form(type, rows, nb, m, false, sk, narrow_lds)) {
+      g.form = kGemvFormNarrow;
+      g.waves = 8;
+      g.grid_x = static_cast<unsigned>((rows + kNarrowRows - 1) / kNarrowRows);
+      g.lds = narrow_lds;
+      return g;
+    }
+    g.form = kGemvFormLds;
+    g.waves = lds_splits;
+    g.grid_x = static_cast<unsigned>((rows + 63) / 64);
+    g.grid_y = static_cast<unsigned>(sk.ks);
+    g.lds = lds;
+    return g;
+  }
+  // Waves per work-group never exceed what each kernel is built for: the
+  // other forms have launch bound 512 and 8 reduction slots.
+  if (splits < 1) splits = gemv_default_splits(rows, nb, m, variant);
+  g.waves = splits > 8 ? 8 : splits;
+  if (variant >= 2 && m <= 4) {
+    g.form = kGemvFormRows;
+    g.grid_x = static_cast<unsigned>((rows + 63) / 64);
+  } else {
+    g.form = kGemvFormLanes8;
+    g.grid_x = static_cast<unsigned>((rows + 7) / 8);
+  }
+  return g;
+}
+
+void launch_gemv_int8(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, const int8_t* values,
+                      const float* scales, const int32_t* sums, uint64_t m, float* y, const float* addend,
+                      uint64_t addend_stride, int splits, int variant, const GemvSplitK& sk,
+                      hipStream_t stream) {
+  const int inb = static_cast<int>(nb);
+  const GemvShape g = gemv_int8_shape(type, rows, nb, m, splits, variant, sk);
+  if (g.form == kGemvFormLds || g.form == kGemvFormNarrow) {
+    int lds_splits = 0;
+    size_t lds = 0;
+    lds_form_shape(type, rows, nb, m, splits, sk.ks, lds_splits, lds);
     launch_gemv_lds<false>(type, tiled, rows, nb, values, scales, sums, nullptr, m, y, addend, addend_stride,
                            lds_splits, sk, lds, stream);
     return;
   }
-  if (splits < 1) splits = gemv_default_splits(rows, nb, m, variant);
-  splits = splits > 8 ? 8 : splits;  // the other forms: launch bound 512, 8 reduction slots
-  if (variant >= 2 && m <= 4) {
-    dim3 grid(static_cast<unsigned>((rows + 63) / 64)), block(64 * splits);
+  splits = g.waves;
+  if (g.form == kGemvFormRows) {
+    dim3 grid(g.grid_x), block(64 * splits);
     if (type == kTypeQ4K) {
       switch (m) {
 #define X(MM)                                                                                            \

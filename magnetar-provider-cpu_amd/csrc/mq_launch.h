@@ -44,6 +44,21 @@ int gemv_default_ksplit(uint64_t rows, uint64_t nb);
 // The matmul kernels write y[i][n] = product [+ addend[i * addend_stride + n]]
 // (addend may be null; stride 0 broadcasts one row, as a bias).
 
+// The launch the pre-quantized int8 decode GEMV takes: its form, waves per
+// work-group (clamped to the form's launch bound), grid and dynamic LDS.
+constexpr int kGemvFormLanes8 = 1;  // variant 1: 8 lanes per row
+constexpr int kGemvFormRows = 2;    // variant 2: one row per lane, scalar activations
+constexpr int kGemvFormLds = 3;     // variant 3: 64 rows per work-group, activations in LDS, split-K
+constexpr int kGemvFormNarrow = 4;  // variant 3's 16-row form (long rows, few output rows)
+struct GemvShape {
+  int form = 0;
+  int waves = 0;
+  unsigned grid_x = 0, grid_y = 1;
+  size_t lds = 0;
+};
+GemvShape gemv_int8_shape(int type, uint64_t rows, uint64_t nb, uint64_t m, int splits, int variant,
+                          const GemvSplitK& sk);
+
 // Decode GEMV, m in 1..8, int8 activations. variant 1: 8 lanes per row
 // (any m); variant 2: one row per lane, activations through scalar loads
 // (m <= 4); 3: row per lane with the activations staged in LDS (m <= 8,

@@ -17,6 +17,7 @@ PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 GPU_LIB = os.path.join(PKG_DIR, "libmagnetar_gpu.so")
 GGUF_LIB = os.path.join(PKG_DIR, "libmagnetar_gguf.so")
 EXECUTOR_LIB = os.path.join(PKG_DIR, "libmagnetar_executor.so")
+PROBE_LIB = os.path.join(PKG_DIR, "libmagnetar_probe.so")
 
 Q4_0 = 2
 Q8_0 = 8
@@ -57,6 +58,15 @@ EPILOGUE_ROPE_KV = 1
 EPILOGUE_SILU_PAIRS = 2
 
 
+class GemvShape(ctypes.Structure):
+    """mq_gemv_shape (include/magnetar_gpu.h)."""
+    _fields_ = [("form", ctypes.c_uint32), ("waves", ctypes.c_uint32), ("grid_x", ctypes.c_uint32),
+                ("grid_y", ctypes.c_uint32), ("lds_bytes", ctypes.c_uint64)]
+
+
+GEMV_FORM_LANES8, GEMV_FORM_ROWS, GEMV_FORM_LDS, GEMV_FORM_NARROW = 1, 2, 3, 4
+
+
 class DecodeFusion(ctypes.Structure):
     """mq_decode_fusion (include/magnetar_gpu.h)."""
     _fields_ = [("norm_weight", ctypes.c_void_p), ("norm_epsilon", ctypes.c_float), ("epilogue", ctypes.c_uint32),
@@ -73,6 +83,7 @@ _vp = ctypes.c_void_p
 
 _gpu = None
 _gguf = None
+_probe = None
 
 
 class GpuError(RuntimeError):
@@ -102,6 +113,8 @@ def gpu_lib():
         L.mq_last_error.argtypes = [_vp]
         L.mq_last_error.restype = ctypes.c_char_p
         L.mq_version.restype = ctypes.c_char_p
+        L.mq_gemv_launch_shape.argtypes = [ctypes.c_uint32, _u64, _u64, _u64, ctypes.c_int, ctypes.c_int,
+                                           ctypes.c_int, ctypes.POINTER(GemvShape)]
         L.mq_weight_upload.argtypes = [_vp, ctypes.c_uint32, _u64, _u64, ctypes.c_int, _u8p,
                                        ctypes.c_size_t, ctypes.POINTER(_u64)]
         L.mq_weight_release.argtypes = [_vp, _u64]
@@ -149,6 +162,29 @@ def gguf_lib():
         L.gg_quantize.argtypes = [ctypes.c_uint32, _f32p, _u64, _u64, _u8p]
         _gguf = L
     return _gguf
+
+
+def gemv_launch_shape(gguf_type, rows, cols, m, waves=0, variant=0, ksplit=0):
+    """The launch the pre-quantized decode GEMV takes (mq_gemv_launch_shape),
+    computed on the host: a GemvShape."""
+    out = GemvShape()
+    rc = gpu_lib().mq_gemv_launch_shape(gguf_type, rows, cols, m, waves, variant, ksplit, ctypes.byref(out))
+    if rc:
+        raise GpuError(rc, gpu_lib().mq_last_error(None).decode())
+    return out
+
+
+def probe_lib():
+    """The streaming-read probe (libmagnetar_probe.so), a measurement aid of
+    the benchmark: mqp_stream_read reads a device buffer once, nothing else."""
+    global _probe
+    if _probe is None:
+        L = _load(PROBE_LIB)
+        L.mqp_stream_read.argtypes = [_vp, _u64, ctypes.c_int, ctypes.c_int, _vp, _vp]
+        L.mqp_stream_groups.argtypes = [_u64, ctypes.c_int, ctypes.c_int]
+        L.mqp_stream_groups.restype = _u64
+        _probe = L
+    return _probe
 
 
 def _p(a, ctype):

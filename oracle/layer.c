@@ -21,7 +21,8 @@
  * input row (w_rows == rows). */
 int or_rmsnorm(const float *x, uint64_t rows, uint64_t cols, const float *w, uint64_t w_rows, float epsilon,
                float *out) {
-  if (cols == 0 || !(epsilon > 0.0f) || (w_rows != 1 && w_rows != rows)) return -1;
+  /* the reference rejects epsilon <= 0 only: a NaN epsilon gives NaN rows */
+  if (cols == 0 || epsilon <= 0.0f || (w_rows != 1 && w_rows != rows)) return -1;
   for (uint64_t r = 0; r < rows; ++r) {
     const float *v = x + r * cols;
     const float *wv = w + (w_rows == 1 ? 0 : r * cols);

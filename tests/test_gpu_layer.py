@@ -46,6 +46,20 @@ def test_rmsnorm(ctx, rows, cols, per_row):
     close(host(out), oracle.rmsnorm(x, w, 1e-5), 2e-6, "rmsnorm")
 
 
+def test_rmsnorm_epsilon_rule_matches_the_reference(ctx):
+    """The reference rejects epsilon <= 0 and nothing else (src/lib.rs:388):
+    zero and negative epsilons are shape errors, NaN runs and gives NaN."""
+    x = torch.from_numpy(rng(7).standard_normal((2, 256)).astype(np.float32)).cuda()
+    w = torch.ones(256, dtype=torch.float32, device="cuda")
+    out = torch.empty_like(x)
+    for eps in (0.0, -1e-5):
+        with pytest.raises(mg.GpuError) as e:
+            ctx.rmsnorm_dev(x.data_ptr(), 2, 256, w.data_ptr(), 1, eps, out.data_ptr())
+        assert e.value.code == mg.ERR_SHAPE and "epsilon must be positive" in e.value.reason
+    ctx.rmsnorm_dev(x.data_ptr(), 2, 256, w.data_ptr(), 1, float("nan"), out.data_ptr())
+    assert torch.isnan(out).all()
+
+
 @pytest.mark.parametrize("heads,dim,offset,half,inplace", [(32, 128, 4095, False, False), (8, 128, 4095, False, True),
                                                            (4, 64, 7, True, False), (2, 16, 100000, False, False)])
 def test_rope(ctx, heads, dim, offset, half, inplace):

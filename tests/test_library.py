@@ -94,3 +94,35 @@ def test_workload_weights_hash_matches_fixture():
         spec = workloads.WEIGHTS[name]
         data = workloads.weight_bytes(name)
         assert hashlib.sha256(data.tobytes()).hexdigest() == digest, (name, spec)
+
+
+@pytest.mark.parametrize("fmt", [Q4_K, IQ4_XS])
+@pytest.mark.parametrize("variant", [0, 1, 2, 3])
+@pytest.mark.parametrize("m", [1, 4, 8])
+def test_gemv_wave_override_clamps_to_the_launch_bound(fmt, variant, m):
+    """A 16-wave override (MQ_GEMV_SPLITS=16) never launches more than the
+    512 threads every GEMV kernel is built for (__launch_bounds__(512), 8
+    reduction slots): the launch that once faulted with 1024 threads."""
+    for rows, cols in ((14336, 4096), (4096, 14336), (64, 256), (1000, 512)):
+        for ksplit in (0, 1, 4, 16):
+            g = mg.gemv_launch_shape(fmt, rows, cols, m, waves=16, variant=variant, ksplit=ksplit)
+            assert 1 <= g.waves <= 8, (rows, cols, ksplit, g.form, g.waves)
+            assert g.lds_bytes <= 65536
+            if variant in (1, 2):
+                assert g.form in (mg.GEMV_FORM_LANES8, mg.GEMV_FORM_ROWS)
+            if g.form == mg.GEMV_FORM_ROWS:
+                assert m <= 4 and g.grid_x == -(-rows // 64)
+            if g.form == mg.GEMV_FORM_LANES8:
+                assert g.grid_x == -(-rows // 8)
+
+
+def test_gemv_default_launch_shapes():
+    """The defaults the measured shapes take: the 64-row LDS form for the
+    14336 x 4096 up projection (224 work-groups, no K split), the 16-row form
+    for the 4096 x 14336 down projection (256 work-groups)."""
+    g = mg.gemv_launch_shape(Q4_K, 14336, 4096, 1)
+    assert (g.form, g.grid_x, g.grid_y, g.waves) == (mg.GEMV_FORM_LDS, 224, 1, 8)
+    g = mg.gemv_launch_shape(IQ4_XS, 4096, 14336, 1)
+    assert (g.form, g.grid_x, g.grid_y, g.waves) == (mg.GEMV_FORM_NARROW, 256, 1, 8)
+    with pytest.raises(mg.GpuError):
+        mg.gemv_launch_shape(Q4_K, 14336, 4096, 9)

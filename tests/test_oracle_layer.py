@@ -46,7 +46,12 @@ def test_rmsnorm_is_scale_invariant_and_rejects_bad_epsilon():
     with pytest.raises(ValueError):
         oracle.rmsnorm(x, w, 0.0)
     with pytest.raises(ValueError):
+        oracle.rmsnorm(x, w, -1e-5)
+    with pytest.raises(ValueError):
         oracle.rmsnorm(x, np.ones(3, np.float32), 1e-5)
+    # the reference tests `epsilon <= 0.0` (src/lib.rs:388): NaN is accepted
+    # and propagates through the scale
+    assert np.all(np.isnan(oracle.rmsnorm(x, w, float("nan"))))
 
 
 # ---- rope (src/lib.rs:427-687) -----------------------------------------------------
