@@ -308,6 +308,37 @@ typedef struct {
 int mq_decode_matmul_dev(mq_ctx *ctx, uint64_t handle, const float *x_dev, uint64_t k,
                          const mq_decode_fusion *fusion, float *y_dev, void *stream);
 
+/* ---- Device-resident tensor storage ---------------------------------------------
+ * The memory a device Provider keeps its tensors in (placement
+ * ProviderOwnedOpaque): the reference stores them in a host map
+ * (`ReferenceCpuExecutor::storage`, src/lib.rs:1556-1621); a GPU Provider
+ * keeps them in HBM and copies to or from the host only on request
+ * (`read_tensor`, `write_tensor`). */
+
+/* The context's own stream (a hipStream_t), the one its host-pointer entry
+ * points use; NULL for a NULL context. */
+void *mq_context_stream(mq_ctx *ctx);
+
+/* Device memory of the context's GPU (bytes 0: *dev = NULL). */
+int mq_device_alloc(mq_ctx *ctx, uint64_t bytes, void **dev);
+
+/* Frees mq_device_alloc memory after the context's stream has drained. */
+int mq_device_free(mq_ctx *ctx, void *dev);
+
+/* Host -> device and device -> host copies ordered on the context's stream
+ * (after the work queued on it); they return when the copy is done. */
+int mq_copy_to_device(mq_ctx *ctx, void *dst_dev, const void *src, uint64_t bytes);
+int mq_copy_to_host(mq_ctx *ctx, void *dst, const void *src_dev, uint64_t bytes);
+
+/* Device -> device copy, enqueued on `stream`. */
+int mq_copy_dev(mq_ctx *ctx, void *dst_dev, const void *src_dev, uint64_t bytes, void *stream);
+
+/* dst[0..count) = value, a fill kernel enqueued on `stream`. */
+int mq_fill_dev(mq_ctx *ctx, float *dst_dev, uint64_t count, float value, void *stream);
+
+/* Waits for the work queued on `stream`. */
+int mq_synchronize(mq_ctx *ctx, void *stream);
+
 /* ---- Launch-shape query --------------------------------------------------------
  * No counterpart in the reference (its pool has no launch shape): the launch
  * the pre-quantized int8 decode GEMV (mq_matmul_prequantized_dev) takes for

@@ -1134,4 +1134,68 @@ int mq_add_dev(mq_ctx* ctx, const float* a_dev, uint64_t n, const float* b_dev, 
   return MQ_OK;
 } MQ_CATCH(ctx)
 
+// ---- device-resident tensor storage -------------------------------------------
+
+void* mq_context_stream(mq_ctx* ctx) { return ctx ? static_cast<void*>(ctx->stream) : nullptr; }
+
+int mq_device_alloc(mq_ctx* ctx, uint64_t bytes, void** dev) try {
+  if (!ctx || !dev) return fail(ctx, MQ_ERR_ARGUMENT, "mq_device_alloc: null argument");
+  *dev = nullptr;
+  if (bytes == 0) return MQ_OK;
+  DeviceGuard guard(ctx->device);
+  MQ_HIP(ctx, hipMalloc(dev, bytes));
+  return MQ_OK;
+} MQ_CATCH(ctx)
+
+int mq_device_free(mq_ctx* ctx, void* dev) try {
+  if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_device_free: null context");
+  if (!dev) return MQ_OK;
+  DeviceGuard guard(ctx->device);
+  MQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  MQ_HIP(ctx, hipFree(dev));
+  return MQ_OK;
+} MQ_CATCH(ctx)
+
+int mq_copy_to_device(mq_ctx* ctx, void* dst_dev, const void* src, uint64_t bytes) try {
+  if (!ctx || (bytes && (!dst_dev || !src))) return fail(ctx, MQ_ERR_ARGUMENT, "mq_copy_to_device: null argument");
+  if (bytes == 0) return MQ_OK;
+  DeviceGuard guard(ctx->device);
+  MQ_HIP(ctx, hipMemcpyAsync(dst_dev, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+  MQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return MQ_OK;
+} MQ_CATCH(ctx)
+
+int mq_copy_to_host(mq_ctx* ctx, void* dst, const void* src_dev, uint64_t bytes) try {
+  if (!ctx || (bytes && (!dst || !src_dev))) return fail(ctx, MQ_ERR_ARGUMENT, "mq_copy_to_host: null argument");
+  if (bytes == 0) return MQ_OK;
+  DeviceGuard guard(ctx->device);
+  MQ_HIP(ctx, hipMemcpyAsync(dst, src_dev, bytes, hipMemcpyDeviceToHost, ctx->stream));
+  MQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return MQ_OK;
+} MQ_CATCH(ctx)
+
+int mq_copy_dev(mq_ctx* ctx, void* dst_dev, const void* src_dev, uint64_t bytes, void* stream) try {
+  if (!ctx || (bytes && (!dst_dev || !src_dev))) return fail(ctx, MQ_ERR_ARGUMENT, "mq_copy_dev: null argument");
+  if (bytes == 0 || dst_dev == src_dev) return MQ_OK;
+  DeviceGuard guard(ctx->device);
+  MQ_HIP(ctx, hipMemcpyAsync(dst_dev, src_dev, bytes, hipMemcpyDeviceToDevice, static_cast<hipStream_t>(stream)));
+  return MQ_OK;
+} MQ_CATCH(ctx)
+
+int mq_fill_dev(mq_ctx* ctx, float* dst_dev, uint64_t count, float value, void* stream) try {
+  if (!ctx || (count && !dst_dev)) return fail(ctx, MQ_ERR_ARGUMENT, "mq_fill_dev: null argument");
+  if (count == 0) return MQ_OK;
+  DeviceGuard guard(ctx->device);
+  mq::launch_fill(dst_dev, count, value, static_cast<hipStream_t>(stream));
+  MQ_HIP(ctx, hipGetLastError());
+  return MQ_OK;
+} MQ_CATCH(ctx)
+
+int mq_synchronize(mq_ctx* ctx, void* stream) try {
+  if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_synchronize: null context");
+  DeviceGuard guard(ctx->device);
+  MQ_HIP(ctx, hipStreamSynchronize(static_cast<hipStream_t>(stream)));
+  return MQ_OK;
+} MQ_CATCH(ctx)
+
 }  // extern "C"

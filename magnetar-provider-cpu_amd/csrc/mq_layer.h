@@ -29,6 +29,9 @@ bool launch_attention(const float* q, const float* k, const float* v, uint64_t s
 // dst[i] = src[i], i < n (the buffers must not overlap)
 void launch_copy(const float* src, uint64_t n, float* dst, hipStream_t stream);
 
+// dst[i] = value, i < n (a kernel, not a memset: safe to record in a graph)
+void launch_fill(float* dst, uint64_t n, float value, hipStream_t stream);
+
 void launch_silu_mul(const float* g, const float* u, uint64_t n, float* out, hipStream_t stream);
 // out[i] = a[i] + b[i % b_n]
 void launch_add(const float* a, uint64_t n, const float* b, uint64_t b_n, float* out, hipStream_t stream);

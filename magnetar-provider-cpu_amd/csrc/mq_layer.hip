@@ -320,6 +320,11 @@ __global__ __launch_bounds__(256) void copy_kernel(const float* __restrict__ src
   if (i < n) dst[i] = src[i];
 }
 
+__global__ __launch_bounds__(256) void fill_kernel(float* __restrict__ dst, uint64_t n, float value) {
+  const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) dst[i] = value;
+}
+
 unsigned blocks_for(uint64_t n, unsigned per) { return static_cast<unsigned>((n + per - 1) / per); }
 
 }  // namespace
@@ -379,6 +384,10 @@ void launch_add(const float* a, uint64_t n, const float* b, uint64_t b_n, float*
 
 void launch_copy(const float* src, uint64_t n, float* dst, hipStream_t stream) {
   hipLaunchKernelGGL(copy_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, src, n, dst);
+}
+
+void launch_fill(float* dst, uint64_t n, float value, hipStream_t stream) {
+  hipLaunchKernelGGL(fill_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, dst, n, value);
 }
 
 }  // namespace mq

@@ -1,5 +1,5 @@
 """ctypes binding of libmagnetar_executor.so (include/magnetar_executor.h):
-the Provider-side contract of the GPU packed-weight matmul Kernel."""
+the Provider side of the GPU path, with device-resident tensors."""
 
 import ctypes
 import json
@@ -18,6 +18,8 @@ MEMORY_DENIED = 6
 UNKNOWN = 7
 ERR_ARGUMENT = 8
 ERR_DEVICE = 9
+ERR_OOM = 10
+KV_F32 = 0
 
 _lib = None
 
@@ -62,6 +64,20 @@ def lib():
         L.mg_materialization_count.restype = u64
         L.mg_memory_used.argtypes = [vp]
         L.mg_memory_used.restype = u64
+        L.mg_write_tensor_value.argtypes = [vp, ctypes.c_char_p, ctypes.c_int, ctypes.POINTER(u64), ctypes.c_uint32,
+                                            ctypes.POINTER(ctypes.c_float)]
+        L.mg_write_tensor_value_admitted.argtypes = L.mg_write_tensor_value.argtypes
+        L.mg_copy_tensor_admitted.argtypes = [vp, ctypes.c_char_p, ctypes.c_char_p]
+        L.mg_write_zeroed_kv_store.argtypes = [vp, ctypes.c_char_p, ctypes.POINTER(u64), ctypes.c_uint32,
+                                               ctypes.c_uint32, u64, u64, ctypes.POINTER(ctypes.c_int)]
+        L.mg_allocate_workspace.argtypes = [vp, u64, ctypes.c_char_p, ctypes.c_size_t]
+        L.mg_release_workspace.argtypes = [vp, ctypes.c_char_p]
+        L.mg_release_admitted_tensor.argtypes = [vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int)]
+        L.mg_synchronize.argtypes = [vp]
+        L.mg_profile_count.argtypes = [vp]
+        L.mg_profile_count.restype = ctypes.c_uint32
+        L.mg_profile_entry.argtypes = [vp, ctypes.c_uint32, ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(u64),
+                                       ctypes.POINTER(ctypes.c_double)]
         _lib = L
     return _lib
 
@@ -159,6 +175,53 @@ class GpuExecutor:
         out = np.empty(shape, np.float32)
         self._check(lib().mg_read_tensor(self.ptr, rid.encode(), out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
                                          out.size))
+        return out
+
+    def write_tensor_value(self, rid, tensor=None, admitted=False):
+        """`write_tensor_value(_admitted)`: tensor None writes back the Opaque
+        value (stores nothing); an array is a Host value that replaces."""
+        f = lib().mg_write_tensor_value_admitted if admitted else lib().mg_write_tensor_value
+        if tensor is None:
+            self._check(f(self.ptr, rid.encode(), 1, None, 0, None))
+            return
+        t, shape = self._tensor_args(tensor)
+        self._check(f(self.ptr, rid.encode(), 0, shape, t.ndim, t.ctypes.data_as(ctypes.POINTER(ctypes.c_float))))
+
+    def copy_tensor_admitted(self, src, dst):
+        self._check(lib().mg_copy_tensor_admitted(self.ptr, src.encode(), dst.encode()))
+
+    def write_zeroed_kv_store(self, rid, shape, head_dimension, precision=KV_F32, exact_rows=0):
+        """Returns True when the store was created."""
+        s = (ctypes.c_uint64 * max(1, len(shape)))(*shape)
+        created = ctypes.c_int()
+        self._check(lib().mg_write_zeroed_kv_store(self.ptr, rid.encode(), s, len(shape), precision, head_dimension,
+                                                   exact_rows, ctypes.byref(created)))
+        return bool(created.value)
+
+    def allocate_workspace(self, nbytes):
+        out = ctypes.create_string_buffer(128)
+        self._check(lib().mg_allocate_workspace(self.ptr, nbytes, out, 128))
+        return out.value.decode()
+
+    def release_workspace(self, allocation):
+        self._check(lib().mg_release_workspace(self.ptr, allocation.encode()))
+
+    def release_admitted_tensor(self, rid):
+        r = ctypes.c_int()
+        self._check(lib().mg_release_admitted_tensor(self.ptr, rid.encode(), ctypes.byref(r)))
+        return bool(r.value)
+
+    def synchronize(self):
+        self._check(lib().mg_synchronize(self.ptr))
+
+    def profile(self):
+        """[(kernel, calls, seconds)], most time first (MAGNETAR_GPU_PROFILE=1)."""
+        out = []
+        name = ctypes.create_string_buffer(128)
+        calls, secs = ctypes.c_uint64(), ctypes.c_double()
+        for i in range(lib().mg_profile_count(self.ptr)):
+            self._check(lib().mg_profile_entry(self.ptr, i, name, 128, ctypes.byref(calls), ctypes.byref(secs)))
+            out.append((name.value.decode(), calls.value, secs.value))
         return out
 
     def is_packed(self, rid):

@@ -20,7 +20,8 @@ def test_kernel_advertisements_under_the_gpu_identity():
     reference's f32 / contiguous / Host / TimeoutOnly shape."""
     ads = ex.kernel_advertisements()
     names = {a["name"] for a in ads}
-    assert {"matmul", "matmul-bias", "matmul-residual"} <= names
+    assert {"matmul", "matmul-bias", "matmul-residual", "embedding", "rmsnorm", "rope", "kv-write", "attention",
+            "silu-mul", "add", "residual-add"} == names
     for a in ads:
         assert a["provider"] == "magnetar-provider-gpu-mi355x"
         assert a["provider"] != "magnetar-provider-cpu-reference"
@@ -29,6 +30,23 @@ def test_kernel_advertisements_under_the_gpu_identity():
         assert a["cancellation"] == "TimeoutOnly"
         assert a["conformance_profile"] == "reference-cpu-conformance-v1"
     assert [a["rank"] for a in ads if a["name"] == "matmul"] == [2]
+
+
+def test_absurd_tensor_shape_is_an_error_not_an_abort():
+    """No exception crosses the C ABI: a [2^30, 2^30] tensor (4 EiB of f32)
+    cannot be held, and mg_write_tensor returns MG_ERR_OOM instead of
+    terminating the process (the host copy is attempted first)."""
+    import ctypes
+
+    L = ex.lib()
+    shape = (ctypes.c_uint64 * 2)(1 << 30, 1 << 30)
+    data = (ctypes.c_float * 4)()
+    rc = L.mg_write_tensor(None, b"t", shape, 2, data)
+    assert rc == ex.ERR_OOM
+    assert b"memory" in L.mg_executor_last_error(None) or b"size" in L.mg_executor_last_error(None)
+    # a shape whose byte count overflows 64 bits is rejected as an argument
+    shape = (ctypes.c_uint64 * 2)(1 << 40, 1 << 40)
+    assert L.mg_write_tensor(None, b"t", shape, 2, data) == ex.ERR_ARGUMENT
 
 
 def test_executor_without_a_device_reports_an_error():
