@@ -347,11 +347,13 @@ int mq_synchronize(mq_ctx *ctx, void *stream);
  * the default; 1, 2, 3: the MQ_GEMV_VARIANT forms) and ksplit (< 1: the
  * default K split) are the overrides a context reads from MQ_GEMV_SPLITS,
  * MQ_GEMV_VARIANT and MQ_GEMV_KSPLIT; every form clamps waves to its
- * kernel's launch bound (8 waves, 512 threads). */
+ * kernel's launch bound (8 waves, 512 threads; the one-block-per-wave form,
+ * taken only without a waves override, 16 waves, 1024 threads). */
 #define MQ_GEMV_FORM_LANES8 1u /* 8 lanes per row */
 #define MQ_GEMV_FORM_ROWS 2u   /* one row per lane, scalar activation reads (m <= 4) */
 #define MQ_GEMV_FORM_LDS 3u    /* 64 rows per work-group, activations in LDS, split-K over grid_y */
 #define MQ_GEMV_FORM_NARROW 4u /* 16 rows per work-group, activations in LDS */
+#define MQ_GEMV_FORM_WAVE 5u   /* 64 rows per work-group, one super-block per wave (up to 16 waves) */
 
 typedef struct {
   uint32_t form;

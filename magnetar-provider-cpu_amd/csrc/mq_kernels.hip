@@ -133,8 +133,24 @@ __device__ inline int sat_i8(float v) {
   return static_cast<int>(v);
 }
 
-// Four values of one 32-value block; the block's 8 lanes are consecutive
-// and all execute this together (the shuffles stay inside the 8).
+// Lane exchanges inside each aligned group of 8 lanes by DPP (no LDS
+// permute, no wait): quad_perm [1, 0, 3, 2] pairs lanes i ^ 1, quad_perm
+// [2, 3, 0, 1] lanes i ^ 2, and row_half_mirror (i <-> 7 - i) pairs every
+// lane with one of the other quad. Every lane of the group must be active.
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141;
+
+template <int CTRL>
+__device__ inline int dpp_i32(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+
+template <int CTRL>
+__device__ inline float dpp_f32(float v) {
+  return __int_as_float(dpp_i32<CTRL>(__float_as_int(v)));
+}
+
+// Four values of one 32-value block; the block's 8 lanes are consecutive,
+// start at a multiple of 8, and all execute this together.
 struct Quant4 {
   int q0, q1, q2, q3;
   float d;
@@ -145,7 +161,10 @@ struct Quant4 {
 __device__ inline Quant4 quantize4(float4 v) {
   Quant4 r;
   float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-  for (int o = 1; o < 8; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 8));
+  // the max over the 8 lanes (fmaxf ignores NaN, in any order)
+  amax = fmaxf(amax, dpp_f32<kDppXor1>(amax));
+  amax = fmaxf(amax, dpp_f32<kDppXor2>(amax));
+  amax = fmaxf(amax, dpp_f32<kDppHalfMirror>(amax));
   amax = fmaxf(0.0f, amax);
   r.d = amax / 127.0f;
   r.q0 = r.q1 = r.q2 = r.q3 = 0;
@@ -156,10 +175,10 @@ __device__ inline Quant4 quantize4(float4 v) {
     r.q3 = sat_i8(rintf(v.w / r.d));
   }
   int hs = r.q0 + r.q1 + r.q2 + r.q3;
-  hs += __shfl_xor(hs, 1, 8);
-  hs += __shfl_xor(hs, 2, 8);
-  r.half_sum = hs;
-  r.run_sum = hs + __shfl_xor(hs, 4, 8);
+  hs += dpp_i32<kDppXor1>(hs);
+  hs += dpp_i32<kDppXor2>(hs);
+  r.half_sum = hs;  // the quad's 16 values
+  r.run_sum = hs + dpp_i32<kDppHalfMirror>(hs);
   return r;
 }
 
@@ -1254,7 +1273,7 @@ __device__ inline void row_block(const RawRowBlock& a, const uint8_t* lds, int k
 // 0..31 copy the two blocks' int8 values (16 B each), lanes 32..47 their
 // runs' scales (and sums), through buffer loads predicated by offset (no
 // branch for a merge to wait on).
-template <int TYPE, int M, bool FUSED>
+template <int TYPE, int M, bool FUSED, bool TWO = true>
 struct WaveStage {
   float4 xa[M], xb[M];
   uint4 vv[M];
@@ -1268,7 +1287,7 @@ struct WaveStage {
       for (int m = 0; m < M; ++m) {
         const float4* xr = reinterpret_cast<const float4*>(xf + m * K);
         xa[m] = bA < b1 ? xr[64 * static_cast<uint64_t>(bA) + lane] : make_float4(0.f, 0.f, 0.f, 0.f);
-        xb[m] = bB < b1 ? xr[64 * static_cast<uint64_t>(bB) + lane] : make_float4(0.f, 0.f, 0.f, 0.f);
+        if (TWO) xb[m] = bB < b1 ? xr[64 * static_cast<uint64_t>(bB) + lane] : make_float4(0.f, 0.f, 0.f, 0.f);
       }
     } else {
       const uint32_t runs = static_cast<uint32_t>(K / 32);
@@ -1293,9 +1312,12 @@ struct WaveStage {
     if constexpr (FUSED) {
 #pragma unroll
       for (int m = 0; m < M; ++m) {
-        const Quant4 qa = quantize4(xa[m]), qb = quantize4(xb[m]);
+        const Quant4 qa = quantize4(xa[m]);
         if (bA < b1) FusedStage<TYPE, M, false>::put(qa, m * (kn / 4) + 64 * (bA - b0) + lane, lds, M * kn);
-        if (bB < b1) FusedStage<TYPE, M, false>::put(qb, m * (kn / 4) + 64 * (bB - b0) + lane, lds, M * kn);
+        if (TWO) {
+          const Quant4 qb = quantize4(xb[m]);
+          if (bB < b1) FusedStage<TYPE, M, false>::put(qb, m * (kn / 4) + 64 * (bB - b0) + lane, lds, M * kn);
+        }
       }
     } else {
       const bool is_val = lane < 32, is_run = lane >= 32 && lane < 48;
@@ -1397,6 +1419,56 @@ __global__ __launch_bounds__(512) void gemv_lds_int8_kernel(
   }
   finish_rows<M, EPI>(acc, mins, rows, y, addend, addend_stride, reinterpret_cast<float*>(lds), sk.partials,
                       sk.counters, sk.ks, fu);
+}
+
+// ---------------------------------------------------------------------------
+// Decode GEMV with one super-block per wave (Q4_K, IQ4_XS; m <= 4): the
+// LDS form's work-group of 64 stored rows with as many waves as the row has
+// super-blocks (up to 16, 1024 threads), wave s taking block s of every
+// row. Each wave stages its own block's activations (wave-local, no
+// barrier before the math), so a wave holds one block of weights (36
+// registers) instead of two: four waves per SIMD hide the math of one
+// wave behind the loads of the others, and the math left after the last
+// weight bytes arrive is one block. The waves' sums meet in LDS in wave
+// order (finish_rows), so results are deterministic; they differ from the
+// two-blocks-per-wave form by rounding only. No K split.
+// ---------------------------------------------------------------------------
+
+template <int TYPE, int M, bool FUSED, int EPI = kEpiPlain>
+__global__ __launch_bounds__(1024) void gemv_wave_int8_kernel(
+    const uint8_t* __restrict__ w, int nb, uint64_t rows, const int8_t* __restrict__ xv,
+    const float* __restrict__ xs, const int32_t* __restrict__ xsum, const float* __restrict__ xf,
+    float* __restrict__ y, const float* __restrict__ addend, uint64_t addend_stride, Fusion fu) {
+  static_assert(M <= 4, "wave-local staging holds at most 4 activation rows");
+  constexpr bool PIPE = M == 1;
+  constexpr int kTile = TYPE == kTypeQ4K ? kQ4kTileBytes : kIq4xsTileBytes;
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int lane = threadIdx.x & 63;
+  const int s = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // the wave's super-block
+  const int r = lane & 7;
+  const uint64_t K = static_cast<uint64_t>(nb) * 256;
+  const int kn = nb * 256, kruns = kn / 32;
+  const uint64_t groups = (rows + 7) / 8, group_bytes = static_cast<uint64_t>(nb) * kTile;
+  const uint64_t g0 = static_cast<uint64_t>(blockIdx.x) * 8;
+  const uint64_t span = (groups - g0 < 8 ? groups - g0 : 8) * group_bytes;
+  const __amdgpu_buffer_rsrc_t rsrc = buffer_rsrc(w + g0 * group_bytes, static_cast<uint32_t>(span));
+  const uint32_t off = static_cast<uint32_t>((lane >> 3) * group_bytes) + static_cast<uint32_t>(s) * kTile;
+
+  float acc[M], mins[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) acc[m] = mins[m] = 0.0f;
+  Chunk<M> next;
+  // activation loads first (per-wave returns come in issue order), then
+  // the weight block, then the staging
+  WaveStage<TYPE, M, FUSED, false> ws;
+  ws.load(xf, xv, xs, xsum, K, s, nb, nb, lane);
+  RawRowBlock A;
+  load_row_block<TYPE>(A, rsrc, off, r);
+  ws.put(lds, kn, kruns, 0, s, nb, nb, lane);
+  if (PIPE) read_chunk<TYPE, M>(next, lds, kn, kruns, s, 0);
+  row_block<TYPE, M, PIPE>(A, lds, kn, kruns, s, nb, false, next, acc, mins);
+  finish_rows<M, EPI>(acc, mins, rows, y, addend, addend_stride, reinterpret_cast<float*>(lds), nullptr, nullptr, 1,
+                      fu);
 }
 
 // ---------------------------------------------------------------------------
@@ -4042,15 +4114,72 @@ void launch_gemv_narrow(int type, const uint8_t* tiled, uint64_t rows, uint64_t 
   }
 }
 
+// The one-block-per-wave form: rows without a K split (enough 64-row
+// blocks to cover the CUs), 2..16 super-blocks, m <= 4, unless a sweep
+// forces the waves per work-group. Q4_K 14336 x 4096 m = 1 fused: 8.4 ->
+// 7.6 us (two blocks per wave at 8 waves against one per wave at 16).
+bool wave_form(uint64_t nb, uint64_t m, int splits_hint, const GemvSplitK& sk, size_t& lds, int type) {
+  if (sk.ks != 1 || m > 4 || nb < 2 || nb > 16 || splits_hint > 0 || sk.narrow == 1) return false;
+  lds = gemv_lds_bytes(type, nb, m, static_cast<int>(nb));
+  return lds <= 65536;
+}
+
+template <bool FUSED, int EPI = kEpiPlain>
+void launch_gemv_wave(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, const int8_t* values,
+                      const float* scales, const int32_t* sums, const float* x, uint64_t m, float* y,
+                      const float* addend, uint64_t addend_stride, size_t lds, const Fusion& fu, hipStream_t stream) {
+  dim3 grid(static_cast<unsigned>((rows + 63) / 64)), block(static_cast<unsigned>(64 * nb));
+  const int inb = static_cast<int>(nb);
+  if constexpr (EPI != kEpiPlain) {
+    // the decode-step epilogues take one activation row
+    if (type == kTypeQ4K)
+      hipLaunchKernelGGL((gemv_wave_int8_kernel<kTypeQ4K, 1, FUSED, EPI>), grid, block, lds, stream, tiled, inb, rows,
+                         values, scales, sums, x, y, addend, addend_stride, fu);
+    else
+      hipLaunchKernelGGL((gemv_wave_int8_kernel<kTypeIq4Xs, 1, FUSED, EPI>), grid, block, lds, stream, tiled, inb,
+                         rows, values, scales, nullptr, x, y, addend, addend_stride, fu);
+  } else if (type == kTypeQ4K) {
+    switch (m) {
+#define X(MM)                                                                                                   \
+  case MM:                                                                                                      \
+    hipLaunchKernelGGL((gemv_wave_int8_kernel<kTypeQ4K, MM, FUSED, EPI>), grid, block, lds, stream, tiled, inb, \
+                       rows, values, scales, sums, x, y, addend, addend_stride, fu);                            \
+    break;
+      X(1) X(2) X(3) X(4)
+#undef X
+      default:
+        break;
+    }
+  } else {
+    switch (m) {
+#define X(MM)                                                                                                     \
+  case MM:                                                                                                        \
+    hipLaunchKernelGGL((gemv_wave_int8_kernel<kTypeIq4Xs, MM, FUSED, EPI>), grid, block, lds, stream, tiled, inb, \
+                       rows, values, scales, nullptr, x, y, addend, addend_stride, fu);                           \
+    break;
+      X(1) X(2) X(3) X(4)
+#undef X
+      default:
+        break;
+    }
+  }
+}
+
 template <bool FUSED>
 void launch_gemv_lds(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, const int8_t* values,
                      const float* scales, const int32_t* sums, const float* x, uint64_t m, float* y,
-                     const float* addend, uint64_t addend_stride, int splits, const GemvSplitK& sk, size_t lds,
-                     hipStream_t stream) {
+                     const float* addend, uint64_t addend_stride, int splits, int splits_hint, const GemvSplitK& sk,
+                     size_t lds, hipStream_t stream) {
   size_t narrow_lds = 0;
   if (narrow_form(type, rows, nb, m, FUSED, sk, narrow_lds)) {
     launch_gemv_narrow<FUSED>(type, tiled, rows, nb, values, scales, sums, x, m, y, addend, addend_stride,
                               narrow_lds, stream);
+    return;
+  }
+  size_t wave_lds = 0;
+  if (wave_form(nb, m, splits_hint, sk, wave_lds, type)) {
+    launch_gemv_wave<FUSED>(type, tiled, rows, nb, values, scales, sums, x, m, y, addend, addend_stride, wave_lds,
+                            Fusion{}, stream);
     return;
   }
   dim3 grid(static_cast<unsigned>((rows + 63) / 64), static_cast<unsigned>(sk.ks)), block(64 * splits);
@@ -4116,6 +4245,14 @@ GemvShape gemv_int8_shape(int type, uint64_t rows, uint64_t nb, uint64_t m, int 
       g.lds = narrow_lds;
       return g;
     }
+    size_t wave_lds = 0;
+    if (wave_form(nb, m, splits, sk, wave_lds, type)) {
+      g.form = kGemvFormWave;
+      g.waves = static_cast<int>(nb);
+      g.grid_x = static_cast<unsigned>((rows + 63) / 64);
+      g.lds = wave_lds;
+      return g;
+    }
     g.form = kGemvFormLds;
     g.waves = lds_splits;
     g.grid_x = static_cast<unsigned>((rows + 63) / 64);
@@ -4143,12 +4280,12 @@ void launch_gemv_int8(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb
                       hipStream_t stream) {
   const int inb = static_cast<int>(nb);
   const GemvShape g = gemv_int8_shape(type, rows, nb, m, splits, variant, sk);
-  if (g.form == kGemvFormLds || g.form == kGemvFormNarrow) {
+  if (g.form == kGemvFormLds || g.form == kGemvFormNarrow || g.form == kGemvFormWave) {
     int lds_splits = 0;
     size_t lds = 0;
     lds_form_shape(type, rows, nb, m, splits, sk.ks, lds_splits, lds);
     launch_gemv_lds<false>(type, tiled, rows, nb, values, scales, sums, nullptr, m, y, addend, addend_stride,
-                           lds_splits, sk, lds, stream);
+                           lds_splits, splits, sk, lds, stream);
     return;
   }
   splits = g.waves;
@@ -4216,7 +4353,7 @@ bool launch_gemv_fused(int type, const uint8_t* tiled, uint64_t rows, uint64_t n
   size_t lds = 0;
   if (!lds_form_shape(type, rows, nb, m, splits, sk.ks, lds_splits, lds)) return false;
   launch_gemv_lds<true>(type, tiled, rows, nb, nullptr, nullptr, nullptr, x, m, y, addend, addend_stride,
-                        lds_splits, sk, lds, stream);
+                        lds_splits, splits, sk, lds, stream);
   return true;
 }
 
@@ -4241,6 +4378,20 @@ bool launch_gemv_decode_fused(int type, const uint8_t* tiled, uint64_t rows, uin
       default:
         return false;
     }
+  }
+  size_t wave_lds = 0;
+  if (!norm && wave_form(nb, 1, 0, sk, wave_lds, type)) {
+    // the same form as the plain fused GEMV of this shape takes
+    if (epilogue == kEpiRope)
+      launch_gemv_wave<true, kEpiRope>(type, tiled, rows, nb, nullptr, nullptr, nullptr, x, 1, y, nullptr, 0,
+                                       wave_lds, fu, stream);
+    else if (epilogue == kEpiSiluPairs)
+      launch_gemv_wave<true, kEpiSiluPairs>(type, tiled, rows, nb, nullptr, nullptr, nullptr, x, 1, y, nullptr, 0,
+                                            wave_lds, fu, stream);
+    else
+      launch_gemv_wave<true>(type, tiled, rows, nb, nullptr, nullptr, nullptr, x, 1, y, nullptr, 0, wave_lds, fu,
+                             stream);
+    return true;
   }
   int splits = 0;
   size_t lds = 0;

@@ -50,6 +50,7 @@ constexpr int kGemvFormLanes8 = 1;  // variant 1: 8 lanes per row
 constexpr int kGemvFormRows = 2;    // variant 2: one row per lane, scalar activations
 constexpr int kGemvFormLds = 3;     // variant 3: 64 rows per work-group, activations in LDS, split-K
 constexpr int kGemvFormNarrow = 4;  // variant 3's 16-row form (long rows, few output rows)
+constexpr int kGemvFormWave = 5;    // variant 3 with one super-block per wave (no K split)
 struct GemvShape {
   int form = 0;
   int waves = 0;

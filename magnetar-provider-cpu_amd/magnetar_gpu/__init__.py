@@ -64,7 +64,7 @@ class GemvShape(ctypes.Structure):
                 ("grid_y", ctypes.c_uint32), ("lds_bytes", ctypes.c_uint64)]
 
 
-GEMV_FORM_LANES8, GEMV_FORM_ROWS, GEMV_FORM_LDS, GEMV_FORM_NARROW = 1, 2, 3, 4
+GEMV_FORM_LANES8, GEMV_FORM_ROWS, GEMV_FORM_LDS, GEMV_FORM_NARROW, GEMV_FORM_WAVE = 1, 2, 3, 4, 5
 
 
 class DecodeFusion(ctypes.Structure):
