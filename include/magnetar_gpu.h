@@ -133,6 +133,21 @@ int mq_matmul(mq_ctx *ctx, uint64_t handle, const float *x, uint64_t m,
 int mq_matmul_dev(mq_ctx *ctx, uint64_t handle, const float *x_dev, uint64_t m,
                   uint64_t k, uint32_t flags, float *y_dev, void *stream);
 
+/* mq_matmul_dev without any device allocation, for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). No counterpart in the reference. Every
+ * temporary (int8 or f16 activations, split-K partials and counters) lives
+ * in one fixed 32 MiB device array per GPU (its address resolved by
+ * mq_create), which calls no hipMalloc, hipFree or allocating library
+ * routine; a matmul whose temporaries exceed 32 MiB less 64 KiB of
+ * counters (e.g. a prefill of m * k * 2 bytes of f16 activations above
+ * that) is MQ_ERR_SHAPE. The array is shared by every call on the GPU and
+ * keeps the last call's contents (what must start at zero is cleared by
+ * each call): calls that overlap on one GPU, on any stream or context,
+ * race. Same results as mq_matmul_dev. */
+int mq_matmul_noalloc_dev(mq_ctx *ctx, uint64_t handle, const float *x_dev, uint64_t m,
+                          uint64_t k, uint32_t flags, float *y_dev, void *stream);
+
 /* y = x . W^T + addend, the addition fused into the kernel's output write
  * (the product rounded first, then the addend added): addend_rows = 1
  * broadcasts one [stored_rows] row (a bias), addend_rows = m adds an

@@ -35,6 +35,16 @@ struct Weight {
 
 thread_local std::string g_create_error;
 
+// The no-allocation matmul's temporaries (mq_matmul_noalloc_dev): one
+// device array per GPU, resolved once per device by mq_create (with that
+// device current) and shared by every call on the GPU. Host code uses only
+// the resolved address: the array's name is a host-side stand-in.
+constexpr size_t kScratchBytes = 32u << 20;
+constexpr size_t kScratchCounterBytes = 64u << 10;  // split-K arrival counters, 16384 row blocks
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+std::mutex g_scratch_mu;
+std::map<int, uint8_t*> g_scratch_address;
+
 }  // namespace
 
 struct mq_ctx {
@@ -63,6 +73,8 @@ struct mq_ctx {
   int gemv_splits_override = 0;
   int gemv_variant = 0;
   int gemm_variant = 0;
+  // This device's scratch array (mq_matmul_noalloc_dev).
+  uint8_t* scratch = nullptr;
   // Token ids of the embedding lookup (device copy).
   uint32_t* ids = nullptr;
   size_t ids_cap = 0;
@@ -192,9 +204,41 @@ int acquire_workspace(mq_ctx* ctx, hipStream_t stream, size_t bytes) {
   return MQ_OK;
 }
 
+// Where one matmul's temporaries live: the context's growable buffers
+// (fixed == nullptr), or the fixed scratch array of the no-allocation entry
+// point, laid out as [split-K counters | split-K partials | workspace].
+struct Scratch {
+  uint8_t* fixed = nullptr;
+  size_t bytes = 0;
+  size_t used = kScratchCounterBytes;  // the next free byte past the counters
+};
+
+int scratch_overflow(mq_ctx* ctx, size_t need) {
+  return fail(ctx, MQ_ERR_SHAPE, "this matmul needs " + std::to_string(need) +
+                                     " bytes of temporaries, above the no-allocation entry point's " +
+                                     std::to_string(kScratchBytes - kScratchCounterBytes));
+}
+
+// `bytes` of workspace: the context's (grown as needed), or the next free
+// part of the fixed scratch. Caller holds ctx->mu.
+int workspace(mq_ctx* ctx, hipStream_t stream, size_t bytes, Scratch* sc, void** out) {
+  if (sc && sc->fixed) {
+    const size_t at = (sc->used + 255) & ~static_cast<size_t>(255);
+    if (at + bytes > sc->bytes) return scratch_overflow(ctx, at + bytes - kScratchCounterBytes);
+    *out = sc->fixed + at;
+    sc->used = at + bytes;
+    return MQ_OK;
+  }
+  int rc = acquire_workspace(ctx, stream, bytes);
+  if (rc) return rc;
+  *out = ctx->ws;
+  return MQ_OK;
+}
+
 // The GEMV's split-K buffers for `w` and m rows (ks == 1: none). Caller
 // holds ctx->mu and has ordered `stream` (order_stream).
-int acquire_splitk(mq_ctx* ctx, hipStream_t stream, const Weight& w, uint64_t m, mq::GemvSplitK& sk) {
+int acquire_splitk(mq_ctx* ctx, hipStream_t stream, const Weight& w, uint64_t m, mq::GemvSplitK& sk,
+                   Scratch* sc = nullptr) {
   sk = mq::GemvSplitK{};
   sk.ks = ctx->gemv_ksplit_override > 0 ? ctx->gemv_ksplit_override : mq::gemv_default_ksplit(w.rows, w.nb);
   sk.narrow = ctx->gemv_narrow_override;
@@ -213,6 +257,18 @@ int acquire_splitk(mq_ctx* ctx, hipStream_t stream, const Weight& w, uint64_t m,
   }
   const uint64_t blocks = (w.rows + 63) / 64;
   const size_t partials = static_cast<size_t>(sk.ks) * m * 2 * blocks * 64 * sizeof(float);
+  if (sc && sc->fixed) {
+    // the counters start at zero for this call whatever an earlier call
+    // left there: cleared by a fill kernel, not a memset (graph-safe)
+    if (blocks * sizeof(uint32_t) > kScratchCounterBytes) return scratch_overflow(ctx, blocks * sizeof(uint32_t));
+    void* part = nullptr;
+    int rc = workspace(ctx, stream, partials, sc, &part);
+    if (rc) return rc;
+    sk.counters = reinterpret_cast<uint32_t*>(sc->fixed);
+    sk.partials = static_cast<float*>(part);
+    mq::launch_fill(reinterpret_cast<float*>(sc->fixed), blocks, 0.0f, stream);
+    return MQ_OK;
+  }
   if (blocks > ctx->sk_counters || ctx->sk_counters * sizeof(uint32_t) + partials > ctx->sk_bytes) {
     // grow: the counter region keeps a fixed capacity between growths, so a
     // smaller weight's partials never land on another weight's counters
@@ -286,17 +342,19 @@ constexpr uint64_t kGemmMinK = 512;
 // The decode GEMV for m <= 8 rows. Caller holds ctx->mu and has validated
 // the arguments.
 int gemv_locked(mq_ctx* ctx, const Weight& w, const float* x, uint64_t m, uint64_t k, bool int8, float* y,
-                hipStream_t stream, const float* addend, uint64_t addend_stride) {
+                hipStream_t stream, const float* addend, uint64_t addend_stride, Scratch* sc = nullptr) {
   mq::GemvSplitK sk;
   int rc = MQ_OK;
+  if (sc) sc->used = kScratchCounterBytes;  // each launch sequence reuses the scratch, stream-ordered
   if (grid_type(w.type)) {
     int8_t* values = nullptr;
     float* scales = nullptr;
     if (int8) {
       const size_t vb = align256(m * k), sb = align256(m * k / 32 * 4), hb = align256(m * k / 32 * 8);
-      rc = acquire_workspace(ctx, stream, vb + sb + hb);
+      void* ws = nullptr;
+      rc = workspace(ctx, stream, vb + sb + hb, sc, &ws);
       if (rc) return rc;
-      auto* base = static_cast<uint8_t*>(ctx->ws);
+      auto* base = static_cast<uint8_t*>(ws);
       values = reinterpret_cast<int8_t*>(base);
       scales = reinterpret_cast<float*>(base + vb);
       mq::launch_quantize_activations(x, m, k, values, scales, reinterpret_cast<int32_t*>(base + vb + sb), nullptr, 1,
@@ -307,8 +365,8 @@ int gemv_locked(mq_ctx* ctx, const Weight& w, const float* x, uint64_t m, uint64
     return MQ_OK;
   }
   if (int8) {
-    rc = order_stream(ctx, stream);
-    if (!rc) rc = acquire_splitk(ctx, stream, w, m, sk);
+    rc = sc && sc->fixed ? MQ_OK : order_stream(ctx, stream);
+    if (!rc) rc = acquire_splitk(ctx, stream, w, m, sk, sc);
     if (rc) return rc;
   }
   if (plane_type(w.type)) {
@@ -327,9 +385,10 @@ int gemv_locked(mq_ctx* ctx, const Weight& w, const float* x, uint64_t m, uint64
     // one launch: quantized into LDS and multiplied
   } else if (int8) {
     const size_t vb = align256(m * k), sb = align256(m * k / 32 * 4), hb = align256(m * k / 32 * 8);
-    rc = acquire_workspace(ctx, stream, vb + sb + hb);
+    void* ws = nullptr;
+    rc = workspace(ctx, stream, vb + sb + hb, sc, &ws);
     if (rc) return rc;
-    auto* base = static_cast<uint8_t*>(ctx->ws);
+    auto* base = static_cast<uint8_t*>(ws);
     auto* values = reinterpret_cast<int8_t*>(base);
     auto* scales = reinterpret_cast<float*>(base + vb);
     auto* sums = reinterpret_cast<int32_t*>(base + vb + sb);
@@ -346,7 +405,8 @@ int gemv_locked(mq_ctx* ctx, const Weight& w, const float* x, uint64_t m, uint64
 // Enqueues y = x . W^T [+ addend] on `stream`. Caller holds ctx->mu.
 // addend_rows: 0 (no addend), 1 (one row broadcast) or m.
 int matmul_locked(mq_ctx* ctx, const Weight& w, const float* x, uint64_t m, uint64_t k, uint32_t flags, float* y,
-                  hipStream_t stream, const float* addend = nullptr, uint64_t addend_rows = 0) {
+                  hipStream_t stream, const float* addend = nullptr, uint64_t addend_rows = 0,
+                  Scratch* sc = nullptr) {
   if (flags & ~(MQ_INT8_ACTIVATIONS | MQ_TRANSPOSE_B)) return fail(ctx, MQ_ERR_ARGUMENT, "unknown matmul flag bits");
   int rc = check_k(ctx, w, k, flags);
   if (rc) return rc;
@@ -363,15 +423,17 @@ int matmul_locked(mq_ctx* ctx, const Weight& w, const float* x, uint64_t m, uint
     // input-major (axpy): f32 activations whatever the int8 setting, as
     // the reference's `packed_axpy` (src/native/mod.rs:154-194)
     const int ks = mq::axpy_ksplit(k, n);
-    rc = acquire_workspace(ctx, stream, align256(static_cast<size_t>(ks) * 4 * n * sizeof(float)));
+    void* ws = nullptr;
+    if (sc) sc->used = kScratchCounterBytes;
+    rc = workspace(ctx, stream, align256(static_cast<size_t>(ks) * 4 * n * sizeof(float)), sc, &ws);
     if (rc) return rc;
     mq::launch_axpy(static_cast<int>(w.type), w.dev, w.nb, k, n, x, m, y, addend, addend_stride,
-                    static_cast<float*>(ctx->ws), ks, stream);
+                    static_cast<float*>(ws), ks, stream);
   } else if (m <= kGemvChunkRows || k < kGemmMinK || (grid_type(w.type) && !grid_gemm_ready(ctx->device))) {
     for (uint64_t r0 = 0; r0 < m; r0 += kGemvMaxRows) {
       const uint64_t mc = m - r0 < kGemvMaxRows ? m - r0 : kGemvMaxRows;
       const float* ad = addend ? addend + (addend_stride ? r0 * w.rows : 0) : nullptr;
-      rc = gemv_locked(ctx, w, x + r0 * k, mc, k, int8, y + r0 * w.rows, stream, ad, addend_stride);
+      rc = gemv_locked(ctx, w, x + r0 * k, mc, k, int8, y + r0 * w.rows, stream, ad, addend_stride, sc);
       if (rc) return rc;
     }
   } else {
@@ -380,10 +442,12 @@ int matmul_locked(mq_ctx* ctx, const Weight& w, const float* x, uint64_t m, uint
     const int ks = mq::gemm_splits(static_cast<int>(w.type), w.rows, m, w.nb, k, ctx->gemm_variant);
     const size_t abytes = align256(m * k * 2);
     const size_t pbytes = ks > 1 ? align256(static_cast<size_t>(ks) * m * w.rows * sizeof(float)) : 0;
-    rc = acquire_workspace(ctx, stream, abytes + pbytes);
+    void* ws = nullptr;
+    if (sc) sc->used = kScratchCounterBytes;
+    rc = workspace(ctx, stream, abytes + pbytes, sc, &ws);
     if (rc) return rc;
-    auto* a16 = static_cast<uint16_t*>(ctx->ws);
-    float* part = ks > 1 ? reinterpret_cast<float*>(static_cast<uint8_t*>(ctx->ws) + abytes) : nullptr;
+    auto* a16 = static_cast<uint16_t*>(ws);
+    float* part = ks > 1 ? reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + abytes) : nullptr;
     if (int8)
       mq::launch_quantize_activations(x, m, k, nullptr, nullptr, nullptr, a16, 1, stream);
     else
@@ -485,6 +549,23 @@ int mq_create(int device, mq_ctx** out) try {
     return hip_fail(nullptr, e, "mq_create");
   }
   ctx->ws_stream = ctx->stream;
+  {
+    // the scratch array's address on this device (the device is current)
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    auto it = g_scratch_address.find(device);
+    if (it == g_scratch_address.end()) {
+      void* p = nullptr;
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !p) {
+        (void)hipEventDestroy(ctx->ws_event);
+        (void)hipStreamDestroy(ctx->stream);
+        delete ctx;
+        return hip_fail(nullptr, e != hipSuccess ? e : hipErrorInvalidSymbol, "hipGetSymbolAddress(scratch)");
+      }
+      it = g_scratch_address.emplace(device, static_cast<uint8_t*>(p)).first;
+    }
+    ctx->scratch = it->second;
+  }
   if (const char* s = std::getenv("MQ_GEMV_SPLITS")) ctx->gemv_splits_override = std::atoi(s);
   if (const char* s = std::getenv("MQ_GEMV_KSPLIT")) ctx->gemv_ksplit_override = std::atoi(s);
   if (const char* s = std::getenv("MQ_GEMV_NARROW")) ctx->gemv_narrow_override = std::atoi(s);
@@ -677,6 +758,20 @@ int mq_matmul_dev(mq_ctx* ctx, uint64_t handle, const float* x_dev, uint64_t m, 
   DeviceGuard guard(ctx->device);
   hipStream_t s = static_cast<hipStream_t>(stream);
   return matmul_locked(ctx, *w, x_dev, m, k, flags, y_dev, s);
+} MQ_CATCH(ctx)
+
+int mq_matmul_noalloc_dev(mq_ctx* ctx, uint64_t handle, const float* x_dev, uint64_t m, uint64_t k, uint32_t flags,
+                          float* y_dev, void* stream) try {
+  if (!ctx) return fail(ctx, MQ_ERR_ARGUMENT, "mq_matmul_noalloc_dev: null context");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  const Weight* w = find_weight(ctx, handle);
+  if (!w) return fail(ctx, MQ_ERR_ARGUMENT, "unknown weight handle " + std::to_string(handle));
+  if (!ctx->scratch) return fail(ctx, MQ_ERR_ARGUMENT, "mq_matmul_noalloc_dev: no scratch address on this device");
+  DeviceGuard guard(ctx->device);
+  Scratch sc;
+  sc.fixed = ctx->scratch;
+  sc.bytes = kScratchBytes;
+  return matmul_locked(ctx, *w, x_dev, m, k, flags, y_dev, static_cast<hipStream_t>(stream), nullptr, 0, &sc);
 } MQ_CATCH(ctx)
 
 namespace {

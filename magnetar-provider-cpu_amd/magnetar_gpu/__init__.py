@@ -125,6 +125,7 @@ def gpu_lib():
                                      ctypes.POINTER(_u64), ctypes.POINTER(ctypes.c_int), ctypes.POINTER(_u64)]
         L.mq_matmul.argtypes = [_vp, _u64, _f32p, _u64, _u64, ctypes.c_uint32, _f32p]
         L.mq_matmul_dev.argtypes = [_vp, _u64, _vp, _u64, _u64, ctypes.c_uint32, _vp, _vp]
+        L.mq_matmul_noalloc_dev.argtypes = [_vp, _u64, _vp, _u64, _u64, ctypes.c_uint32, _vp, _vp]
         L.mq_quantize_activations_dev.argtypes = [_vp, _vp, _u64, _u64, _vp, _vp, _vp, _vp]
         L.mq_matmul_prequantized_dev.argtypes = [_vp, _u64, _vp, _vp, _vp, _u64, _u64, _vp, _vp]
         L.mq_prepare_activations_f16_dev.argtypes = [_vp, _vp, _u64, _u64, ctypes.c_uint32, _vp, _vp]
