@@ -471,7 +471,7 @@ def gemm_part(ctx, torch, workloads, use_graph, args):
     gm_rows = 512
     gw = ctx.upload(gfmt, gn, gk, workloads.weight_bytes(gname))
     gx = torch.from_numpy(workloads.activations(gseed, gm_rows, gk)).cuda()
-    ga = torch.empty(gm_rows * gk, dtype=torch.float16, device="cuda")
+    ga = torch.empty(gm_rows * gk + 2 * gm_rows, dtype=torch.float16, device="cuda")  # values, then row factors
     gy = torch.empty((gm_rows, gn), dtype=torch.float32, device="cuda")
     flops = 2.0 * gm_rows * gn * gk
 
@@ -513,7 +513,7 @@ def gemm_part(ctx, torch, workloads, use_graph, args):
         sfmt, sn, sk, sseed, _ = workloads.WEIGHTS[wname]
         sw = gw if wname == gname else ctx.upload(sfmt, sn, sk, workloads.weight_bytes(wname))
         sx = torch.from_numpy(workloads.activations(sseed, mm, sk)).cuda()
-        sa = torch.empty(mm * sk, dtype=torch.float16, device="cuda")
+        sa = torch.empty(mm * sk + 2 * mm, dtype=torch.float16, device="cuda")
         sy = torch.empty((mm, sn), dtype=torch.float32, device="cuda")
         ctx.prepare_activations_f16_dev(sx.data_ptr(), mm, sk, sa.data_ptr(), int8=True, stream=stream)
 

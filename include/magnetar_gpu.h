@@ -182,15 +182,20 @@ int mq_matmul_prequantized_dev(mq_ctx *ctx, uint64_t handle,
                                const int32_t *sums_dev, uint64_t m, uint64_t k,
                                float *y_dev, void *stream);
 
-/* The prefill path's activation operand on device: a16[m*k] f16 holding
- * f16(int8_rounded(x)) with MQ_INT8_ACTIVATIONS (the values the reference's
+/* The prefill path's activation operand on device: a16_dev holds m*k f16
+ * values, then m f32 row factors (m*k*2 + m*4 bytes; the factors start at
+ * the float after the last f16 value). Value (r, c) is f16(v * 2^e_r), v =
+ * int8_rounded(x) with MQ_INT8_ACTIVATIONS (the values the reference's
  * int8 activations stand for, `int8_rounded`, src/native/tests.rs:77-89),
- * else f16(x). */
+ * else x; 2^e_r puts row r's largest magnitude in [2^14, 2^15) (f16's
+ * range: up to 65504, full precision from 2^-14), and the row factor is
+ * 2^-e_r, which the GEMM applies to its f32 output. */
 int mq_prepare_activations_f16_dev(mq_ctx *ctx, const float *x_dev, uint64_t m,
                                    uint64_t k, uint32_t flags, uint16_t *a16_dev,
                                    void *stream);
 
-/* The prefill GEMM on prepared f16 activations (any m): y[m][stored_rows]
+/* The prefill GEMM on prepared f16 activations (any m, the buffer of
+ * mq_prepare_activations_f16_dev): y[m][stored_rows]
  * = a16 . dequantize(W)^T with f32 accumulation, the MFMA replacement of
  * the column kernels for many activation rows
  * (src/native/quant.rs:666-744, 1386-1433 via src/native/mod.rs:110-152).

@@ -31,7 +31,18 @@ struct Weight {
   int transposed = 1;
   uint8_t* dev = nullptr;
   uint64_t dev_bytes = 0;
+  // the prefill GEMM's f16 range factors (mq::weight_f16_factors of the
+  // largest dequantized magnitude)
+  float f16_up = 1.0f, f16_down = 1.0f;
 };
+
+mq::F16Range range(const Weight& w, const float* row_factors) {
+  mq::F16Range r;
+  r.row = row_factors;
+  r.up = w.f16_up;
+  r.down = w.f16_down;
+  return r;
+}
 
 thread_local std::string g_create_error;
 
@@ -357,8 +368,7 @@ int gemv_locked(mq_ctx* ctx, const Weight& w, const float* x, uint64_t m, uint64
       auto* base = static_cast<uint8_t*>(ws);
       values = reinterpret_cast<int8_t*>(base);
       scales = reinterpret_cast<float*>(base + vb);
-      mq::launch_quantize_activations(x, m, k, values, scales, reinterpret_cast<int32_t*>(base + vb + sb), nullptr, 1,
-                                      stream);
+      mq::launch_quantize_activations(x, m, k, values, scales, reinterpret_cast<int32_t*>(base + vb + sb), stream);
     }
     mq::launch_gemv_grid(static_cast<int>(w.type), w.dev, w.nb, w.rows, values, scales, x, m, int8 ? 1 : 0, y, addend,
                          addend_stride, stream);
@@ -392,7 +402,7 @@ int gemv_locked(mq_ctx* ctx, const Weight& w, const float* x, uint64_t m, uint64
     auto* values = reinterpret_cast<int8_t*>(base);
     auto* scales = reinterpret_cast<float*>(base + vb);
     auto* sums = reinterpret_cast<int32_t*>(base + vb + sb);
-    mq::launch_quantize_activations(x, m, k, values, scales, sums, nullptr, 1, stream);
+    mq::launch_quantize_activations(x, m, k, values, scales, sums, stream);
     mq::launch_gemv_int8(static_cast<int>(w.type), w.dev, w.rows, w.nb, values, scales, sums, m, y, addend,
                          addend_stride, ctx->gemv_splits_override, ctx->gemv_variant, sk, stream);
   } else {
@@ -437,23 +447,21 @@ int matmul_locked(mq_ctx* ctx, const Weight& w, const float* x, uint64_t m, uint
       if (rc) return rc;
     }
   } else {
-    // workspace: the f16 activations, then (under-filled GEMMs) the split-K
-    // partials
+    // workspace: the f16 activations and their row factors, then
+    // (under-filled GEMMs) the split-K partials
     const int ks = mq::gemm_splits(static_cast<int>(w.type), w.rows, m, w.nb, k, ctx->gemm_variant);
-    const size_t abytes = align256(m * k * 2);
+    const size_t abytes = align256(m * k * 2) + align256(m * sizeof(float));
     const size_t pbytes = ks > 1 ? align256(static_cast<size_t>(ks) * m * w.rows * sizeof(float)) : 0;
     void* ws = nullptr;
     if (sc) sc->used = kScratchCounterBytes;
     rc = workspace(ctx, stream, abytes + pbytes, sc, &ws);
     if (rc) return rc;
     auto* a16 = static_cast<uint16_t*>(ws);
+    auto* factors = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + align256(m * k * 2));
     float* part = ks > 1 ? reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + abytes) : nullptr;
-    if (int8)
-      mq::launch_quantize_activations(x, m, k, nullptr, nullptr, nullptr, a16, 1, stream);
-    else
-      mq::launch_activations_f16(x, m, k, a16, stream);
+    mq::launch_activations_f16(x, m, k, int8 ? 1 : 0, a16, factors, stream);
     mq::launch_gemm(static_cast<int>(w.type), w.dev, w.rows, w.nb, k, a16, m, y, addend, addend_stride,
-                    ctx->gemm_variant, stream, part);
+                    ctx->gemm_variant, stream, range(w, factors), part);
   }
   MQ_HIP(ctx, hipGetLastError());
   return MQ_OK;
@@ -628,6 +636,50 @@ int mq_set_iq_grids(mq_ctx* ctx, const uint64_t* iq2xxs, const uint64_t* iq2xs, 
   return MQ_OK;
 } MQ_CATCH(ctx)
 
+// The largest magnitude among a weight's dequantized values (device
+// dequantization in chunks of whole 8-row tiles, at most 8 Mi values each)
+// and the prefill GEMM's f16 factors from it. Caller holds ctx->mu.
+hipError_t set_f16_range(mq_ctx* ctx, Weight& w) {
+  const int type = static_cast<int>(w.type);
+  uint64_t chunk = (8ull << 20) / w.cols / 8 * 8;
+  if (chunk < 8) chunk = 8;
+  if (chunk > w.rows) chunk = w.rows;
+  float* tmp = nullptr;
+  uint32_t* amax = nullptr;
+  hipError_t e = hipMalloc(&tmp, chunk * w.cols * sizeof(float));
+  if (e != hipSuccess) return e;
+  e = hipMalloc(&amax, sizeof(uint32_t));
+  if (e != hipSuccess) {
+    (void)hipFree(tmp);
+    return e;
+  }
+  e = hipMemsetAsync(amax, 0, sizeof(uint32_t), ctx->stream);
+  for (uint64_t r0 = 0; e == hipSuccess && r0 < w.rows; r0 += chunk) {
+    const uint64_t rc = chunk < w.rows - r0 ? chunk : w.rows - r0;
+    if (grid_type(w.type))
+      mq::launch_dequantize_grid(type, w.dev + r0 * w.nb * static_cast<uint64_t>(mq::block_bytes_of(type)), rc, w.nb,
+                                 0, tmp, ctx->stream);
+    else if (plane_type(w.type))
+      mq::launch_dequantize_planes(type, w.dev + r0 / 8 * w.nb * static_cast<uint64_t>(mq::tile_bytes(type)), rc,
+                                   w.cols, w.nb, 0, tmp, ctx->stream);
+    else
+      mq::launch_dequantize(type, w.dev + r0 / 8 * w.nb * static_cast<uint64_t>(mq::tile_bytes(type)), rc, w.nb, 0,
+                            tmp, ctx->stream);
+    mq::launch_absmax(tmp, rc * w.cols, amax, ctx->stream);
+    e = hipGetLastError();
+  }
+  uint32_t bits = 0;
+  if (e == hipSuccess) e = hipMemcpyAsync(&bits, amax, sizeof bits, hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  (void)hipFree(tmp);
+  (void)hipFree(amax);
+  if (e != hipSuccess) return e;
+  float a;
+  std::memcpy(&a, &bits, sizeof a);
+  mq::weight_f16_factors(a, &w.f16_up, &w.f16_down);
+  return hipSuccess;
+}
+
 int mq_weight_upload(mq_ctx* ctx, uint32_t gguf_type, uint64_t stored_rows, uint64_t stored_cols, int transposed,
                      const uint8_t* bytes, size_t len, uint64_t* handle) try {
   if (!ctx || !handle) return fail(ctx, MQ_ERR_ARGUMENT, "mq_weight_upload: null argument");
@@ -665,6 +717,7 @@ int mq_weight_upload(mq_ctx* ctx, uint32_t gguf_type, uint64_t stored_rows, uint
     if (e != hipSuccess) return hip_fail(ctx, e, "hipMalloc(weight)");
     e = hipMemcpyAsync(w.dev, bytes, len, hipMemcpyHostToDevice, ctx->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e == hipSuccess) e = set_f16_range(ctx, w);
     if (e != hipSuccess) {
       (void)hipFree(w.dev);
       return hip_fail(ctx, e, "mq_weight_upload");
@@ -691,6 +744,7 @@ int mq_weight_upload(mq_ctx* ctx, uint32_t gguf_type, uint64_t stored_rows, uint
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
   }
   (void)hipFree(raw);
+  if (e == hipSuccess) e = set_f16_range(ctx, w);
   if (e != hipSuccess) {
     (void)hipFree(w.dev);
     return hip_fail(ctx, e, "mq_weight_upload");
@@ -855,7 +909,7 @@ int mq_quantize_activations_dev(mq_ctx* ctx, const float* x_dev, uint64_t m, uin
     return fail(ctx, MQ_ERR_ARGUMENT, "mq_quantize_activations_dev: null pointer");
   DeviceGuard guard(ctx->device);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  mq::launch_quantize_activations(x_dev, m, k, values_dev, scales_dev, sums_dev, nullptr, 1, s);
+  mq::launch_quantize_activations(x_dev, m, k, values_dev, scales_dev, sums_dev, s);
   MQ_HIP(ctx, hipGetLastError());
   return MQ_OK;
 } MQ_CATCH(ctx)
@@ -903,10 +957,8 @@ int mq_prepare_activations_f16_dev(mq_ctx* ctx, const float* x_dev, uint64_t m, 
   if (!x_dev || !a16_dev) return fail(ctx, MQ_ERR_ARGUMENT, "mq_prepare_activations_f16_dev: null pointer");
   DeviceGuard guard(ctx->device);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (flags & MQ_INT8_ACTIVATIONS)
-    mq::launch_quantize_activations(x_dev, m, k, nullptr, nullptr, nullptr, a16_dev, 1, s);
-  else
-    mq::launch_activations_f16(x_dev, m, k, a16_dev, s);
+  mq::launch_activations_f16(x_dev, m, k, (flags & MQ_INT8_ACTIVATIONS) ? 1 : 0, a16_dev,
+                             reinterpret_cast<float*>(a16_dev + m * k), s);
   MQ_HIP(ctx, hipGetLastError());
   return MQ_OK;
 } MQ_CATCH(ctx)
@@ -933,7 +985,7 @@ int mq_matmul_f16_dev(mq_ctx* ctx, uint64_t handle, const uint16_t* a16_dev, uin
     part = static_cast<float*>(ctx->ws);
   }
   mq::launch_gemm(static_cast<int>(w->type), w->dev, w->rows, w->nb, w->cols, a16_dev, m, y_dev, nullptr, 0,
-                  ctx->gemm_variant, s, part);
+                  ctx->gemm_variant, s, range(*w, reinterpret_cast<const float*>(a16_dev + m * k)), part);
   MQ_HIP(ctx, hipGetLastError());
   return MQ_OK;
 } MQ_CATCH(ctx)

@@ -5,6 +5,7 @@
 // Built with -ffp-contract=off: no multiply-add is fused unless written as
 // fmaf, so the dequantizer reproduces the reference's separately rounded
 // product and difference.
+#include <cmath>
 #include <type_traits>
 
 #include "mq_device.h"
@@ -189,7 +190,7 @@ __device__ inline uint32_t pack_q4(const Quant4& q) {
 
 __global__ void quantize_act_kernel(const float* __restrict__ x, uint64_t total,
                                     int8_t* __restrict__ values, float* __restrict__ scales,
-                                    int32_t* __restrict__ sums, uint16_t* __restrict__ a16, int int8) {
+                                    int32_t* __restrict__ sums) {
   uint64_t t = blockIdx.x * static_cast<uint64_t>(blockDim.x) + threadIdx.x;
   bool active = t < total / 4;
   float4 v = active ? reinterpret_cast<const float4*>(x)[t] : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -200,37 +201,111 @@ __global__ void quantize_act_kernel(const float* __restrict__ x, uint64_t total,
   uint64_t blk = t >> 3;
   if (scales && sub == 0) scales[blk] = q.d;
   if (sums && (sub & 3) == 0) sums[2 * blk + (sub >> 2)] = q.half_sum;
-  if (a16) {
-    float f0, f1, f2, f3;
-    if (int8) {
-      f0 = static_cast<float>(q.q0) * q.d;
-      f1 = static_cast<float>(q.q1) * q.d;
-      f2 = static_cast<float>(q.q2) * q.d;
-      f3 = static_cast<float>(q.q3) * q.d;
-    } else {
-      f0 = v.x;
-      f1 = v.y;
-      f2 = v.z;
-      f3 = v.w;
-    }
-    __half2 h01 = __floats2half2_rn(f0, f1), h23 = __floats2half2_rn(f2, f3);
-    uint2 w;
-    w.x = *reinterpret_cast<uint32_t*>(&h01);
-    w.y = *reinterpret_cast<uint32_t*>(&h23);
-    reinterpret_cast<uint2*>(a16)[t] = w;
-  }
 }
 
-__global__ void activations_f16_kernel(const float* __restrict__ x, uint64_t total,
-                                       uint16_t* __restrict__ a16) {
-  uint64_t t = blockIdx.x * static_cast<uint64_t>(blockDim.x) + threadIdx.x;
-  if (t >= total / 4) return;
-  float4 v = reinterpret_cast<const float4*>(x)[t];
-  __half2 h01 = __floats2half2_rn(v.x, v.y), h23 = __floats2half2_rn(v.z, v.w);
+// The f16 range of the prefill operands. f16 holds magnitudes up to 65504
+// and has full precision only above 2^-14: unscaled, a row of large
+// activations would turn into infinities and a row of tiny ones into
+// subnormals. A power of two 2^e moves the largest magnitude into
+// [2^14, 2^15): multiplying by it is exact in f32, and f16(v 2^e) =
+// f16(v) 2^e wherever f16(v) is a normal number, so only the lost range is
+// changed. Zero rows, and rows whose largest magnitude is infinite, keep
+// e = 0. e stays within [-80, 80] (rows whose largest magnitude lies in
+// [2^-65, 2^95]): with the weight's factor 2^f, f in [-40, 40], the
+// output factor 2^-(e + f) is a normal f32.
+__device__ inline int f16_range_exponent(float amax) {
+  if (!(amax > 0.0f) || amax == __builtin_huge_valf()) return 0;
+  const int ex = __builtin_amdgcn_frexp_expf(amax);  // amax = mantissa 2^ex, mantissa in [0.5, 1)
+  const int e = 15 - ex;
+  return e < -80 ? -80 : (e > 80 ? 80 : e);
+}
+
+// The output factor 2^-(e_r + f) of activation row `row` (clamped into the
+// matrix). Each GEMM work-group loads its tile's factors in its prologue,
+// one per thread, and keeps them in LDS for the epilogue, so that the
+// epilogue's stores wait for no global load.
+__device__ inline float out_factor(const F16Range& rg, uint64_t row, uint64_t m_rows) {
+  return rg.row[row < m_rows ? row : m_rows - 1] * rg.down;
+}
+
+// One work-group per activation row: the row's largest magnitude (NaN
+// ignored), then a16 = f16(v 2^e) with v = x, or the int8 round trip q d of
+// x (quantize_act_kernel's blocks: lanes 8j .. 8j + 7 of a wave hold one
+// 32-value block, since k % 32 == 0), and row_factor = 2^-e. HELD > 0: the
+// row is at most 256 HELD float4, all loaded at once (indices clamped into
+// the row, so no load waits behind a branch) and kept in registers between
+// the two passes; HELD == 0: longer rows, read twice.
+__device__ inline void store_f16x4(uint2* out, int t, float4 v, float up, int int8) {
+  float f0 = v.x, f1 = v.y, f2 = v.z, f3 = v.w;
+  if (int8) {
+    const Quant4 q = quantize4(v);
+    f0 = static_cast<float>(q.q0) * q.d;
+    f1 = static_cast<float>(q.q1) * q.d;
+    f2 = static_cast<float>(q.q2) * q.d;
+    f3 = static_cast<float>(q.q3) * q.d;
+  }
+  __half2 h01 = __floats2half2_rn(f0 * up, f1 * up), h23 = __floats2half2_rn(f2 * up, f3 * up);
   uint2 w;
   w.x = *reinterpret_cast<uint32_t*>(&h01);
   w.y = *reinterpret_cast<uint32_t*>(&h23);
-  reinterpret_cast<uint2*>(a16)[t] = w;
+  out[t] = w;
+}
+
+__device__ inline float absmax4(float4 v) {
+  return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+}
+
+template <int HELD>
+__global__ __launch_bounds__(256) void activations_f16_kernel(const float* __restrict__ x, uint64_t k, int int8,
+                                                              uint16_t* __restrict__ a16,
+                                                              float* __restrict__ row_factor) {
+  const uint64_t row = blockIdx.x;
+  const float4* xr = reinterpret_cast<const float4*>(x + row * k);
+  uint2* out = reinterpret_cast<uint2*>(a16 + row * k);
+  const int n4 = static_cast<int>(k / 4);
+  const int tid = static_cast<int>(threadIdx.x);
+  float4 v[HELD > 0 ? HELD : 1];
+  float amax = 0.0f;
+  if constexpr (HELD > 0) {
+#pragma unroll
+    for (int i = 0; i < HELD; ++i) v[i] = xr[min(tid + 256 * i, n4 - 1)];
+#pragma unroll
+    for (int i = 0; i < HELD; ++i)
+      if (tid + 256 * i < n4) amax = fmaxf(amax, absmax4(v[i]));
+  } else {
+    for (int t = tid; t < n4; t += 256) amax = fmaxf(amax, absmax4(xr[t]));
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+  __shared__ float wave_max[4];
+  if ((tid & 63) == 0) wave_max[tid >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(wave_max[0], wave_max[1]), fmaxf(wave_max[2], wave_max[3]));
+  const int e = f16_range_exponent(amax);
+  const float up = __builtin_amdgcn_ldexpf(1.0f, e);
+  if (tid == 0) row_factor[row] = __builtin_amdgcn_ldexpf(1.0f, -e);
+  // a 32-value block's 8 lanes are all in the row or all past it (n4 % 8
+  // == 0), so the quantization's lane exchanges stay among active lanes
+  if constexpr (HELD > 0) {
+#pragma unroll
+    for (int i = 0; i < HELD; ++i) {
+      const int t = tid + 256 * i;
+      if (t < n4) store_f16x4(out, t, v[i], up, int8);
+    }
+  } else {
+    for (int t = tid; t < n4; t += 256) store_f16x4(out, t, xr[t], up, int8);
+  }
+}
+
+// out = max |x| as f32 bits (non-negative floats order as their bits).
+__global__ __launch_bounds__(256) void absmax_kernel(const float* __restrict__ x, uint64_t n,
+                                                     uint32_t* __restrict__ out) {
+  float amax = 0.0f;
+  for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += static_cast<uint64_t>(gridDim.x) * 256)
+    amax = fmaxf(amax, fabsf(x[i]));
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+  if ((threadIdx.x & 63) == 0) atomicMax(out, __float_as_uint(amax));
 }
 
 // ---------------------------------------------------------------------------
@@ -2841,11 +2916,13 @@ __global__ __launch_bounds__(256) void gemm_kernel(const uint8_t* __restrict__ w
                                                    uint64_t rows_padded, const uint16_t* __restrict__ a16,
                                                    uint64_t m_rows, float* __restrict__ y,
                                                    const float* __restrict__ addend, uint64_t addend_stride,
-                                                   uint64_t kdim) {
+                                                   uint64_t kdim, F16Range rg) {
   __shared__ __attribute__((aligned(16))) uint16_t As[kBM][kLdsK];
   __shared__ __attribute__((aligned(16))) uint16_t Bs[kBN][kLdsK];
+  __shared__ float row_fac[kBM];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const uint64_t m0 = static_cast<uint64_t>(blockIdx.y) * kBM;
+  if (tid < kBM) row_fac[tid] = out_factor(rg, m0 + tid, m_rows);  // read after the loop's barriers
   const uint64_t n0 = static_cast<uint64_t>(blockIdx.x) * kBN;
   const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
   const uint64_t K = kdim;  // the logical row length (a multiple of 32)
@@ -2885,7 +2962,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const uint8_t* __restrict__ w
           plane_run_signed<TYPE>(planes, d_bits, 2 * c + h, q, sc, mn);
 #pragma unroll
           for (int t = 0; t < 8; ++t) {
-            const float s = sc[t >> 2], m = mn[t >> 2];
+            const float s = sc[t >> 2] * rg.up, m = mn[t >> 2] * rg.up;
             out[2 * t] = pack_f16x2(fmaf(s, static_cast<float>(static_cast<int8_t>(byte_of(q[t], 0))), -m),
                                     fmaf(s, static_cast<float>(static_cast<int8_t>(byte_of(q[t], 1))), -m));
             out[2 * t + 1] = pack_f16x2(fmaf(s, static_cast<float>(static_cast<int8_t>(byte_of(q[t], 2))), -m),
@@ -2899,7 +2976,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const uint8_t* __restrict__ w
           uint32_t sc0, mm0, sc1, mm1;
           q4k_sc_m(six, 2 * c, sc0, mm0);
           q4k_sc_m(six, 2 * c + 1, sc1, mm1);
-          const float d = half_bits(hdr.x), dmin = half_bits(hdr.x >> 16);
+          const float d = half_bits(hdr.x) * rg.up, dmin = half_bits(hdr.x >> 16) * rg.up;
           const float s0 = d * static_cast<float>(sc0), s1 = d * static_cast<float>(sc1);
           const float mn0 = dmin * static_cast<float>(mm0), mn1 = dmin * static_cast<float>(mm1);
           const uint32_t wv[4] = {qq.x, qq.y, qq.z, qq.w};
@@ -2920,7 +2997,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const uint8_t* __restrict__ w
           const uint8_t* tile = w + ((n >> 3) * nb + b) * kIq4xsTileBytes;
           const uint2 hdr = ld8(tile + (n & 7) * 8);
           const uint4 qq = ld16(tile + 64 + 128 * j + (n & 7) * 16);
-          const float sj = half_bits(hdr.x) * static_cast<float>(iq4xs_ls(hdr, j));
+          const float sj = half_bits(hdr.x) * rg.up * static_cast<float>(iq4xs_ls(hdr, j));
           const uint32_t wv[4] = {qq.x, qq.y, qq.z, qq.w};
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
@@ -2971,6 +3048,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(const uint8_t* __restrict__ w
   // D layout: lane holds column (lane & 15), rows 4 * (lane >> 4) + e.
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
+    float rf[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) rf[e] = row_fac[wm + 16 * i + 4 * (lane >> 4) + e];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint64_t col = n0 + wn + 16 * j + (lane & 15);
@@ -2978,7 +3058,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const uint8_t* __restrict__ w
       for (int e = 0; e < 4; ++e) {
         const uint64_t row = m0 + wm + 16 * i + 4 * (lane >> 4) + e;
         if (row < m_rows && col < rows) {
-          float v = acc[i][j][e];
+          float v = acc[i][j][e] * rf[e];
           if (addend) v = v + addend[row * addend_stride + col];
           y[row * rows + col] = v;
         }
@@ -3052,7 +3132,7 @@ __device__ inline void load_raw_b_iq4(RawB<kTypeIq4Xs, NF>& r, const uint8_t* co
 }
 
 template <int TYPE, int NF, int C>
-__device__ inline void dequant_b(const RawB<TYPE, NF>& r, int kq, half8 (&bop)[2][NF]) {
+__device__ inline void dequant_b(const RawB<TYPE, NF>& r, int kq, float up, half8 (&bop)[2][NF]) {
 #pragma unroll
   for (int f = 0; f < NF; ++f) {
     uint32_t p0[4], p1[4];
@@ -3061,7 +3141,7 @@ __device__ inline void dequant_b(const RawB<TYPE, NF>& r, int kq, half8 (&bop)[2
       uint32_t sc0, mm0, sc1, mm1;
       q4k_sc_m(six, 2 * C, sc0, mm0);
       q4k_sc_m(six, 2 * C + 1, sc1, mm1);
-      const float d = half_bits(r.hdr[f].x), dmin = half_bits(r.hdr[f].x >> 16);
+      const float d = half_bits(r.hdr[f].x) * up, dmin = half_bits(r.hdr[f].x >> 16) * up;
       const float s0 = d * static_cast<float>(sc0), s1 = d * static_cast<float>(sc1);
       const float n0m = -(dmin * static_cast<float>(mm0)), n1m = -(dmin * static_cast<float>(mm1));
       const uint2 qa = r.qa[C][f];
@@ -3080,7 +3160,7 @@ __device__ inline void dequant_b(const RawB<TYPE, NF>& r, int kq, half8 (&bop)[2
       }
     } else {
       const uint2 h2 = make_uint2(r.hdr[f].x, r.hdr[f].y);
-      const float d = half_bits(h2.x);
+      const float d = half_bits(h2.x) * up;
       const float sa = d * static_cast<float>(iq4xs_ls(h2, 2 * C));
       const float sb = d * static_cast<float>(iq4xs_ls(h2, 2 * C + 1));
       const int sh = 4 * (kq >> 1);  // low nibbles hold weights 0..15, high 16..31
@@ -3177,7 +3257,7 @@ __device__ inline void load_raw_pb(RawPB<TYPE, NF>& r, const uint8_t* const (&ti
 // K-step C (runs 2C, 2C + 1) of the plane formats as MFMA B operands:
 // value = scale * q - min, rounded once to f16.
 template <int TYPE, int NF, int C>
-__device__ inline void dequant_pb(const RawPB<TYPE, NF>& r, int kq, half8 (&bop)[2][NF]) {
+__device__ inline void dequant_pb(const RawPB<TYPE, NF>& r, int kq, float up, half8 (&bop)[2][NF]) {
 #pragma unroll
   for (int f = 0; f < NF; ++f) {
 #pragma unroll
@@ -3231,6 +3311,8 @@ __device__ inline void dequant_pb(const RawPB<TYPE, NF>& r, int kq, half8 (&bop)
         const int si = 8 * hh + 2 * g + (kq >> 1);
         sc = half_bits(r.dsh[f]) * static_cast<float>(static_cast<int8_t>(byte_of(word_of(r.hdr[f], si >> 2), si & 3)));
       }
+      sc *= up;
+      mn *= up;
       uint32_t p[4];
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
@@ -3245,19 +3327,22 @@ __device__ inline void dequant_pb(const RawPB<TYPE, NF>& r, int kq, half8 (&bop)
 }
 
 template <int TYPE, int MF, int NF>
-__global__ __launch_bounds__(256) void gemm_rb_kernel(const uint8_t* __restrict__ w, int nb, uint64_t rows,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NF == 2 ? 2 : 1))) void gemm_rb_kernel(const uint8_t* __restrict__ w, int nb, uint64_t rows,
                                                       uint64_t rows_padded, const uint16_t* __restrict__ a16,
                                                       uint64_t m_rows, float* __restrict__ y,
-                                                      const float* __restrict__ addend, uint64_t addend_stride) {
+                                                      const float* __restrict__ addend, uint64_t addend_stride,
+                                                      F16Range rg) {
   constexpr int BM = MF * 16;
   constexpr int LDK = kBK + 8;  // halves per LDS row (16-byte pad)
   constexpr int A_CHUNKS = BM * kBK / 8 / 256;  // 16-byte chunks per thread per K-step
   __shared__ __attribute__((aligned(16))) uint16_t As[2][BM][LDK];
+  __shared__ float row_fac[BM];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int li = lane & 15, kq = lane >> 4;
   const uint64_t m0 = static_cast<uint64_t>(blockIdx.y) * BM;
   const uint64_t n0 = static_cast<uint64_t>(blockIdx.x) * (4 * NF * 16) + static_cast<uint64_t>(wave) * NF * 16;
   const uint64_t K = static_cast<uint64_t>(nb) * 256;
+  const float my_fac = tid < BM ? out_factor(rg, m0 + tid, m_rows) : 0.0f;
   // split-K over gridDim.z work-groups: super-blocks [bl, bh) of the row,
   // results to the split's own [m_rows][rows] slice of y (the partials,
   // which the host sums in split order)
@@ -3321,6 +3406,7 @@ __global__ __launch_bounds__(256) void gemm_rb_kernel(const uint8_t* __restrict_
   uint4 areg[A_CHUNKS];
   load_a(4 * bl, areg);
   store_a(0, areg);  // K-step 4 bl is even: buffer 0
+  if (tid < BM) row_fac[tid] = my_fac;
   __syncthreads();
 
   auto kstep = [&](int kb, const half8 (&bop)[2][NF]) {
@@ -3346,28 +3432,31 @@ __global__ __launch_bounds__(256) void gemm_rb_kernel(const uint8_t* __restrict_
     if (b + 1 < bh) load_b(nxt, static_cast<uint64_t>(b + 1));
     half8 bop[2][NF];
     if constexpr (is_plane_format(TYPE)) {
-      dequant_pb<TYPE, NF, 0>(cur, kq, bop);
+      dequant_pb<TYPE, NF, 0>(cur, kq, rg.up, bop);
       kstep(4 * b + 0, bop);
-      dequant_pb<TYPE, NF, 1>(cur, kq, bop);
+      dequant_pb<TYPE, NF, 1>(cur, kq, rg.up, bop);
       kstep(4 * b + 1, bop);
-      dequant_pb<TYPE, NF, 2>(cur, kq, bop);
+      dequant_pb<TYPE, NF, 2>(cur, kq, rg.up, bop);
       kstep(4 * b + 2, bop);
-      dequant_pb<TYPE, NF, 3>(cur, kq, bop);
+      dequant_pb<TYPE, NF, 3>(cur, kq, rg.up, bop);
       kstep(4 * b + 3, bop);
     } else {
-      dequant_b<TYPE, NF, 0>(cur, kq, bop);
+      dequant_b<TYPE, NF, 0>(cur, kq, rg.up, bop);
       kstep(4 * b + 0, bop);
-      dequant_b<TYPE, NF, 1>(cur, kq, bop);
+      dequant_b<TYPE, NF, 1>(cur, kq, rg.up, bop);
       kstep(4 * b + 1, bop);
-      dequant_b<TYPE, NF, 2>(cur, kq, bop);
+      dequant_b<TYPE, NF, 2>(cur, kq, rg.up, bop);
       kstep(4 * b + 2, bop);
-      dequant_b<TYPE, NF, 3>(cur, kq, bop);
+      dequant_b<TYPE, NF, 3>(cur, kq, rg.up, bop);
       kstep(4 * b + 3, bop);
     }
   }
 
 #pragma unroll
   for (int i = 0; i < MF; ++i) {
+    float rf[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) rf[e] = row_fac[16 * i + 4 * kq + e];
 #pragma unroll
     for (int f = 0; f < NF; ++f) {
       const uint64_t col = n0 + 16 * f + li;
@@ -3375,7 +3464,7 @@ __global__ __launch_bounds__(256) void gemm_rb_kernel(const uint8_t* __restrict_
       for (int e = 0; e < 4; ++e) {
         const uint64_t row = m0 + 16 * i + 4 * kq + e;
         if (row < m_rows && col < rows) {
-          float v = acc[i][f][e];
+          float v = acc[i][f][e] * rf[e];
           if (addend) v = v + addend[row * addend_stride + col];
           y[row * rows + col] = v;
         }
@@ -3458,14 +3547,14 @@ struct KsScales {
 
 // Scales of chunk C (runs 2C, 2C + 1) for both fragments.
 template <int C>
-__device__ inline void ks_scales(const uint4 (&hdr)[2], KsScales& cs) {
+__device__ inline void ks_scales(const uint4 (&hdr)[2], float up, KsScales& cs) {
 #pragma unroll
   for (int f = 0; f < 2; ++f) {
     const Q4kSixBit six = q4k_six_bit(hdr[f]);
     uint32_t sc0, mm0, sc1, mm1;
     q4k_sc_m(six, 2 * C, sc0, mm0);
     q4k_sc_m(six, 2 * C + 1, sc1, mm1);
-    const float d = half_bits(hdr[f].x), dmin = half_bits(hdr[f].x >> 16);
+    const float d = half_bits(hdr[f].x) * up, dmin = half_bits(hdr[f].x >> 16) * up;
     const float s0 = d * static_cast<float>(sc0), s1 = d * static_cast<float>(sc1) * 0.0625f;
     cs.s[0][f] = s0;
     cs.s[1][f] = s1;
@@ -3498,13 +3587,17 @@ __global__ __launch_bounds__(kKsThreads) void gemm_ks_kernel(const uint8_t* __re
                                                               uint64_t rows_padded, const uint16_t* __restrict__ a16,
                                                               uint64_t m_rows, float* __restrict__ y,
                                                               const float* __restrict__ addend,
-                                                              uint64_t addend_stride) {
+                                                              uint64_t addend_stride, F16Range rg) {
   constexpr int MF = 4, NF = 2, D = kKsDma;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * 4 * kKsStage];  // [kw][stage]
+  __shared__ float row_fac[kKsBM];
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int nw = wave & 3, kw = wave >> 2;
   const int l32 = lane & 31, kh = lane >> 5;
   const uint64_t m0 = static_cast<uint64_t>(blockIdx.y) * kKsBM;
+  // the tile's output factors: loaded before the weight and activation
+  // prefetches, so the prologue's vmcnt wait covers them
+  const float my_fac = tid < kKsBM ? out_factor(rg, m0 + tid, m_rows) : 0.0f;
   const uint64_t n0 = static_cast<uint64_t>(blockIdx.x) * kKsBN + static_cast<uint64_t>(nw) * 64;
   const uint64_t K = static_cast<uint64_t>(nb) * 256;
   const int nbh = (nb + 1) / 2, sb0 = kw * nbh;
@@ -3599,11 +3692,12 @@ __global__ __launch_bounds__(kKsThreads) void gemm_ks_kernel(const uint8_t* __re
   dma(1, 1);
   dma(2, 2);
   __builtin_amdgcn_s_waitcnt(wait_vmcnt(2 * D));  // stage 0 (and every B load) complete
+  if (tid < kKsBM) row_fac[tid] = my_fac;  // read in the epilogue, after the K loop's barriers
   wg_barrier();
   half8 af[MF], an[MF], bc[NF], bn[NF];
   read_a(0, 0, af);
   KsScales sc_cur, sc_nxt;
-  ks_scales<0>(hb[0], sc_cur);
+  ks_scales<0>(hb[0], rg.up, sc_cur);
   ks_slice<0>(qb[0], sc_cur, bc);
 
   // Slice SL of K-step j = 4 bl + C: read the next slice's A, dequantize the
@@ -3614,7 +3708,7 @@ __global__ __launch_bounds__(kKsThreads) void gemm_ks_kernel(const uint8_t* __re
     if (SL < 3) {                                                                              \
       ks_slice<(SL + 1) % 4>(qb[C], sc_cur, bn);                                               \
     } else {                                                                                   \
-      if (C < 3) ks_scales<(C + 1) % 4>(hb[HB], sc_nxt); else ks_scales<0>(hb[HB ^ 1], sc_nxt); \
+      if (C < 3) ks_scales<(C + 1) % 4>(hb[HB], rg.up, sc_nxt); else ks_scales<0>(hb[HB ^ 1], rg.up, sc_nxt); \
       ks_slice<0>(qb[(C + 1) % 4], sc_nxt, bn);                                                \
     }                                                                                          \
     _Pragma("unroll") for (int i = 0; i < MF; ++i)                                             \
@@ -3680,7 +3774,10 @@ __global__ __launch_bounds__(kKsThreads) void gemm_ks_kernel(const uint8_t* __re
   if (kw == 0) {
     // D layout (32 x 32): lane holds column l32, rows 8 g + 4 kh + e of fragment element 4 g + e
 #pragma unroll
-    for (int i = 0; i < MF; ++i)
+    for (int i = 0; i < MF; ++i) {
+      float rf[16];
+#pragma unroll
+      for (int ge = 0; ge < 16; ++ge) rf[ge] = row_fac[32 * i + 8 * (ge >> 2) + 4 * kh + (ge & 3)];
 #pragma unroll
       for (int f = 0; f < NF; ++f) {
         const uint64_t col = n0 + 32 * f + l32;
@@ -3692,13 +3789,14 @@ __global__ __launch_bounds__(kKsThreads) void gemm_ks_kernel(const uint8_t* __re
           for (int e = 0; e < 4; ++e) {
             const uint64_t row = m0 + 32 * i + 8 * g + 4 * kh + e;
             if (row < m_rows && col < rows) {
-              float v = acc[i][f][4 * g + e] + ov[e];
+              float v = (acc[i][f][4 * g + e] + ov[e]) * rf[4 * g + e];
               if (addend) v = v + addend[row * addend_stride + col];
               y[row * rows + col] = v;
             }
           }
         }
       }
+    }
   }
 }
 
@@ -3785,12 +3883,12 @@ __device__ inline void load_raw_g(RawG<NF, DEPTH>& r, const uint8_t* const (&blk
 // and scale arithmetic as grid_run).
 template <int TYPE, int NF, int DEPTH>
 __device__ inline void dequant_g(const RawG<NF, DEPTH>& r, const uint32_t (&dbits)[NF], int j, int q, int l,
-                                 const uint8_t* glds, const uint4* smask, half8 (&bop)[NF]) {
+                                 const uint8_t* glds, const uint4* smask, float up, half8 (&bop)[NF]) {
   const uint2* g64 = reinterpret_cast<const uint2*>(glds);
   const uint32_t* g32 = reinterpret_cast<const uint32_t*>(glds);
 #pragma unroll
   for (int f = 0; f < NF; ++f) {
-    const float d = half_bits(dbits[f]);
+    const float d = half_bits(dbits[f]) * up;
     uint32_t m0, m1, sg;
     float s;
     if constexpr (TYPE == kTypeIq2Xxs) {
@@ -3849,7 +3947,7 @@ template <int TYPE, int MF, int NF>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NF == 2 ? 2 : 1))) void gemm_grid_kernel(const uint8_t* __restrict__ w, int nb, uint64_t rows,
                                                         const uint16_t* __restrict__ a16, uint64_t m_rows,
                                                         float* __restrict__ y, const float* __restrict__ addend,
-                                                        uint64_t addend_stride) {
+                                                        uint64_t addend_stride, F16Range rg) {
   constexpr int BM = MF * 16;
   constexpr int LDK = kBK + 8;                  // halves per LDS row (16-byte pad)
   constexpr int A_CHUNKS = BM * kBK / 8 / 256;  // 16-byte chunks per thread per K-step
@@ -3857,9 +3955,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NF == 2 ? 2
   __shared__ __attribute__((aligned(16))) uint16_t As[2][BM][LDK];
   __shared__ __attribute__((aligned(16))) uint8_t glds[GBYTES];
   __shared__ uint4 smask[256];
+  __shared__ float row_fac[BM];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int li = lane & 15, kq = lane >> 4;
   const uint64_t m0 = static_cast<uint64_t>(blockIdx.y) * BM;
+  const float my_fac = tid < BM ? out_factor(rg, m0 + tid, m_rows) : 0.0f;
   const uint64_t n0 = static_cast<uint64_t>(blockIdx.x) * (4 * NF * 16) + static_cast<uint64_t>(wave) * NF * 16;
   const uint64_t K = static_cast<uint64_t>(nb) * 256;
   // split-K over gridDim.z: super-blocks [bl, bh), results to the split's
@@ -3928,6 +4028,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NF == 2 ? 2
   uint4 areg[A_CHUNKS];
   load_a(4 * bl, areg);
   store_a(0, areg);  // K-step 4 bl is even: buffer 0
+  if (tid < BM) row_fac[tid] = my_fac;
   __syncthreads();
 
   auto kstep = [&](int kb, const half8 (&bop)[2][NF]) {
@@ -3951,8 +4052,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NF == 2 ? 2
   auto step = [&](int b, auto cc) {
     constexpr int C = decltype(cc)::value, Q = 2 * (C % DEPTH);
     half8 bop[2][NF];
-    dequant_g<TYPE, NF, DEPTH>(raw, dcur, 2 * C, Q, kq, glds, smask, bop[0]);
-    dequant_g<TYPE, NF, DEPTH>(raw, dcur, 2 * C + 1, Q + 1, kq, glds, smask, bop[1]);
+    dequant_g<TYPE, NF, DEPTH>(raw, dcur, 2 * C, Q, kq, glds, smask, rg.up, bop[0]);
+    dequant_g<TYPE, NF, DEPTH>(raw, dcur, 2 * C + 1, Q + 1, kq, glds, smask, rg.up, bop[1]);
     // refill the slot with K-step C + DEPTH (this block's, or the next's)
     constexpr int CN = (C + DEPTH) % 4;
     const int bn = b + (C + DEPTH) / 4;
@@ -3974,6 +4075,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NF == 2 ? 2
 
 #pragma unroll
   for (int i = 0; i < MF; ++i) {
+    float rf[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) rf[e] = row_fac[16 * i + 4 * kq + e];
 #pragma unroll
     for (int f = 0; f < NF; ++f) {
       const uint64_t col = n0 + 16 * f + li;
@@ -3981,7 +4085,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NF == 2 ? 2
       for (int e = 0; e < 4; ++e) {
         const uint64_t row = m0 + 16 * i + 4 * kq + e;
         if (row < m_rows && col < rows) {
-          float v = acc[i][f][e];
+          float v = acc[i][f][e] * rf[e];
           if (addend) v = v + addend[row * addend_stride + col];
           y[row * rows + col] = v;
         }
@@ -4021,16 +4125,46 @@ void launch_dequantize(int type, const uint8_t* tiled, uint64_t rows, uint64_t n
 }
 
 void launch_quantize_activations(const float* x, uint64_t m, uint64_t k, int8_t* values, float* scales,
-                                 int32_t* sums, uint16_t* a16, int int8, hipStream_t stream) {
+                                 int32_t* sums, hipStream_t stream) {
   uint64_t total = m * k;
   hipLaunchKernelGGL(quantize_act_kernel, dim3(grid_for(total / 4, 256)), dim3(256), 0, stream, x, total,
-                     values, scales, sums, a16, int8);
+                     values, scales, sums);
 }
 
-void launch_activations_f16(const float* x, uint64_t m, uint64_t k, uint16_t* a16, hipStream_t stream) {
-  uint64_t total = m * k;
-  hipLaunchKernelGGL(activations_f16_kernel, dim3(grid_for(total / 4, 256)), dim3(256), 0, stream, x, total,
-                     a16);
+void launch_activations_f16(const float* x, uint64_t m, uint64_t k, int int8, uint16_t* a16, float* row_factor,
+                            hipStream_t stream) {
+  const uint64_t held = (k / 4 + 255) / 256;
+  switch (held) {
+#define X(H)                                                                                                     \
+  case H:                                                                                                        \
+    hipLaunchKernelGGL(activations_f16_kernel<H>, dim3(static_cast<unsigned>(m)), dim3(256), 0, stream, x, k, int8, \
+                       a16, row_factor);                                                                         \
+    return;
+    X(1) X(2) X(3) X(4) X(5) X(6) X(7) X(8) X(9) X(10) X(11) X(12) X(13) X(14) X(15) X(16)
+#undef X
+    default:
+      hipLaunchKernelGGL(activations_f16_kernel<0>, dim3(static_cast<unsigned>(m)), dim3(256), 0, stream, x, k, int8,
+                         a16, row_factor);
+  }
+}
+
+void weight_f16_factors(float amax, float* up, float* down) {
+  int e = 0;
+  if (amax > 0.0f && std::isfinite(amax)) {
+    int ex = 0;
+    (void)std::frexp(amax, &ex);
+    e = 15 - ex;  // the weight's exponent range lies within [-40, 40]
+    e = e < -40 ? -40 : (e > 40 ? 40 : e);
+  }
+  *up = std::ldexp(1.0f, e);
+  *down = std::ldexp(1.0f, -e);
+}
+
+void launch_absmax(const float* x, uint64_t n, uint32_t* out, hipStream_t stream) {
+  uint64_t groups = grid_for(n, 256);
+  if (groups > 2048) groups = 2048;
+  if (groups == 0) return;
+  hipLaunchKernelGGL(absmax_kernel, dim3(static_cast<unsigned>(groups)), dim3(256), 0, stream, x, n, out);
 }
 
 int gemv_default_splits(uint64_t rows, uint64_t nb, uint64_t m, int variant) {
@@ -4701,7 +4835,8 @@ namespace {
 
 template <int MF, int NF>
 void launch_gemm_rb(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, const uint16_t* a16, uint64_t m,
-                    float* y, const float* addend, uint64_t addend_stride, hipStream_t stream, int ks = 1) {
+                    float* y, const float* addend, uint64_t addend_stride, F16Range rg, hipStream_t stream,
+                    int ks = 1) {
   const uint64_t rows_padded = (rows + 7) / 8 * 8;
   const uint64_t bn = 4 * NF * 16, bm = MF * 16;
   dim3 grid(static_cast<unsigned>((rows + bn - 1) / bn), static_cast<unsigned>((m + bm - 1) / bm),
@@ -4710,7 +4845,7 @@ void launch_gemm_rb(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, 
 #define X(T)                                                                                                     \
   case T:                                                                                                        \
     hipLaunchKernelGGL((gemm_rb_kernel<T, MF, NF>), grid, dim3(256), 0, stream, tiled, static_cast<int>(nb), rows, \
-                       rows_padded, a16, m, y, addend, addend_stride);                                          \
+                       rows_padded, a16, m, y, addend, addend_stride, rg);                                      \
     break;
     MQ_ALL_TYPES(X)
 #undef X
@@ -4721,7 +4856,8 @@ void launch_gemm_rb(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, 
 
 template <int MF, int NF>
 void launch_gemm_grid(int type, const uint8_t* w, uint64_t rows, uint64_t nb, const uint16_t* a16, uint64_t m,
-                      float* y, const float* addend, uint64_t addend_stride, hipStream_t stream, int ks = 1) {
+                      float* y, const float* addend, uint64_t addend_stride, F16Range rg, hipStream_t stream,
+                      int ks = 1) {
   const uint64_t bn = 4 * NF * 16, bm = MF * 16;
   dim3 grid(static_cast<unsigned>((rows + bn - 1) / bn), static_cast<unsigned>((m + bm - 1) / bm),
             static_cast<unsigned>(ks));
@@ -4729,7 +4865,7 @@ void launch_gemm_grid(int type, const uint8_t* w, uint64_t rows, uint64_t nb, co
 #define X(T)                                                                                                    \
   case T:                                                                                                       \
     hipLaunchKernelGGL((gemm_grid_kernel<T, MF, NF>), grid, dim3(256), 0, stream, w, static_cast<int>(nb), rows, \
-                       a16, m, y, addend, addend_stride);                                                      \
+                       a16, m, y, addend, addend_stride, rg);                                                  \
     break;
     MQ_GRID_TYPES(X)
 #undef X
@@ -4796,13 +4932,13 @@ int gemm_splits(int type, uint64_t rows, uint64_t m, uint64_t nb, uint64_t k, in
 
 void launch_gemm(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, uint64_t k, const uint16_t* a16,
                  uint64_t m, float* y, const float* addend, uint64_t addend_stride, int variant,
-                 hipStream_t stream, float* part) {
+                 hipStream_t stream, F16Range rg, float* part) {
   const int ks = part ? gemm_splits(type, rows, m, nb, k, variant) : 1;
   if (ks > 1 && is_grid_format(type)) {
     if (variant == 2)
-      launch_gemm_grid<8, 4>(type, tiled, rows, nb, a16, m, part, nullptr, 0, stream, ks);
+      launch_gemm_grid<8, 4>(type, tiled, rows, nb, a16, m, part, nullptr, 0, rg, stream, ks);
     else
-      launch_gemm_grid<8, 2>(type, tiled, rows, nb, a16, m, part, nullptr, 0, stream, ks);
+      launch_gemm_grid<8, 2>(type, tiled, rows, nb, a16, m, part, nullptr, 0, rg, stream, ks);
     hipLaunchKernelGGL(gemm_split_reduce_kernel, dim3(grid_for(m * rows, 256)), dim3(256), 0, stream, part, ks, m,
                        rows, y, addend, addend_stride);
     return;
@@ -4811,11 +4947,11 @@ void launch_gemm(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, uin
     // the register-B form over ks K ranges into `part`, then their sum
     const int v = variant == 0 ? gemm_default_variant(type, rows, m) : (variant == 5 ? 3 : variant);
     if (v == 2)
-      launch_gemm_rb<8, 4>(type, tiled, rows, nb, a16, m, part, nullptr, 0, stream, ks);
+      launch_gemm_rb<8, 4>(type, tiled, rows, nb, a16, m, part, nullptr, 0, rg, stream, ks);
     else if (v == 4)
-      launch_gemm_rb<4, 4>(type, tiled, rows, nb, a16, m, part, nullptr, 0, stream, ks);
+      launch_gemm_rb<4, 4>(type, tiled, rows, nb, a16, m, part, nullptr, 0, rg, stream, ks);
     else
-      launch_gemm_rb<8, 2>(type, tiled, rows, nb, a16, m, part, nullptr, 0, stream, ks);
+      launch_gemm_rb<8, 2>(type, tiled, rows, nb, a16, m, part, nullptr, 0, rg, stream, ks);
     hipLaunchKernelGGL(gemm_split_reduce_kernel, dim3(grid_for(m * rows, 256)), dim3(256), 0, stream, part, ks, m,
                        rows, y, addend, addend_stride);
     return;
@@ -4826,9 +4962,9 @@ void launch_gemm(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, uin
     // grid formats: raw blocks, whole super-blocks (k % 256 == 0)
     if (variant == 0) variant = tiles(rows, m, 256, 128) >= 1024 ? 2 : 3;
     if (variant == 2)
-      launch_gemm_grid<8, 4>(type, tiled, rows, nb, a16, m, y, addend, addend_stride, stream);
+      launch_gemm_grid<8, 4>(type, tiled, rows, nb, a16, m, y, addend, addend_stride, rg, stream);
     else
-      launch_gemm_grid<8, 2>(type, tiled, rows, nb, a16, m, y, addend, addend_stride, stream);
+      launch_gemm_grid<8, 2>(type, tiled, rows, nb, a16, m, y, addend, addend_stride, rg, stream);
     return;
   }
   // plane formats whose rows end inside a group take the LDS-B form
@@ -4838,7 +4974,7 @@ void launch_gemm(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, uin
 #define X(T)                                                                                                       \
   case T:                                                                                                          \
     hipLaunchKernelGGL(gemm_kernel<T>, grid, dim3(256), 0, stream, tiled, static_cast<int>(nb), rows, rows_padded, \
-                       a16, m, y, addend, addend_stride, k);                                                       \
+                       a16, m, y, addend, addend_stride, k, rg);                                                   \
     return;
       X(kTypeQ8_0) X(kTypeQ4_0) X(kTypeIq4Nl) X(kTypeQ2K) X(kTypeQ3K) X(kTypeQ5K) X(kTypeQ6K)
 #undef X
@@ -4852,27 +4988,27 @@ void launch_gemm(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, uin
     case 5: {
       dim3 ks_grid(static_cast<unsigned>((rows + kKsBN - 1) / kKsBN), static_cast<unsigned>((m + kKsBM - 1) / kKsBM));
       hipLaunchKernelGGL(gemm_ks_kernel, ks_grid, dim3(kKsThreads), 0, stream, tiled, static_cast<int>(nb), rows,
-                         rows_padded, a16, m, y, addend, addend_stride);
+                         rows_padded, a16, m, y, addend, addend_stride, rg);
       return;
     }
     case 2:
-      launch_gemm_rb<8, 4>(type, tiled, rows, nb, a16, m, y, addend, addend_stride, stream);
+      launch_gemm_rb<8, 4>(type, tiled, rows, nb, a16, m, y, addend, addend_stride, rg, stream);
       return;
     case 3:
-      launch_gemm_rb<8, 2>(type, tiled, rows, nb, a16, m, y, addend, addend_stride, stream);
+      launch_gemm_rb<8, 2>(type, tiled, rows, nb, a16, m, y, addend, addend_stride, rg, stream);
       return;
     case 4:
-      launch_gemm_rb<4, 4>(type, tiled, rows, nb, a16, m, y, addend, addend_stride, stream);
+      launch_gemm_rb<4, 4>(type, tiled, rows, nb, a16, m, y, addend, addend_stride, rg, stream);
       return;
     default:
       break;
   }
   if (type == kTypeQ4K)
     hipLaunchKernelGGL(gemm_kernel<kTypeQ4K>, grid, dim3(256), 0, stream, tiled, static_cast<int>(nb), rows,
-                       rows_padded, a16, m, y, addend, addend_stride, k);
+                       rows_padded, a16, m, y, addend, addend_stride, k, rg);
   else
     hipLaunchKernelGGL(gemm_kernel<kTypeIq4Xs>, grid, dim3(256), 0, stream, tiled, static_cast<int>(nb), rows,
-                       rows_padded, a16, m, y, addend, addend_stride, k);
+                       rows_padded, a16, m, y, addend, addend_stride, k, rg);
 }
 
 }  // namespace mq

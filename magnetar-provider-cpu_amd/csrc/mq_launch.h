@@ -17,15 +17,29 @@ void launch_repack(int type, const uint8_t* raw, uint64_t rows, uint64_t nb,
 void launch_dequantize(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb,
                        int logical, float* out, hipStream_t stream);
 
-// Int8 activation quantization of x[m][k] per 32-value block; a16 (may be
-// null) receives f16(q * d) when int8 != 0, else f16(x).
+// Int8 activation quantization of x[m][k] per 32-value block (k % 32 == 0).
 void launch_quantize_activations(const float* x, uint64_t m, uint64_t k, int8_t* values,
-                                 float* scales, int32_t* sums, uint16_t* a16, int int8,
-                                 hipStream_t stream);
+                                 float* scales, int32_t* sums, hipStream_t stream);
 
-// f16 copy of x (f32 activations for the MFMA path), no int8 outputs.
-void launch_activations_f16(const float* x, uint64_t m, uint64_t k, uint16_t* a16,
-                            hipStream_t stream);
+// The prefill GEMM's activation operand: a16[m][k] = f16(v * 2^e_r), v =
+// the int8 round trip q d of x (int8 != 0) or x itself, with e_r the power
+// of two that puts row r's largest magnitude in [2^14, 2^15) (0 for rows of
+// zeros or with an infinity), and row_factor[r] = 2^-e_r. k % 32 == 0.
+void launch_activations_f16(const float* x, uint64_t m, uint64_t k, int int8, uint16_t* a16,
+                            float* row_factor, hipStream_t stream);
+
+// The power of two 2^f that puts a weight's largest dequantized magnitude
+// `amax` in [2^14, 2^15) (1 for zero or non-finite amax). The GEMMs scale
+// dequantized values by `up` = 2^f and outputs by `down` = 2^-f.
+struct F16Range {
+  const float* row = nullptr;  // activation row factors 2^-e_r (launch_activations_f16)
+  float up = 1.0f, down = 1.0f;
+};
+void weight_f16_factors(float amax, float* up, float* down);
+
+// out[0] = max |x[i]| over n floats as f32 bits (NaN ignored); out[0] must
+// hold 0 (or an earlier maximum) before the launch.
+void launch_absmax(const float* x, uint64_t n, uint32_t* out, hipStream_t stream);
 
 // Split-K across work-groups for the LDS-staged GEMV: ks work-groups share
 // each 64-row block; partials holds ks * m * 2 * (row blocks * 64) f32 and
@@ -114,9 +128,11 @@ void launch_gemv_f32(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb,
 // part: gemm_splits(...) * m * rows floats of workspace for the split-K
 // partials of an under-filled register-B or grid-format GEMM (nullptr: no
 // split).
+// rg: the activation row factors and the weight's factors; the product is
+// (a16 . (up dequant(W))^T) row[r] down, exact powers of two.
 void launch_gemm(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, uint64_t k,
                  const uint16_t* a16, uint64_t m, float* y, const float* addend, uint64_t addend_stride,
-                 int variant, hipStream_t stream, float* part = nullptr);
+                 int variant, hipStream_t stream, F16Range rg, float* part = nullptr);
 // Split-K factor of that GEMM (register-B and grid-format forms; 1: none).
 int gemm_splits(int type, uint64_t rows, uint64_t m, uint64_t nb, uint64_t k, int variant);
 int gemm_default_variant(int type, uint64_t rows, uint64_t m);

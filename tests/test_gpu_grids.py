@@ -75,6 +75,29 @@ def test_gemv_every_m(gctx, fmt, int8):
         h.release()
 
 
+@pytest.mark.parametrize("fmt", [IQ2_XXS, IQ3_S])
+def test_prefill_huge_block_scales(gctx, fmt):
+    """Block scales near 65504 (dequantized values far beyond f16's range):
+    the grid GEMM's f16 operands stay in range through the weight's
+    power-of-two factor; both activation modes meet the dense oracle's bar."""
+    m, n, k = 96, 300, 1024
+    w = packed(fmt, n, k, 51 + fmt).copy()
+    blocks = w.reshape(n, k // 256, -1)  # a view: each block's f16 d is bytes 0-1
+    bits = blocks[:, :, 0].astype(np.uint16) | (blocks[:, :, 1].astype(np.uint16) << 8)
+    bits = (bits & np.uint16(0x83FF)) | np.uint16(29 << 10)
+    blocks[:, :, 0] = (bits & 0xFF).astype(np.uint8)
+    blocks[:, :, 1] = (bits >> 8).astype(np.uint8)
+    x = activations(m, k, 52)
+    h = gctx.upload(fmt, n, k, w)
+    try:
+        for int8 in (True, False):
+            got = gctx.matmul(h, x, int8=int8)
+            assert np.isfinite(got).all()
+            assert_row_tolerance(got, dense(fmt, w, n, k, x, int8), f"int8 {int8}")
+    finally:
+        h.release()
+
+
 @pytest.mark.parametrize("fmt", GRID_FORMATS)
 def test_prefill_rows_and_residual(gctx, fmt):
     """M = 40 (past 16 rows: the MFMA prefill GEMM) and the residual
@@ -213,7 +236,9 @@ def test_prefill_gemm_tiles_and_ragged_edges(gctx, fmt, variant):
                 for int8 in (True, False):
                     assert_row_tolerance(c.matmul(h, x, int8=int8), dense(fmt, w, n, k, x, int8),
                                          f"m {m} n {n} k {k} int8 {int8}")
-                a16 = dev(x.astype(np.float16))
+                xd = dev(x)
+                a16 = torch.empty(m * k + 2 * m, dtype=torch.float16, device="cuda")  # values, row factors
+                c.prepare_activations_f16_dev(xd.data_ptr(), m, k, a16.data_ptr(), int8=False)
                 y = torch.empty((m, n), dtype=torch.float32, device="cuda")
                 c.matmul_f16_dev(h, a16.data_ptr(), m, k, y.data_ptr())
                 torch.cuda.synchronize()
@@ -241,7 +266,7 @@ def test_prefill_falls_back_for_wide_grid_bytes(gctx):
         h = gctx.upload(IQ2_XXS, n, k, w)
         try:
             assert_row_tolerance(gctx.matmul(h, x), dense(IQ2_XXS, w, n, k, x, True), "prefill, wide bytes")
-            a16 = torch.zeros((m, k), dtype=torch.float16, device="cuda")
+            a16 = torch.zeros(m * k + 2 * m, dtype=torch.float16, device="cuda")
             y = torch.empty((m, n), dtype=torch.float32, device="cuda")
             with pytest.raises(mg.Declined):
                 gctx.matmul_f16_dev(h, a16.data_ptr(), m, k, y.data_ptr())

@@ -11,7 +11,7 @@ import pytest
 
 import magnetar_gpu as mg
 import oracle
-from helpers import (IQ4_XS, Q4_K, Q6_K, activations, assert_close_reference, assert_row_tolerance, packed,
+from helpers import (IQ4_XS, Q2_K, Q4_K, Q6_K, Q8_0, activations, assert_close_reference, assert_row_tolerance, packed,
                      row_tolerance_violation)
 from magnetar_gpu import workloads
 
@@ -318,6 +318,127 @@ def test_int8_power_of_two_scaling_is_exact(ctx, m):
         h.release()
 
 
+@pytest.mark.parametrize("int8", [True, False])
+def test_prefill_power_of_two_scaling_is_exact(ctx, int8):
+    """M = 512 through the f16 MFMA GEMM: y(2^e x) = 2^e y(x) bit for bit in
+    both activation modes, for e far outside f16's range (2^-40 x holds only
+    f16 subnormals and zeros unscaled, 2^30 x only infinities): each row's
+    power-of-two factor absorbs e, so the f16 operand is the same."""
+    name = "q4k_4096x4096_s2"
+    fmt, n, k, seed, _ = workloads.WEIGHTS[name]
+    h = ctx.upload(fmt, n, k, workloads.weight_bytes(name))
+    try:
+        a = workloads.activations(seed, 512, k)
+        y = ctx.matmul(h, a, int8=int8)
+        for e in (-40, 30):
+            y2 = ctx.matmul(h, (a * np.float32(2.0 ** e)).astype(np.float32), int8=int8)
+            np.testing.assert_array_equal(y2, (y.astype(np.float64) * 2.0 ** e).astype(np.float32),
+                                          err_msg=f"e {e}")
+    finally:
+        h.release()
+
+
+@pytest.mark.parametrize("scale", [1e-6, 1e5])
+@pytest.mark.parametrize("int8", [True, False])
+def test_prefill_activations_far_from_unit_scale(ctx, scale, int8):
+    """Activations scaled by 1e-6 (below f16's normal range) and 1e5 (above
+    its 65504) at M = 512: the GEMM rows stay finite and within the bar of
+    the dense oracle, like the decode GEMV's (M = 1 here)."""
+    name = "q4k_4096x4096_s2"
+    fmt, n, k, seed, _ = workloads.WEIGHTS[name]
+    w = workloads.weight_bytes(name)
+    a = (workloads.activations(seed, 512, k) * np.float32(scale)).astype(np.float32)
+    h = ctx.upload(fmt, n, k, w)
+    try:
+        got = ctx.matmul(h, a, int8=int8)
+        one = ctx.matmul(h, a[:1], int8=int8)
+    finally:
+        h.release()
+    rows = np.unique(np.concatenate([[0, 511], np.random.default_rng(7).integers(0, 512, 14)]))
+    exp = expected(fmt, w, n, k, a, int8, rows)
+    assert np.isfinite(got).all()
+    assert_row_tolerance(got[rows], exp, f"scale {scale}")
+    assert_row_tolerance(one, exp[:1], f"scale {scale}, m 1")
+
+
+# block-scale exponent fields and mantissa masks: the smallest f16
+# subnormals (at most 15 x 2^-24), and scales near 65504
+_TINY_SCALES = ((0,), 0x00F)
+_HUGE_SCALES = ((28, 29, 30), 0x3FF)
+
+
+@pytest.mark.parametrize("int8", [True, False])
+def test_prefill_rows_longer_than_the_register_hold(ctx, int8):
+    """K = 16640 (65 super-blocks): the f16 operand's rows are read twice
+    instead of held in registers; both activation modes against the oracle."""
+    m, n, k = 24, 72, 16640
+    w = packed(Q4_K, n, k, 86)
+    a = activations(m, k, 87)
+    h = ctx.upload(Q4_K, n, k, w)
+    try:
+        assert_row_tolerance(ctx.matmul(h, a, int8=int8), expected(Q4_K, w, n, k, a, int8), f"int8 {int8}")
+    finally:
+        h.release()
+
+
+def _rescaled_block_scales(fmt, w, scales, seed):
+    """w with every f16 block scale (d, dmin) given an exponent field drawn
+    from scales[0] and its mantissa masked by scales[1]."""
+    from helpers import BLOCK_BYTES, half_offsets
+
+    exponents, mantissa = scales
+    out = w.copy().reshape(-1, BLOCK_BYTES[fmt])
+    rng = np.random.default_rng(seed)
+    for at in half_offsets(fmt):
+        bits = out[:, at].astype(np.uint16) | (out[:, at + 1].astype(np.uint16) << 8)
+        ex = rng.choice(np.asarray(exponents, np.uint16), size=bits.shape[0])
+        bits = (bits & np.uint16(0x8000 | mantissa)) | (ex << np.uint16(10))
+        out[:, at] = (bits & 0xFF).astype(np.uint8)
+        out[:, at + 1] = (bits >> 8).astype(np.uint8)
+    return out.reshape(w.shape)
+
+
+@pytest.mark.parametrize("fmt", [Q4_K, IQ4_XS, Q6_K, Q8_0, Q2_K])
+@pytest.mark.parametrize("scales", [_TINY_SCALES, _HUGE_SCALES], ids=["tiny", "huge"])
+def test_prefill_weights_far_from_unit_scale(ctx, fmt, scales):
+    """Weights whose block scales are the smallest f16 subnormals
+    (dequantized values at most about 1e-4) or near 65504 (values up to
+    3e8, far beyond f16): the weight's power-of-two factor keeps the GEMM's
+    f16 operands in range, so the register-B and split-K register-B forms
+    meet the bar of the dense oracle in both activation modes, as the
+    decode GEMV does."""
+    for m, n, k in ((160, 384, 1024), (512, 512, 1024)):
+        w = _rescaled_block_scales(fmt, packed(fmt, n, k, 80 + m), scales, m)
+        a = activations(m, k, 81 + m)
+        h = ctx.upload(fmt, n, k, w)
+        try:
+            for int8 in (True, False):
+                exp = expected(fmt, w, n, k, a, int8)
+                got = ctx.matmul(h, a, int8=int8)
+                assert np.isfinite(got).all(), f"m {m} int8 {int8}"
+                assert_row_tolerance(got, exp, f"m {m} n {n} int8 {int8}")
+                assert_row_tolerance(ctx.matmul(h, a[:3], int8=int8), exp[:3], f"m 3 n {n} int8 {int8}")
+        finally:
+            h.release()
+
+
+@pytest.mark.parametrize("scales", [_TINY_SCALES, _HUGE_SCALES], ids=["tiny", "huge"])
+def test_k_split_form_weights_far_from_unit_scale(ks_ctx, scales):
+    """The Q4_K K-split GEMM on weights with subnormal or near-65504 block
+    scales, both activation modes, against the dense oracle."""
+    m, n, k = 200, 300, 768
+    w = _rescaled_block_scales(Q4_K, packed(Q4_K, n, k, 83), scales, 84)
+    a = activations(m, k, 85)
+    h = ks_ctx.upload(Q4_K, n, k, w)
+    try:
+        for int8 in (True, False):
+            got = ks_ctx.matmul(h, a, int8=int8)
+            assert np.isfinite(got).all()
+            assert_row_tolerance(got, expected(Q4_K, w, n, k, a, int8), f"int8 {int8}")
+    finally:
+        h.release()
+
+
 def test_matmul_is_deterministic_and_linear_in_weights_rows(ctx):
     """Repeated calls are bit-identical; each output column depends on its
     stored row only (a permutation of stored rows permutes the outputs)."""
@@ -429,12 +550,13 @@ def test_boundary_errors_and_declines(ctx):
 
 def test_non_finite_activations(ctx):
     """f32 mode: a NaN activation makes its output row NaN (no zero-skip);
-    int8 mode: NaN quantizes to 0, as the reference's `as i8` does."""
+    int8 mode: NaN quantizes to 0, as the reference's `as i8` does. M = 40
+    takes the f16 GEMM, whose row factor ignores the NaN."""
     n, k = 64, 512
     w = packed(Q4_K, n, k, 3)
     h = ctx.upload(Q4_K, n, k, w)
     try:
-        for m in (1, 12):
+        for m in (1, 12, 40):
             a = activations(m, k, 5)
             a[0, 17] = np.nan
             y32 = ctx.matmul(h, a, int8=False)
