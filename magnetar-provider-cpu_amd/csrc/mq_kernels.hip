@@ -1348,6 +1348,10 @@ __device__ inline void row_block(const RawRowBlock& a, const uint8_t* lds, int k
 // 0..31 copy the two blocks' int8 values (16 B each), lanes 32..47 their
 // runs' scales (and sums), through buffer loads predicated by offset (no
 // branch for a merge to wait on).
+__device__ inline float4 u4_as_f4(uint4 v) {
+  return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+}
+
 template <int TYPE, int M, bool FUSED, bool TWO = true>
 struct WaveStage {
   float4 xa[M], xb[M];
@@ -1358,12 +1362,34 @@ struct WaveStage {
   __device__ void load(const float* __restrict__ xf, const int8_t* __restrict__ xv, const float* __restrict__ xs,
                        const int32_t* __restrict__ xsum, uint64_t K, int bA, int bB, int b1, int lane) {
     if constexpr (FUSED) {
+      // buffer loads predicated by offset (blocks past b1 read zeros): no
+      // branch, so none of the weight loads that follow waits behind them
+      const __amdgpu_buffer_rsrc_t rsx = buffer_rsrc(xf, static_cast<uint32_t>(M * K * 4));
 #pragma unroll
       for (int m = 0; m < M; ++m) {
-        const float4* xr = reinterpret_cast<const float4*>(xf + m * K);
-        xa[m] = bA < b1 ? xr[64 * static_cast<uint64_t>(bA) + lane] : make_float4(0.f, 0.f, 0.f, 0.f);
-        if (TWO) xb[m] = bB < b1 ? xr[64 * static_cast<uint64_t>(bB) + lane] : make_float4(0.f, 0.f, 0.f, 0.f);
+        const uint32_t row = static_cast<uint32_t>(m * K * 4) + 16 * static_cast<uint32_t>(lane);
+        xa[m] = u4_as_f4(buffer_ld16(rsx, bA < b1 ? row + 1024 * static_cast<uint32_t>(bA) : kBufferNone));
+        if (TWO) xb[m] = u4_as_f4(buffer_ld16(rsx, bB < b1 ? row + 1024 * static_cast<uint32_t>(bB) : kBufferNone));
       }
+    } else if constexpr (!TWO) {
+      // one block: lane group g = lane / 16 copies the values of rows g,
+      // g + 4 (16 B per lane), lane group lane / 8 the run data of row
+      // lane / 8, so no lane holds more than two rows' worth
+      const uint32_t runs = static_cast<uint32_t>(K / 32);
+      const __amdgpu_buffer_rsrc_t rsv = buffer_rsrc(xv, static_cast<uint32_t>(M * K));
+      const __amdgpu_buffer_rsrc_t rss = buffer_rsrc(xs, static_cast<uint32_t>(M * runs * 4));
+      const __amdgpu_buffer_rsrc_t rsh = buffer_rsrc(xsum, TYPE == kTypeQ4K ? static_cast<uint32_t>(M * runs * 8) : 0u);
+      const bool live = bA < b1;
+#pragma unroll
+      for (int i = 0; i < (M + 3) / 4; ++i) {
+        const int m = (lane >> 4) + 4 * i;
+        const uint32_t c16 = static_cast<uint32_t>(m * K + 256 * bA + 16 * (lane & 15));
+        vv[i] = buffer_ld16(rsv, live && m < M ? c16 : kBufferNone);
+      }
+      const int mr = lane >> 3;
+      const uint32_t src = static_cast<uint32_t>(mr) * runs + 8 * bA + (lane & 7);
+      dd[0] = buffer_ld4(rss, live && mr < M ? 4 * src : kBufferNone);
+      hh[0] = buffer_ld8(rsh, live && mr < M ? 8 * src : kBufferNone);
     } else {
       const uint32_t runs = static_cast<uint32_t>(K / 32);
       const __amdgpu_buffer_rsrc_t rsv = buffer_rsrc(xv, static_cast<uint32_t>(M * K));
@@ -1394,6 +1420,23 @@ struct WaveStage {
           if (bB < b1) FusedStage<TYPE, M, false>::put(qb, m * (kn / 4) + 64 * (bB - b0) + lane, lds, M * kn);
         }
       }
+    } else if constexpr (!TWO) {
+      const bool live = bA < b1;
+      float* rs = reinterpret_cast<float*>(lds + M * kn);
+      // lanes without a row store to a spare 16 bytes past the staging
+      // (unused until the cross-wave sums): a store under a branch would
+      // let the compiler sink its load below the weight loads
+      const int spare = (M * kn + M * kruns * (TYPE == kTypeQ4K ? 8 : 4)) / 16;
+#pragma unroll
+      for (int i = 0; i < (M + 3) / 4; ++i) {
+        const int m = (lane >> 4) + 4 * i;
+        const int at = live && m < M ? m * (kn / 16) + 16 * (bA - b0) + (lane & 15) : spare;
+        reinterpret_cast<uint4*>(lds)[at] = vv[i];
+      }
+      const int mr = lane >> 3;
+      if (live && mr < M)
+        QuantizedStage<TYPE, M>::put_run(rs, mr * kruns + 8 * (bA - b0) + (lane & 7), __uint_as_float(dd[0]),
+                                         static_cast<int>(hh[0].x + hh[0].y), static_cast<int>(hh[0].y));
     } else {
       const bool is_val = lane < 32, is_run = lane >= 32 && lane < 48;
       const int blk = is_val ? (lane < 16 ? bA : bB) : (lane < 40 ? bA : bB);
@@ -1497,7 +1540,7 @@ __global__ __launch_bounds__(512) void gemv_lds_int8_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Decode GEMV with one super-block per wave (Q4_K, IQ4_XS; m <= 4): the
+// Decode GEMV with one super-block per wave (Q4_K, IQ4_XS; m <= 8): the
 // LDS form's work-group of 64 stored rows with as many waves as the row has
 // super-blocks (up to 16, 1024 threads), wave s taking block s of every
 // row. Each wave stages its own block's activations (wave-local, no
@@ -1514,7 +1557,7 @@ __global__ __launch_bounds__(1024) void gemv_wave_int8_kernel(
     const uint8_t* __restrict__ w, int nb, uint64_t rows, const int8_t* __restrict__ xv,
     const float* __restrict__ xs, const int32_t* __restrict__ xsum, const float* __restrict__ xf,
     float* __restrict__ y, const float* __restrict__ addend, uint64_t addend_stride, Fusion fu) {
-  static_assert(M <= 4, "wave-local staging holds at most 4 activation rows");
+  static_assert(M <= 8, "wave-local staging holds at most 8 activation rows");
   constexpr bool PIPE = M == 1;
   constexpr int kTile = TYPE == kTypeQ4K ? kQ4kTileBytes : kIq4xsTileBytes;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -1537,8 +1580,14 @@ __global__ __launch_bounds__(1024) void gemv_wave_int8_kernel(
   // the weight block, then the staging
   WaveStage<TYPE, M, FUSED, false> ws;
   ws.load(xf, xv, xs, xsum, K, s, nb, nb, lane);
+  __builtin_amdgcn_sched_barrier(0);
   RawRowBlock A;
   load_row_block<TYPE>(A, rsrc, off, r);
+  // the weight loads issue before any use of the activations: left free,
+  // the scheduler hoists the quantization's first operations above them,
+  // and the wait for the activation load then holds the weight loads back
+  // by a memory round trip
+  __builtin_amdgcn_sched_barrier(0);
   ws.put(lds, kn, kruns, 0, s, nb, nb, lane);
   if (PIPE) read_chunk<TYPE, M>(next, lds, kn, kruns, s, 0);
   row_block<TYPE, M, PIPE>(A, lds, kn, kruns, s, nb, false, next, acc, mins);
@@ -4253,7 +4302,7 @@ void launch_gemv_narrow(int type, const uint8_t* tiled, uint64_t rows, uint64_t 
 // forces the waves per work-group. Q4_K 14336 x 4096 m = 1 fused: 8.4 ->
 // 7.6 us (two blocks per wave at 8 waves against one per wave at 16).
 bool wave_form(uint64_t nb, uint64_t m, int splits_hint, const GemvSplitK& sk, size_t& lds, int type) {
-  if (sk.ks != 1 || m > 4 || nb < 2 || nb > 16 || splits_hint > 0 || sk.narrow == 1) return false;
+  if (sk.ks != 1 || m > 8 || nb < 2 || nb > 16 || splits_hint > 0 || sk.narrow == 1) return false;
   lds = gemv_lds_bytes(type, nb, m, static_cast<int>(nb));
   return lds <= 65536;
 }
@@ -4279,7 +4328,7 @@ void launch_gemv_wave(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb
     hipLaunchKernelGGL((gemv_wave_int8_kernel<kTypeQ4K, MM, FUSED, EPI>), grid, block, lds, stream, tiled, inb, \
                        rows, values, scales, sums, x, y, addend, addend_stride, fu);                            \
     break;
-      X(1) X(2) X(3) X(4)
+      X(1) X(2) X(3) X(4) X(5) X(6) X(7) X(8)
 #undef X
       default:
         break;
@@ -4291,7 +4340,7 @@ void launch_gemv_wave(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb
     hipLaunchKernelGGL((gemv_wave_int8_kernel<kTypeIq4Xs, MM, FUSED, EPI>), grid, block, lds, stream, tiled, inb, \
                        rows, values, scales, nullptr, x, y, addend, addend_stride, fu);                           \
     break;
-      X(1) X(2) X(3) X(4)
+      X(1) X(2) X(3) X(4) X(5) X(6) X(7) X(8)
 #undef X
       default:
         break;

@@ -119,9 +119,10 @@ def test_gemv_wave_override_clamps_to_the_launch_bound(fmt, variant, m):
 
 def test_gemv_default_launch_shapes():
     """The defaults the measured shapes take: one super-block per wave for
-    the 14336 x 4096 up projection (224 work-groups of 16 waves, no K split;
-    with a waves override the two-blocks-per-wave LDS form), the 16-row form
-    for the 4096 x 14336 down projection (256 work-groups)."""
+    the 14336 x 4096 up projection at every m <= 8 (224 work-groups of 16
+    waves, no K split; with a waves override the two-blocks-per-wave LDS
+    form), the 16-row form for the 4096 x 14336 down projection (256
+    work-groups)."""
     g = mg.gemv_launch_shape(Q4_K, 14336, 4096, 1)
     assert (g.form, g.grid_x, g.grid_y, g.waves) == (mg.GEMV_FORM_WAVE, 224, 1, 16)
     assert g.lds_bytes <= 65536
@@ -129,8 +130,9 @@ def test_gemv_default_launch_shapes():
     assert (g.form, g.waves) == (mg.GEMV_FORM_WAVE, 16)
     g = mg.gemv_launch_shape(Q4_K, 14336, 4096, 1, waves=8)
     assert (g.form, g.grid_x, g.grid_y, g.waves) == (mg.GEMV_FORM_LDS, 224, 1, 8)
-    g = mg.gemv_launch_shape(Q4_K, 14336, 4096, 8)  # more rows than the wave form stages
-    assert g.form == mg.GEMV_FORM_LDS
+    g = mg.gemv_launch_shape(Q4_K, 14336, 4096, 8)
+    assert (g.form, g.waves) == (mg.GEMV_FORM_WAVE, 16)
+    assert g.lds_bytes <= 65536
     g = mg.gemv_launch_shape(IQ4_XS, 4096, 14336, 1)
     assert (g.form, g.grid_x, g.grid_y, g.waves) == (mg.GEMV_FORM_NARROW, 256, 1, 8)
     with pytest.raises(mg.GpuError):
