@@ -297,15 +297,23 @@ __global__ __launch_bounds__(256) void activations_f16_kernel(const float* __res
   }
 }
 
-// out = max |x| as f32 bits (non-negative floats order as their bits).
+// out = max |x| as f32 bits (non-negative floats order as their bits): one
+// atomic per work-group, float4 reads (n % 4 == 0).
 __global__ __launch_bounds__(256) void absmax_kernel(const float* __restrict__ x, uint64_t n,
                                                      uint32_t* __restrict__ out) {
   float amax = 0.0f;
-  for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += static_cast<uint64_t>(gridDim.x) * 256)
-    amax = fmaxf(amax, fabsf(x[i]));
+  const float4* x4 = reinterpret_cast<const float4*>(x);
+  for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n / 4; i += static_cast<uint64_t>(gridDim.x) * 256) {
+    const float4 v = x4[i];
+    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+  }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
-  if ((threadIdx.x & 63) == 0) atomicMax(out, __float_as_uint(amax));
+  __shared__ float wave_max[4];
+  if ((threadIdx.x & 63) == 0) wave_max[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  if (threadIdx.x == 0)
+    atomicMax(out, __float_as_uint(fmaxf(fmaxf(wave_max[0], wave_max[1]), fmaxf(wave_max[2], wave_max[3]))));
 }
 
 // ---------------------------------------------------------------------------
@@ -835,7 +843,18 @@ __device__ inline void finish_rows(float (&acc)[M], float (&mins)[M], uint64_t r
                                    uint64_t addend_stride, float* red, float* partials, uint32_t* counters, int KS,
                                    const Fusion& fu = Fusion{}) {
   const int lane = threadIdx.x & 63, s = threadIdx.x >> 6, S = blockDim.x >> 6;
-  if (S > 1) {
+  if (M == 1 && KS == 1 && S > 1) {
+    // one activation row: each wave hands over acc - mins, so wave 0 sums
+    // S values per row (in wave order) rather than 2 S
+    __syncthreads();  // every wave is done reading activations
+    red[s * 64 + lane] = acc[0] - mins[0];
+    __syncthreads();
+    if (s != 0) return;
+    float v = red[lane];
+    for (int i = 1; i < S; ++i) v += red[i * 64 + lane];
+    acc[0] = v;
+    mins[0] = 0.0f;
+  } else if (S > 1) {
     __syncthreads();  // every wave is done reading activations
 #pragma unroll
     for (int m = 0; m < M; ++m) {
@@ -843,6 +862,25 @@ __device__ inline void finish_rows(float (&acc)[M], float (&mins)[M], uint64_t r
       red[((s * M + m) * 2 + 1) * 64 + lane] = mins[m];
     }
     __syncthreads();
+    if constexpr (M > 1 && EPI == kEpiPlain) {
+      if (KS == 1 && S >= M) {
+        // one wave per activation row: wave s sums row s's partials in
+        // wave order (the same order and values as below) and stores it
+        if (s >= M) return;
+        float a = red[(s * 2 + 0) * 64 + lane], mn = red[(s * 2 + 1) * 64 + lane];
+        for (int i = 1; i < S; ++i) {
+          a += red[((i * M + s) * 2 + 0) * 64 + lane];
+          mn += red[((i * M + s) * 2 + 1) * 64 + lane];
+        }
+        const uint64_t row = static_cast<uint64_t>(blockIdx.x) * 64 + lane;
+        if (row < rows) {
+          float v = a - mn;
+          if (addend) v = v + addend[s * addend_stride + row];
+          y[s * rows + row] = v;
+        }
+        return;
+      }
+    }
     if (s != 0) return;
 #pragma unroll
     for (int m = 0; m < M; ++m) {
@@ -4210,8 +4248,8 @@ void weight_f16_factors(float amax, float* up, float* down) {
 }
 
 void launch_absmax(const float* x, uint64_t n, uint32_t* out, hipStream_t stream) {
-  uint64_t groups = grid_for(n, 256);
-  if (groups > 2048) groups = 2048;
+  uint64_t groups = grid_for(n / 4, 256);
+  if (groups > 1024) groups = 1024;
   if (groups == 0) return;
   hipLaunchKernelGGL(absmax_kernel, dim3(static_cast<unsigned>(groups)), dim3(256), 0, stream, x, n, out);
 }

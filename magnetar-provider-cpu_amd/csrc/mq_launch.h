@@ -37,7 +37,7 @@ struct F16Range {
 };
 void weight_f16_factors(float amax, float* up, float* down);
 
-// out[0] = max |x[i]| over n floats as f32 bits (NaN ignored); out[0] must
+// out[0] = max |x[i]| over n floats (n % 4 == 0) as f32 bits (NaN ignored); out[0] must
 // hold 0 (or an earlier maximum) before the launch.
 void launch_absmax(const float* x, uint64_t n, uint32_t* out, hipStream_t stream);
 
