@@ -2998,6 +2998,10 @@ __device__ inline uint32_t pack_f16x2(float a, float b) {
   return *reinterpret_cast<uint32_t*>(&h);
 }
 
+// Work-group barrier that waits for this wave's LDS operations only (not
+// for its vector-memory loads in flight, as __syncthreads() would).
+__device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 template <int TYPE>
 __global__ __launch_bounds__(256) void gemm_kernel(const uint8_t* __restrict__ w, int nb, uint64_t rows,
                                                    uint64_t rows_padded, const uint16_t* __restrict__ a16,
@@ -3488,18 +3492,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NF == 2 ? 2
       if constexpr (TYPE == kTypeIq4Xs) load_raw_b_iq4<NF>(r, planes0, wlive, b);
     }
   };
+  // Pipeline: the activations of K-step kb + 2 are loaded into registers
+  // during K-step kb (areg[kb & 1]) and stored to the other LDS buffer at
+  // the end of K-step kb + 1; the next super-block's weights are loaded
+  // during the block's second K-step, after that step's activation load.
+  // So each wait for a load (vector memory returns in issue order) comes
+  // about two K-steps after it was issued, and the barrier between K-steps
+  // waits for LDS only, not for the loads in flight.
   Raw cur, nxt;
+  uint4 areg[2][A_CHUNKS];
+  load_a(4 * bl, areg[0]);
+  if (4 * bl + 1 < ksteps) load_a(4 * bl + 1, areg[1]);
   load_b(nxt, static_cast<uint64_t>(bl));
-  uint4 areg[A_CHUNKS];
-  load_a(4 * bl, areg);
-  store_a(0, areg);  // K-step 4 bl is even: buffer 0
+  store_a(0, areg[0]);  // K-step 4 bl is even: buffer 0
   if (tid < BM) row_fac[tid] = my_fac;
   __syncthreads();
 
-  auto kstep = [&](int kb, const half8 (&bop)[2][NF]) {
+  // ld: the registers of K-step kb's parity (free: stored at the end of
+  // K-step kb - 1), st: those of kb + 1
+  auto kstep = [&](int kb, const half8 (&bop)[2][NF], uint4 (&ld)[A_CHUNKS], uint4 (&st)[A_CHUNKS], int b_next) {
     const int buf = kb & 1;
-    const bool more = kb + 1 < ksteps;
-    if (more) load_a(kb + 1, areg);
+    if (kb + 2 < ksteps) load_a(kb + 2, ld);
+    if (b_next >= 0) load_b(nxt, static_cast<uint64_t>(b_next));
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
 #pragma unroll
@@ -3510,32 +3524,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NF == 2 ? 2
           acc[i][f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bop[r][f], acc[i][f], 0, 0, 0);
       }
     }
-    if (more) store_a(buf ^ 1, areg);
-    __syncthreads();
+    if (kb + 1 < ksteps) store_a(buf ^ 1, st);
+    lds_barrier();
   };
 
   for (int b = bl; b < bh; ++b) {
     cur = nxt;
-    if (b + 1 < bh) load_b(nxt, static_cast<uint64_t>(b + 1));
+    const int b_next = b + 1 < bh ? b + 1 : -1;
     half8 bop[2][NF];
     if constexpr (is_plane_format(TYPE)) {
       dequant_pb<TYPE, NF, 0>(cur, kq, rg.up, bop);
-      kstep(4 * b + 0, bop);
+      kstep(4 * b + 0, bop, areg[0], areg[1], -1);
       dequant_pb<TYPE, NF, 1>(cur, kq, rg.up, bop);
-      kstep(4 * b + 1, bop);
+      kstep(4 * b + 1, bop, areg[1], areg[0], b_next);
       dequant_pb<TYPE, NF, 2>(cur, kq, rg.up, bop);
-      kstep(4 * b + 2, bop);
+      kstep(4 * b + 2, bop, areg[0], areg[1], -1);
       dequant_pb<TYPE, NF, 3>(cur, kq, rg.up, bop);
-      kstep(4 * b + 3, bop);
+      kstep(4 * b + 3, bop, areg[1], areg[0], -1);
     } else {
       dequant_b<TYPE, NF, 0>(cur, kq, rg.up, bop);
-      kstep(4 * b + 0, bop);
+      kstep(4 * b + 0, bop, areg[0], areg[1], -1);
       dequant_b<TYPE, NF, 1>(cur, kq, rg.up, bop);
-      kstep(4 * b + 1, bop);
+      kstep(4 * b + 1, bop, areg[1], areg[0], b_next);
       dequant_b<TYPE, NF, 2>(cur, kq, rg.up, bop);
-      kstep(4 * b + 2, bop);
+      kstep(4 * b + 2, bop, areg[0], areg[1], -1);
       dequant_b<TYPE, NF, 3>(cur, kq, rg.up, bop);
-      kstep(4 * b + 3, bop);
+      kstep(4 * b + 3, bop, areg[1], areg[0], -1);
     }
   }
 
@@ -3687,9 +3701,15 @@ __global__ __launch_bounds__(kKsThreads) void gemm_ks_kernel(const uint8_t* __re
   const float my_fac = tid < kKsBM ? out_factor(rg, m0 + tid, m_rows) : 0.0f;
   const uint64_t n0 = static_cast<uint64_t>(blockIdx.x) * kKsBN + static_cast<uint64_t>(nw) * 64;
   const uint64_t K = static_cast<uint64_t>(nb) * 256;
-  const int nbh = (nb + 1) / 2, sb0 = kw * nbh;
-  const int sb_end = sb0 + nbh < nb ? sb0 + nbh : nb;  // this half's super-blocks [sb0, sb_end)
-  const int ksteps = 4 * nbh;                          // K-steps per half (both halves run as many)
+  // split-K over gridDim.z: super-blocks [zb0, zb1) of the row, the
+  // partials to the split's own [m_rows][rows] slice of y (summed in split
+  // order afterwards); the two K halves divide that range
+  const int zb0 = static_cast<int>(blockIdx.z * static_cast<uint64_t>(nb) / gridDim.z);
+  const int zb1 = static_cast<int>((blockIdx.z + 1) * static_cast<uint64_t>(nb) / gridDim.z);
+  const int nbh = (zb1 - zb0 + 1) / 2, sb0 = zb0 + kw * nbh;
+  const int sb_end = sb0 + nbh < zb1 ? sb0 + nbh : zb1;  // this half's super-blocks [sb0, sb_end)
+  const int ksteps = 4 * nbh;                            // K-steps per half (both halves run as many)
+  y += static_cast<uint64_t>(blockIdx.z) * m_rows * rows;
   uint8_t* const ring = lds + kw * 4 * kKsStage;
   auto swz = [](int row) { return (row >> 1) & 7; };
 
@@ -4981,9 +5001,26 @@ __global__ void gemm_split_reduce_kernel(const float* __restrict__ part, int ks,
 
 }  // namespace
 
-int gemm_default_variant(int type, uint64_t rows, uint64_t m) {
-  // Q4_K: the K-split form once its 128 x 256 tiles cover most CUs.
-  if (type == kTypeQ4K && tiles(rows, m, kKsBN, kKsBM) >= 160) return 5;
+// The K-split form's split count over work-groups: 1 once its 128 x 256
+// tiles cover most CUs, else enough splits for about 224 work-groups, each
+// with at least two super-blocks (one per K half).
+uint64_t ks_form_splits(uint64_t rows, uint64_t m, uint64_t nb) {
+  const uint64_t t = tiles(rows, m, kKsBN, kKsBM);
+  if (t >= 160) return 1;
+  uint64_t z = (224 + t - 1) / t;
+  if (z > nb / 2) z = nb / 2;
+  return z < 1 ? 1 : z;
+}
+
+int gemm_default_variant(int type, uint64_t rows, uint64_t m, uint64_t nb) {
+  // Q4_K: the K-split form while it (split over work-groups if need be)
+  // fills most CUs: measured M = 128 x 14336 x 4096 39.0 us against 44.2
+  // for the split register-B form, M = 512 x 4096 x 4096 41.0 against 45.6;
+  // M = 128 x 4096 x 4096 reaches only 128 work-groups (31.3 us against 27.9)
+  if (type == kTypeQ4K) {
+    const uint64_t t = tiles(rows, m, kKsBN, kKsBM);
+    if (t >= 160 || t * ks_form_splits(rows, m, nb) >= 192) return 5;
+  }
   // Register-B 128 x 128 tiles (two work-groups per CU fit, 2 waves per
   // SIMD); the 128 x 256 tile only once there are work-groups for every CU
   // several times over.
@@ -5000,8 +5037,9 @@ int gemm_splits(int type, uint64_t rows, uint64_t m, uint64_t nb, uint64_t k, in
   if (is_grid_format(type))
     variant = variant == 2 || (variant == 0 && tiles(rows, m, 256, 128) >= 1024) ? 2 : 3;
   else if (variant == 0)
-    variant = gemm_default_variant(type, rows, m);
+    variant = gemm_default_variant(type, rows, m, nb);
   if (variant == 5 && type != kTypeQ4K) variant = 3;
+  if (variant == 5) return static_cast<int>(ks_form_splits(rows, m, nb));
   if (variant != 2 && variant != 3 && variant != 4) return 1;
   const uint64_t t = tiles(rows, m, variant == 3 ? 128 : 256, variant == 4 ? 64 : 128);
   if (t >= 192) return 1;
@@ -5030,9 +5068,20 @@ void launch_gemm(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, uin
                        rows, y, addend, addend_stride);
     return;
   }
+  if (ks > 1 && type == kTypeQ4K && (variant == 5 || (variant == 0 && gemm_default_variant(type, rows, m, nb) == 5))) {
+    // the K-split form over ks K ranges into `part`, then their sum
+    const uint64_t rows_padded = (rows + 7) / 8 * 8;
+    dim3 ks_grid(static_cast<unsigned>((rows + kKsBN - 1) / kKsBN), static_cast<unsigned>((m + kKsBM - 1) / kKsBM),
+                 static_cast<unsigned>(ks));
+    hipLaunchKernelGGL(gemm_ks_kernel, ks_grid, dim3(kKsThreads), 0, stream, tiled, static_cast<int>(nb), rows,
+                       rows_padded, a16, m, part, nullptr, 0, rg);
+    hipLaunchKernelGGL(gemm_split_reduce_kernel, dim3(grid_for(m * rows, 256)), dim3(256), 0, stream, part, ks, m,
+                       rows, y, addend, addend_stride);
+    return;
+  }
   if (ks > 1) {
     // the register-B form over ks K ranges into `part`, then their sum
-    const int v = variant == 0 ? gemm_default_variant(type, rows, m) : (variant == 5 ? 3 : variant);
+    const int v = variant == 0 ? gemm_default_variant(type, rows, m, nb) : (variant == 5 ? 3 : variant);
     if (v == 2)
       launch_gemm_rb<8, 4>(type, tiled, rows, nb, a16, m, part, nullptr, 0, rg, stream, ks);
     else if (v == 4)
@@ -5069,7 +5118,7 @@ void launch_gemm(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, uin
         return;
     }
   }
-  if (variant == 0) variant = gemm_default_variant(type, rows, m);
+  if (variant == 0) variant = gemm_default_variant(type, rows, m, nb);
   if (variant == 5 && type != kTypeQ4K) variant = 3;
   switch (variant) {
     case 5: {

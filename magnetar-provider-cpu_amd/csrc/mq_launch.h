@@ -135,7 +135,7 @@ void launch_gemm(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, uin
                  int variant, hipStream_t stream, F16Range rg, float* part = nullptr);
 // Split-K factor of that GEMM (register-B and grid-format forms; 1: none).
 int gemm_splits(int type, uint64_t rows, uint64_t m, uint64_t nb, uint64_t k, int variant);
-int gemm_default_variant(int type, uint64_t rows, uint64_t m);
+int gemm_default_variant(int type, uint64_t rows, uint64_t m, uint64_t nb);
 
 // IQ2 / IQ3 grid formats (raw checkpoint blocks; mq_device.h). The grid
 // tables (kGridTableBytes, layout in mq_device.h) are copied to this
