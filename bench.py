@@ -9,13 +9,17 @@ device copies (> 256 MB in all) so the MALL cannot serve it. Steps are
 launched from HIP graphs (captured once) so host launch cost does not hide
 the device time.
 
-Also reported: the GEMV kernel alone against the 8 TB/s HBM roofline, the
-other decode shapes, one Llama-3-8B-shaped decoder layer decode step
-(device-resident, weights + KV cache bytes per step), the same GEMV and
-GEMM for Q8_0, Q6_K, Q5_K, Q4_0, IQ4_NL, Q3_K and Q2_K weights, the M=512 prefill
-GEMM (x[512, 4096] . W[14336, 4096]^T) in TFLOP/s against the 2.5 PFLOP/s
-dense f16 MFMA peak, and the reference's CPU path (the oracle's AVX2
-restatement) timed on this host's cores.
+Also reported: the GEMV kernel alone against the 8 TB/s HBM roofline and
+against a streaming-read ceiling measured in the same run (`extra`), the
+GEMV at m = 2, 4, 8 and the IQ4_XS down projection, one Llama-3-8B-shaped
+decoder layer decode step (device-resident, weights + KV cache bytes per
+step, rotated over several layer copies), the same GEMV and GEMM for the
+other formats, the M=512 prefill GEMM (x[512, 4096] . W[14336, 4096]^T) in
+TFLOP/s against the 2.5 PFLOP/s dense f16 MFMA peak with the prefill
+shapes around it, and the reference's CPU path (the oracle's restatement
+of its column kernels) timed on this host's cores: the headline workload
+and legs for the 4096 x 4096 matvec, the M=512 GEMM and the IQ4_XS GEMV
+(`cpu_baseline.legs`).
 """
 
 import argparse
@@ -657,7 +661,7 @@ def emit(args, value, steps, warmup, ms_per_step, n, k, weight_bytes, use_graph,
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": recorded_traffic("gemv_q4k_m1_fused"),
             "traffic_unit": "HBM bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
             "algorithmic_bytes": weight_bytes + 4 * k + 4 * n, "kernel_us": round(kernel_us, 3),
-            "kernel": "gemv_lds_int8_kernel<Q4_K, 1, fused> (64-row form): int8 quantization of x in LDS + Q4_K GEMV, one launch",
+            "kernel": "gemv_wave_int8_kernel<Q4_K, 1, fused> (one super-block per wave, 16 waves per 64 rows): int8 quantization of x in LDS + Q4_K GEMV, one launch",
         },
         "cpu_baseline": cpu,
         "gemm": gemm,

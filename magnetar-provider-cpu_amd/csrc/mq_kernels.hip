@@ -725,6 +725,10 @@ __device__ inline float wave_sum64(float v) {
   return v;
 }
 
+// Work-group barrier that waits for this wave's LDS operations only (not
+// for its vector-memory loads in flight, as __syncthreads() would).
+__device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // Thread t's share of the row's sum of squares: float4 elements t,
 // t + blockDim, ... in that order.
 __device__ inline void add_squares(float& ss, float4 a) {
@@ -742,6 +746,32 @@ __device__ inline float norm_from_squares(float ss, uint64_t K, float eps) {
   __syncthreads();
   float total = 0.0f;
   for (int i = 0; i < static_cast<int>(blockDim.x >> 6); ++i) total += part[i];
+  return 1.0f / sqrtf(total / static_cast<float>(K) + eps);
+}
+
+// norm_from_squares when thread t holds float4 element t of the row and
+// nothing else (K / 4 == blockDim.x, the one-super-block-per-wave GEMV):
+// the same elements, order and value, behind a barrier that waits for LDS
+// only, so the weight loads already in flight are not waited for.
+__device__ inline float wave_norm_scale(float4 v, uint64_t K, float eps) {
+  __shared__ __attribute__((aligned(16))) float part[16];
+  float ss = 0.0f;
+  add_squares(ss, v);
+  ss = wave_sum64(ss);
+  const int S = static_cast<int>(blockDim.x >> 6);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+  if (static_cast<int>(threadIdx.x) < 16 - S) part[S + threadIdx.x] = 0.0f;  // adds nothing below
+  lds_barrier();
+  // the waves' sums in wave order, read four at a time
+  float total = 0.0f;
+  const float4* p4 = reinterpret_cast<const float4*>(part);
+  for (int i = 0; i < (S + 3) / 4; ++i) {
+    const float4 q = p4[i];
+    total += q.x;
+    total += q.y;
+    total += q.z;
+    total += q.w;
+  }
   return 1.0f / sqrtf(total / static_cast<float>(K) + eps);
 }
 
@@ -1447,6 +1477,14 @@ struct WaveStage {
     }
   }
 
+  // one fused activation row, one block, rmsnorm'd first: x * scale * w
+  // (each product rounded, the rmsnorm's order)
+  __device__ void put_normed(uint8_t* lds, int kn, int b0, int bA, int b1, int lane, float nscale, float4 w) const {
+    static_assert(FUSED && M == 1 && !TWO, "the normed staging takes one f32 row, one block per wave");
+    const Quant4 qa = quantize4(FusedStage<TYPE, 1, true>::normed(xa[0], nscale, w));
+    if (bA < b1) FusedStage<TYPE, 1, false>::put(qa, 64 * (bA - b0) + lane, lds, kn);
+  }
+
   __device__ void put(uint8_t* lds, int kn, int kruns, int b0, int bA, int bB, int b1, int lane) const {
     if constexpr (FUSED) {
 #pragma unroll
@@ -1590,12 +1628,16 @@ __global__ __launch_bounds__(512) void gemv_lds_int8_kernel(
 // two-blocks-per-wave form by rounding only. No K split.
 // ---------------------------------------------------------------------------
 
-template <int TYPE, int M, bool FUSED, int EPI = kEpiPlain>
+// (The f32 activations and the rmsnorm weight come right after the weight
+// and its shape, within the kernel arguments preloaded into SGPRs.)
+template <int TYPE, int M, bool FUSED, int EPI = kEpiPlain, bool NORM = false>
 __global__ __launch_bounds__(1024) void gemv_wave_int8_kernel(
-    const uint8_t* __restrict__ w, int nb, uint64_t rows, const int8_t* __restrict__ xv,
-    const float* __restrict__ xs, const int32_t* __restrict__ xsum, const float* __restrict__ xf,
-    float* __restrict__ y, const float* __restrict__ addend, uint64_t addend_stride, Fusion fu) {
+    const uint8_t* __restrict__ w, int nb, uint64_t rows, const float* __restrict__ xf,
+    const float* __restrict__ norm_w, const int8_t* __restrict__ xv, const float* __restrict__ xs,
+    const int32_t* __restrict__ xsum, float* __restrict__ y, const float* __restrict__ addend,
+    uint64_t addend_stride, Fusion fu) {
   static_assert(M <= 8, "wave-local staging holds at most 8 activation rows");
+  static_assert(!NORM || (FUSED && M == 1), "the rmsnorm staging takes one f32 activation row");
   constexpr bool PIPE = M == 1;
   constexpr int kTile = TYPE == kTypeQ4K ? kQ4kTileBytes : kIq4xsTileBytes;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -1618,6 +1660,10 @@ __global__ __launch_bounds__(1024) void gemv_wave_int8_kernel(
   // the weight block, then the staging
   WaveStage<TYPE, M, FUSED, false> ws;
   ws.load(xf, xv, xs, xsum, K, s, nb, nb, lane);
+  float4 nw = make_float4(0.f, 0.f, 0.f, 0.f);  // NORM: the rmsnorm weight at this lane's positions
+  if constexpr (NORM)
+    nw = u4_as_f4(buffer_ld16(buffer_rsrc(norm_w, static_cast<uint32_t>(K * 4)),
+                              1024 * static_cast<uint32_t>(s) + 16 * static_cast<uint32_t>(lane)));
   __builtin_amdgcn_sched_barrier(0);
   RawRowBlock A;
   load_row_block<TYPE>(A, rsrc, off, r);
@@ -1626,7 +1672,16 @@ __global__ __launch_bounds__(1024) void gemv_wave_int8_kernel(
   // and the wait for the activation load then holds the weight loads back
   // by a memory round trip
   __builtin_amdgcn_sched_barrier(0);
-  ws.put(lds, kn, kruns, 0, s, nb, nb, lane);
+  if constexpr (NORM) {
+    // eps, a kernel argument past the preloaded ones, as a scalar load here
+    // (left to the compiler it became a vector load after the barrier,
+    // whose wait then covered every weight load in flight)
+    const uint32_t eps_bits = __builtin_amdgcn_readfirstlane(__float_as_uint(fu.norm_eps));
+    asm volatile("" ::"s"(eps_bits));
+    ws.put_normed(lds, kn, 0, s, nb, lane, wave_norm_scale(ws.xa[0], K, __uint_as_float(eps_bits)), nw);
+  }
+  else
+    ws.put(lds, kn, kruns, 0, s, nb, nb, lane);
   if (PIPE) read_chunk<TYPE, M>(next, lds, kn, kruns, s, 0);
   row_block<TYPE, M, PIPE>(A, lds, kn, kruns, s, nb, false, next, acc, mins);
   finish_rows<M, EPI>(acc, mins, rows, y, addend, addend_stride, reinterpret_cast<float*>(lds), nullptr, nullptr, 1,
@@ -2998,10 +3053,6 @@ __device__ inline uint32_t pack_f16x2(float a, float b) {
   return *reinterpret_cast<uint32_t*>(&h);
 }
 
-// Work-group barrier that waits for this wave's LDS operations only (not
-// for its vector-memory loads in flight, as __syncthreads() would).
-__device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
 template <int TYPE>
 __global__ __launch_bounds__(256) void gemm_kernel(const uint8_t* __restrict__ w, int nb, uint64_t rows,
                                                    uint64_t rows_padded, const uint16_t* __restrict__ a16,
@@ -4365,26 +4416,26 @@ bool wave_form(uint64_t nb, uint64_t m, int splits_hint, const GemvSplitK& sk, s
   return lds <= 65536;
 }
 
-template <bool FUSED, int EPI = kEpiPlain>
+template <bool FUSED, int EPI = kEpiPlain, bool NORM = false>
 void launch_gemv_wave(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb, const int8_t* values,
                       const float* scales, const int32_t* sums, const float* x, uint64_t m, float* y,
                       const float* addend, uint64_t addend_stride, size_t lds, const Fusion& fu, hipStream_t stream) {
   dim3 grid(static_cast<unsigned>((rows + 63) / 64)), block(static_cast<unsigned>(64 * nb));
   const int inb = static_cast<int>(nb);
-  if constexpr (EPI != kEpiPlain) {
-    // the decode-step epilogues take one activation row
+  if constexpr (EPI != kEpiPlain || NORM) {
+    // the decode-step epilogues and the rmsnorm staging take one activation row
     if (type == kTypeQ4K)
-      hipLaunchKernelGGL((gemv_wave_int8_kernel<kTypeQ4K, 1, FUSED, EPI>), grid, block, lds, stream, tiled, inb, rows,
-                         values, scales, sums, x, y, addend, addend_stride, fu);
+      hipLaunchKernelGGL((gemv_wave_int8_kernel<kTypeQ4K, 1, FUSED, EPI, NORM>), grid, block, lds, stream, tiled, inb,
+                         rows, x, fu.norm_w, values, scales, sums, y, addend, addend_stride, fu);
     else
-      hipLaunchKernelGGL((gemv_wave_int8_kernel<kTypeIq4Xs, 1, FUSED, EPI>), grid, block, lds, stream, tiled, inb,
-                         rows, values, scales, nullptr, x, y, addend, addend_stride, fu);
+      hipLaunchKernelGGL((gemv_wave_int8_kernel<kTypeIq4Xs, 1, FUSED, EPI, NORM>), grid, block, lds, stream, tiled,
+                         inb, rows, x, fu.norm_w, values, scales, nullptr, y, addend, addend_stride, fu);
   } else if (type == kTypeQ4K) {
     switch (m) {
 #define X(MM)                                                                                                   \
   case MM:                                                                                                      \
     hipLaunchKernelGGL((gemv_wave_int8_kernel<kTypeQ4K, MM, FUSED, EPI>), grid, block, lds, stream, tiled, inb, \
-                       rows, values, scales, sums, x, y, addend, addend_stride, fu);                            \
+                       rows, x, fu.norm_w, values, scales, sums, y, addend, addend_stride, fu);                 \
     break;
       X(1) X(2) X(3) X(4) X(5) X(6) X(7) X(8)
 #undef X
@@ -4396,7 +4447,7 @@ void launch_gemv_wave(int type, const uint8_t* tiled, uint64_t rows, uint64_t nb
 #define X(MM)                                                                                                     \
   case MM:                                                                                                        \
     hipLaunchKernelGGL((gemv_wave_int8_kernel<kTypeIq4Xs, MM, FUSED, EPI>), grid, block, lds, stream, tiled, inb, \
-                       rows, values, scales, nullptr, x, y, addend, addend_stride, fu);                           \
+                       rows, x, fu.norm_w, values, scales, nullptr, y, addend, addend_stride, fu);                \
     break;
       X(1) X(2) X(3) X(4) X(5) X(6) X(7) X(8)
 #undef X
@@ -4621,17 +4672,20 @@ bool launch_gemv_decode_fused(int type, const uint8_t* tiled, uint64_t rows, uin
     }
   }
   size_t wave_lds = 0;
-  if (!norm && wave_form(nb, 1, 0, sk, wave_lds, type)) {
-    // the same form as the plain fused GEMV of this shape takes
-    if (epilogue == kEpiRope)
-      launch_gemv_wave<true, kEpiRope>(type, tiled, rows, nb, nullptr, nullptr, nullptr, x, 1, y, nullptr, 0,
-                                       wave_lds, fu, stream);
-    else if (epilogue == kEpiSiluPairs)
-      launch_gemv_wave<true, kEpiSiluPairs>(type, tiled, rows, nb, nullptr, nullptr, nullptr, x, 1, y, nullptr, 0,
-                                            wave_lds, fu, stream);
-    else
-      launch_gemv_wave<true>(type, tiled, rows, nb, nullptr, nullptr, nullptr, x, 1, y, nullptr, 0, wave_lds, fu,
-                             stream);
+  if (wave_form(nb, 1, 0, sk, wave_lds, type)) {
+    // the same form as the plain fused GEMV of this shape takes (with the
+    // rmsnorm: each wave's squares of its block, summed over the waves)
+#define MQ_WAVE(E, N)                                                                                       \
+  launch_gemv_wave<true, E, N>(type, tiled, rows, nb, nullptr, nullptr, nullptr, x, 1, y, nullptr, 0, wave_lds, \
+                               fu, stream)
+    if (epilogue == kEpiRope) {
+      if (norm) MQ_WAVE(kEpiRope, true); else MQ_WAVE(kEpiRope, false);
+    } else if (epilogue == kEpiSiluPairs) {
+      if (norm) MQ_WAVE(kEpiSiluPairs, true); else MQ_WAVE(kEpiSiluPairs, false);
+    } else {
+      if (norm) MQ_WAVE(kEpiPlain, true); else MQ_WAVE(kEpiPlain, false);
+    }
+#undef MQ_WAVE
     return true;
   }
   int splits = 0;
