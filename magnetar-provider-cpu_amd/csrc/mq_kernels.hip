@@ -4407,7 +4407,7 @@ void launch_gemv_narrow(int type, const uint8_t* tiled, uint64_t rows, uint64_t 
 }
 
 // The one-block-per-wave form: rows without a K split (enough 64-row
-// blocks to cover the CUs), 2..16 super-blocks, m <= 4, unless a sweep
+// blocks to cover the CUs), 2..16 super-blocks, m <= 8, unless a sweep
 // forces the waves per work-group. Q4_K 14336 x 4096 m = 1 fused: 8.4 ->
 // 7.6 us (two blocks per wave at 8 waves against one per wave at 16).
 bool wave_form(uint64_t nb, uint64_t m, int splits_hint, const GemvSplitK& sk, size_t& lds, int type) {
