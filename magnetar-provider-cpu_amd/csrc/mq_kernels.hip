@@ -3895,29 +3895,35 @@ __global__ __launch_bounds__(kKsThreads) void gemm_ks_kernel(const uint8_t* __re
     MQ_KS_SLICE(C, HB, 3)                                                                      \
     sc_cur = sc_nxt;                                                                           \
   }
-  // two super-blocks per iteration (header buffers alternate); a half with an
-  // odd count runs one super-block of zeros (every load past the half reads 0)
-  for (int bl = 0; bl < nbh; bl += 2) {
+  // One super-block per iteration: the next block's header arrives in hb[1]
+  // during the block (used from its last slice on) and moves to hb[0] at its
+  // end. Bodies of two and four blocks (fewer loop heads, where the compiler
+  // waits for every load in flight) measured slower at 512 x 14336 x 4096
+  // (78.0 and 80.5 us against 72.3 us), and a half of one block no longer
+  // runs a block of zeros.
+  for (int bl = 0; bl < nbh; ++bl) {
     MQ_KS_STEP(0, 0)
     MQ_KS_STEP(1, 0)
     MQ_KS_STEP(2, 0)
     MQ_KS_STEP(3, 0)
-    ++bl;
-    MQ_KS_STEP(0, 1)
-    MQ_KS_STEP(1, 1)
-    MQ_KS_STEP(2, 1)
-    MQ_KS_STEP(3, 1)
-    --bl;
+#pragma unroll
+    for (int f = 0; f < NF; ++f) hb[0][f] = hb[1][f];
   }
 #undef MQ_KS_STEP
 #undef MQ_KS_SLICE
 
-  // K halves summed through LDS: wave (nw, 1) hands its tile to wave (nw, 0).
-  // Every wave's DMAs (including the zero-filled ones past the end) must land
+  // The K halves meet in LDS, and the tile leaves through it: wave (nw, 1)
+  // hands its accumulators to wave (nw, 0) (16-byte LDS writes and reads in
+  // fragment order), which adds them, applies the row factors and writes the
+  // 128 x 64 part row-major into the ring; then all eight waves store whole
+  // rows, 16 bytes per lane (a 1 KB row per wave store). Stores of 4 bytes per
+  // lane from half the waves held the epilogue at about 7 us per tile. Every
+  // wave's DMAs (including the zero-filled ones past the end) must land
   // before the ring is reused.
   __builtin_amdgcn_s_waitcnt(wait_vmcnt(0));
   wg_barrier();
-  float4* red = reinterpret_cast<float4*>(lds + nw * 32768);
+  float4* const red = reinterpret_cast<float4*>(lds + nw * 32768);
+  float* const tile = reinterpret_cast<float*>(lds);  // [kKsBM][kKsBN]
   if (kw == 1) {
 #pragma unroll
     for (int i = 0; i < MF; ++i)
@@ -3928,30 +3934,58 @@ __global__ __launch_bounds__(kKsThreads) void gemm_ks_kernel(const uint8_t* __re
           red[((i * NF + f) * 4 + g) * 64 + lane] =
               make_float4(acc[i][f][4 * g], acc[i][f][4 * g + 1], acc[i][f][4 * g + 2], acc[i][f][4 * g + 3]);
   }
-  wg_barrier();
+  lds_barrier();
   if (kw == 0) {
-    // D layout (32 x 32): lane holds column l32, rows 8 g + 4 kh + e of fragment element 4 g + e
 #pragma unroll
-    for (int i = 0; i < MF; ++i) {
-      float rf[16];
+    for (int i = 0; i < MF; ++i)
 #pragma unroll
-      for (int ge = 0; ge < 16; ++ge) rf[ge] = row_fac[32 * i + 8 * (ge >> 2) + 4 * kh + (ge & 3)];
-#pragma unroll
-      for (int f = 0; f < NF; ++f) {
-        const uint64_t col = n0 + 32 * f + l32;
+      for (int f = 0; f < NF; ++f)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const float4 o = red[((i * NF + f) * 4 + g) * 64 + lane];
-          const float ov[4] = {o.x, o.y, o.z, o.w};
+          acc[i][f][4 * g] += o.x;
+          acc[i][f][4 * g + 1] += o.y;
+          acc[i][f][4 * g + 2] += o.z;
+          acc[i][f][4 * g + 3] += o.w;
+        }
+  }
+  lds_barrier();
+  // D layout (32 x 32): lane holds column l32, rows 8 g + 4 kh + e of fragment element 4 g + e
+  if (kw == 0) {
+    const int tc = 64 * nw + l32;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const uint64_t row = m0 + 32 * i + 8 * g + 4 * kh + e;
-            if (row < m_rows && col < rows) {
-              float v = (acc[i][f][4 * g + e] + ov[e]) * rf[4 * g + e];
-              if (addend) v = v + addend[row * addend_stride + col];
-              y[row * rows + col] = v;
-            }
-          }
+    for (int i = 0; i < MF; ++i)
+#pragma unroll
+      for (int ge = 0; ge < 16; ++ge) {
+        const int r = 32 * i + 8 * (ge >> 2) + 4 * kh + (ge & 3);
+        const float rf = row_fac[r];
+#pragma unroll
+        for (int f = 0; f < NF; ++f) tile[r * kKsBN + tc + 32 * f] = acc[i][f][ge] * rf;
+      }
+  }
+  lds_barrier();
+  const uint64_t c0 = static_cast<uint64_t>(blockIdx.x) * kKsBN + 4 * lane;  // this lane's first column
+  if (rows % 4 == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0 && addend == nullptr &&
+      (blockIdx.x + 1) * static_cast<uint64_t>(kKsBN) <= rows) {
+    // every column of the tile in range, 16-byte aligned rows, no addend
+#pragma unroll 4
+    for (int it = 0; it < kKsBM / 8; ++it) {
+      const int r = 8 * it + wave;
+      if (m0 + r >= m_rows) break;  // uniform
+      const float4 v = *reinterpret_cast<const float4*>(&tile[r * kKsBN + 4 * lane]);
+      *reinterpret_cast<float4*>(y + (m0 + r) * rows + c0) = v;
+    }
+  } else {
+    for (int it = 0; it < kKsBM / 8; ++it) {
+      const int r = 8 * it + wave;
+      const uint64_t row = m0 + r;
+      if (row >= m_rows) break;  // uniform
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        if (c0 + c < rows) {
+          float o = tile[r * kKsBN + 4 * lane + c];
+          if (addend) o = o + addend[row * addend_stride + c0 + c];
+          y[row * rows + c0 + c] = o;
         }
       }
     }
@@ -5068,12 +5102,13 @@ uint64_t ks_form_splits(uint64_t rows, uint64_t m, uint64_t nb) {
 
 int gemm_default_variant(int type, uint64_t rows, uint64_t m, uint64_t nb) {
   // Q4_K: the K-split form while it (split over work-groups if need be)
-  // fills most CUs: measured M = 128 x 14336 x 4096 39.0 us against 44.2
-  // for the split register-B form, M = 512 x 4096 x 4096 41.0 against 45.6;
-  // M = 128 x 4096 x 4096 reaches only 128 work-groups (31.3 us against 27.9)
+  // covers at least half the CUs: M = 128 x 14336 x 4096 39.0 us against
+  // 44.2 for the split register-B form, M = 512 x 4096 x 4096 41.0 against
+  // 45.6; M = 128 x 4096 x 4096 (128 work-groups of two super-blocks each)
+  // 18.6 + 3.9 us (partials, then their sum) against 28.6
   if (type == kTypeQ4K) {
     const uint64_t t = tiles(rows, m, kKsBN, kKsBM);
-    if (t >= 160 || t * ks_form_splits(rows, m, nb) >= 192) return 5;
+    if (t >= 160 || t * ks_form_splits(rows, m, nb) >= 128) return 5;
   }
   // Register-B 128 x 128 tiles (two work-groups per CU fit, 2 waves per
   // SIMD); the 128 x 256 tile only once there are work-groups for every CU
