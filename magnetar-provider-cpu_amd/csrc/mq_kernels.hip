@@ -3742,7 +3742,7 @@ __global__ __launch_bounds__(kKsThreads) void gemm_ks_kernel(const uint8_t* __re
                                                               uint64_t addend_stride, F16Range rg) {
   constexpr int MF = 4, NF = 2, D = kKsDma;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * 4 * kKsStage];  // [kw][stage]
-  __shared__ float row_fac[kKsBM];
+  __shared__ __attribute__((aligned(16))) float row_fac[kKsBM];
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int nw = wave & 3, kw = wave >> 2;
   const int l32 = lane & 31, kh = lane >> 5;
@@ -3859,7 +3859,10 @@ __global__ __launch_bounds__(kKsThreads) void gemm_ks_kernel(const uint8_t* __re
   ks_slice<0>(qb[0], sc_cur, bc);
 
   // Slice SL of K-step j = 4 bl + C: read the next slice's A, dequantize the
-  // next slice's B, 8 MFMAs on the current ones.
+  // next slice's B, 8 MFMAs on the current ones. (Raising the wave priority
+  // around the MFMAs measured slower, 72-78 against 69 us at
+  // 512 x 14336 x 4096, and so did one barrier per two K-steps with the ring
+  // filled two stages at a time, 72-78 us: its extra live registers spill.)
 #define MQ_KS_SLICE(C, HB, SL)                                                                 \
   {                                                                                            \
     if (SL < 3) read_a(C, SL + 1, an); else read_a((C + 1) % 4, 0, an);                        \
@@ -3956,24 +3959,35 @@ __global__ __launch_bounds__(kKsThreads) void gemm_ks_kernel(const uint8_t* __re
 #pragma unroll
     for (int i = 0; i < MF; ++i)
 #pragma unroll
-      for (int ge = 0; ge < 16; ++ge) {
-        const int r = 32 * i + 8 * (ge >> 2) + 4 * kh + (ge & 3);
-        const float rf = row_fac[r];
+      for (int g = 0; g < 4; ++g) {
+        const float4 rf4 = *reinterpret_cast<const float4*>(&row_fac[32 * i + 8 * g + 4 * kh]);
+        const float rf[4] = {rf4.x, rf4.y, rf4.z, rf4.w};
 #pragma unroll
-        for (int f = 0; f < NF; ++f) tile[r * kKsBN + tc + 32 * f] = acc[i][f][ge] * rf;
+        for (int e = 0; e < 4; ++e) {
+          const int r = 32 * i + 8 * g + 4 * kh + e;
+#pragma unroll
+          for (int f = 0; f < NF; ++f) tile[r * kKsBN + tc + 32 * f] = acc[i][f][4 * g + e] * rf[e];
+        }
       }
   }
   lds_barrier();
   const uint64_t c0 = static_cast<uint64_t>(blockIdx.x) * kKsBN + 4 * lane;  // this lane's first column
   if (rows % 4 == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0 && addend == nullptr &&
       (blockIdx.x + 1) * static_cast<uint64_t>(kKsBN) <= rows) {
-    // every column of the tile in range, 16-byte aligned rows, no addend
+    // every column of the tile in range, 16-byte aligned rows, no addend; the
+    // final output (not split partials, which the sum kernel reads next) is
+    // stored nontemporally (about 1-1.5 us less per launch)
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
 #pragma unroll 4
     for (int it = 0; it < kKsBM / 8; ++it) {
       const int r = 8 * it + wave;
       if (m0 + r >= m_rows) break;  // uniform
       const float4 v = *reinterpret_cast<const float4*>(&tile[r * kKsBN + 4 * lane]);
-      *reinterpret_cast<float4*>(y + (m0 + r) * rows + c0) = v;
+      float* const dst = y + (m0 + r) * rows + c0;
+      if (gridDim.z == 1)
+        __builtin_nontemporal_store(f32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<f32x4*>(dst));
+      else
+        *reinterpret_cast<float4*>(dst) = v;
     }
   } else {
     for (int it = 0; it < kKsBM / 8; ++it) {
